@@ -1,0 +1,229 @@
+"""Benchmark: causal attention fwd+bwd on one MI355X (BASELINE.json metric).
+
+A step is one fused forward (wha_attn_fwd) plus one fused backward
+(wha_attn_bwd) over the whole headline batch -- 768-dim config: B=8 sequences,
+H=12 heads, T=1024, head_dim 64, fp32 -- with Q, K, V, dO drawn from the seeded
+generator (seed 42) and already resident in HBM.  Outputs and the backward
+workspace are preallocated, so the timed region holds only kernel launches.
+
+Prints one JSON line: value = tokens/s (B*T per step), plus TFLOP/s on the
+credited FLOPs (12*B*H*D*P, P = T(T+1)/2), a roofline object for the dominant
+kernel (algorithmic FLOPs per launch / its average HIP-event duration), and the
+CPU baseline (the reference-order f32 oracle, one thread per sequence).
+
+    python bench.py [--steps K] [--warmup W] [--config 768|384|168|4096|decode]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+FP32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense fp32 matrix peak
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
+
+CONFIGS = {
+    "168": dict(name="168-dim research config", B=4, H=4, T=256, D=42),
+    "384": dict(name="384-dim grammar config", B=16, H=8, T=512, D=48),
+    "768": dict(name="768-dim production config", B=8, H=12, T=1024, D=64),
+    "4096": dict(name="4096-dim preset", B=4, H=32, T=2048, D=128),
+    "decode": dict(name="768-dim decode (serve tier)", B=64, H=12, T=8192, D=64),
+}
+
+METRIC = "causal attn fwd+bwd tokens/s & TFLOP/s (% fp32 MFMA peak), 768-dim seq1024"
+
+
+def credited_flops(B, H, T, D):
+    P = T * (T + 1) // 2
+    return {"attn_fwd": 4 * B * H * D * P,            # Q K^T and P V
+            "attn_bwd_dkv": 6 * B * H * D * P,        # dP = dO V^T, dV = P^T dO, dK = dS^T Q
+            "attn_bwd_dq": 2 * B * H * D * P,         # dQ = dS K
+            "attn_bwd_delta": 0,
+            "total": 12 * B * H * D * P}
+
+
+def cpu_baseline(cfg, seed=42, max_threads=None):
+    """Reference-order f32 oracle (test infrastructure, the CPU baseline only):
+    forward core + backward from att, one thread per sequence as the reference's
+    training loop runs one thread per batch element."""
+    import numpy as np
+    import oracle
+    B, H, T, D = cfg["B"], cfg["H"], cfg["T"], cfg["D"]
+    ncpu = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    nthreads = min(B, ncpu, max_threads or 16)
+    nseq = nthreads  # one sequence per thread: a bounded sample of the same workload
+    q, k, v, do = oracle.synth_inputs(nseq, H, T, D, seed=seed)
+    qs, ks, vs, dos = (oracle.bhtd_to_seq(a) for a in (q, k, v, do))
+    t0 = time.perf_counter()
+    oracle.batch_fwd_bwd_f32_threaded(qs, ks, vs, dos, H, nthreads=nthreads)
+    dt = time.perf_counter() - t0
+    flops = credited_flops(nseq, H, T, D)["total"]
+    return {"value": nseq * T / dt, "unit": "tokens/s", "cores": nthreads, "kind": "port",
+            "sample": f"{nseq} of the {B} sequences ({nseq}x{T} tokens, {H} heads, D={D}), fwd+bwd, "
+                      f"one thread per sequence; host has {ncpu} cores",
+            "seconds": dt, "tflops": flops / dt / 1e12}
+
+
+def run_attention(args, cfg, pkg, torch):
+    B, H, T, D = cfg["B"], cfg["H"], cfg["T"], cfg["D"]
+    dev = torch.device("cuda:0")
+    q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=42)
+    tq, tk, tv, tdo = (torch.from_numpy(a).to(dev) for a in (q, k, v, do))
+    o = torch.empty_like(tq)
+    lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
+    dq, dk, dv = (torch.empty_like(tq) for _ in range(3))
+    ws = torch.empty(pkg.attn_bwd_workspace_bytes(pkg.layout_of(tq)) // 4, dtype=torch.float32, device=dev)
+
+    def step():
+        pkg.attn_fwd(tq, tk, tv, out=o, lse=lse)
+        pkg.attn_bwd(tq, tk, tv, o, tdo, lse, workspace=ws, dq=dq, dk=dk, dv=dv)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # timed region: wall clock and HIP events on the launch stream around each kernel
+    pkg.timing_reset()
+    pkg.timing_enable(True)
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    pkg.timing_enable(False)
+    kern = {}
+    for name in ("attn_fwd", "attn_bwd_delta", "attn_bwd_dq", "attn_bwd_dkv"):
+        ms, n = pkg.timing_read(name)
+        kern[name] = {"avg_ms": ms / max(n, 1), "launches": n}
+    pkg.timing_reset()
+
+    # a second region without the per-kernel events, for the headline number
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall_plain = time.perf_counter() - t0
+
+    ms_per_step = wall_plain / args.steps * 1e3
+    flops = credited_flops(B, H, T, D)
+    tokens = B * T
+    dom = max(("attn_fwd", "attn_bwd_dq", "attn_bwd_dkv"), key=lambda n: kern[n]["avg_ms"])
+    achieved = flops[dom] / (kern[dom]["avg_ms"] * 1e-3) / 1e12
+    traffic = load_traffic(dom, cfg)
+    fwd_ms = kern["attn_fwd"]["avg_ms"]
+    bwd_ms = kern["attn_bwd_delta"]["avg_ms"] + kern["attn_bwd_dq"]["avg_ms"] + kern["attn_bwd_dkv"]["avg_ms"]
+    res = {
+        "metric": METRIC,
+        "value": tokens / (ms_per_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded xorshift64 + Box-Muller, seed 42)",
+        "config": {"workload": cfg["name"], "batch": B, "heads": H, "seq_len": T, "head_dim": D,
+                   "layout": "[B,H,T,D] contiguous", "causal": True, "parallelism": "none (1 GPU)"},
+        "tflops": flops["total"] / (ms_per_step * 1e-3) / 1e12,
+        "pct_fp32_mfma_peak": 100.0 * flops["total"] / (ms_per_step * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
+        "kernel_ms": {n: round(kern[n]["avg_ms"], 5) for n in kern},
+        "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "ms_per_step_with_events": wall / args.steps * 1e3,
+        "roofline": {"kernel": dom, "bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS, "traffic": traffic,
+                     "algorithmic_flops_per_launch": flops[dom],
+                     "avg_launch_ms": kern[dom]["avg_ms"]},
+    }
+    return res
+
+
+def run_decode(args, cfg, pkg, torch):
+    B, H, T, D = cfg["B"], cfg["H"], cfg["T"], cfg["D"]
+    dev = torch.device("cuda:0")
+    import numpy as np
+    g = pkg.SynthStream(42)
+    sd = 1.0 / np.sqrt(D)
+    q = torch.from_numpy(g.normal(B * H * D, sd).reshape(B, H, D)).to(dev)
+    kc = torch.from_numpy(g.normal(B * H * T * D, sd).reshape(B, H, T, D)).to(dev)
+    vc = torch.from_numpy(g.normal(B * H * T * D, sd).reshape(B, H, T, D)).to(dev)
+    for _ in range(args.warmup):
+        pkg.decode_fwd(q, kc, vc)
+    torch.cuda.synchronize()
+    pkg.timing_reset()
+    pkg.timing_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        pkg.decode_fwd(q, kc, vc)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    pkg.timing_enable(False)
+    ms_split, n = pkg.timing_read("decode_split")
+    ms_merge, _ = pkg.timing_read("decode_merge")
+    bytes_kv = 2 * B * H * T * D * 4
+    achieved = bytes_kv / (ms_split / n * 1e-3) / 1e9
+    ms = wall / args.steps * 1e3
+    return {"metric": "decode HBM GB/s (K+V bytes / time), 768-dim decode Tkv 8192", "value": bytes_kv / (ms * 1e-3) / 1e9,
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic", "config": {"workload": cfg["name"], "batch": B, "heads": H, "kv_len": T,
+                                            "head_dim": D},
+            "kernel_ms": {"decode_split": ms_split / n, "decode_merge": ms_merge / n},
+            "roofline": {"kernel": "decode_split", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic("decode_split", cfg)}}
+
+
+def load_traffic(kernel, cfg):
+    """HBM bytes per launch of `kernel` on this workload, from the rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE summary committed under profiles/ (null if absent)."""
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        table = json.loads(p.read_text())
+        return table.get(f"{kernel}@{cfg['B']}x{cfg['H']}x{cfg['T']}x{cfg['D']}")
+    except (ValueError, OSError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="768", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU; the (b,h) units shard across GPUs with no "
+              "exchange, so run one process per GPU on its share of the batch. --gpus must be 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    cfg = CONFIGS[args.config]
+    if args.config == "decode":
+        res = run_decode(args, cfg, pkg, torch)
+    else:
+        res = run_attention(args, cfg, pkg, torch)
+    if not args.no_cpu_baseline and args.config != "decode":
+        res["cpu_baseline"] = cpu_baseline(cfg)
+    elif args.config == "decode":
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

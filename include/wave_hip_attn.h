@@ -1,0 +1,160 @@
+/* wave_hip_attn.h -- C ABI of the MI355X (gfx950) causal attention tier.
+ *
+ * This is the drop-in boundary for wave-engine's ComputeBackend attention
+ * methods (reference: src/common/compute.rs:8-174).  Everything is plain C:
+ * raw pointers, sizes and a `void*` HIP stream; no Rust, torch or HIP types
+ * appear in a signature, so a Rust `extern "C"` block (or ctypes) binds it
+ * directly.
+ *
+ * Conventions
+ *   - Every function returns 0 (WHA_OK) or a negative WHA_ERR_* code; the
+ *     message for the calling thread's last failure is wha_last_error().
+ *     The reference's methods are infallible and panic on failure
+ *     (e.g. src/wgpu_tier/pipelines.rs:138); a Rust shim turns a non-zero
+ *     return into panic!(wha_last_error()).
+ *   - Device entry points take device pointers, enqueue on `stream`
+ *     (NULL = the null stream) and return without synchronising.
+ *   - Host entry points take host pointers in the reference's per-sequence
+ *     layout and return after the results are in host memory.
+ *   - All tensors are fp32.  Arithmetic is fp32 throughout (MFMA
+ *     v_mfma_f32_16x16x4_f32 for the contractions).
+ *   - Entry points are re-entrant and may be called from several host
+ *     threads at once (the reference calls the backend from one thread per
+ *     batch element, src/cpu/train_loop.rs:320-365).
+ */
+#ifndef WAVE_HIP_ATTN_H
+#define WAVE_HIP_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WHA_OK 0
+#define WHA_ERR_INVALID (-1)     /* bad shape, stride, pointer or scale      */
+#define WHA_ERR_UNSUPPORTED (-2) /* head_dim > 128 or similar limits         */
+#define WHA_ERR_HIP (-3)         /* a HIP runtime call failed                */
+#define WHA_ERR_WORKSPACE (-4)   /* caller workspace too small               */
+#define WHA_ERR_NOMEM (-5)       /* device or host allocation failed         */
+
+/* Strided view of B*H independent [T][D] matrices: element (b,h,t,d) of a
+ * tensor with base pointer p is p[b*stride_b + h*stride_h + t*stride_t + d]
+ * (unit stride on d).  One layout describes q, k, v, o, do, dq, dk and dv.
+ *   device layout [B,H,T,D] contiguous: stride_b=H*T*D, stride_h=T*D, stride_t=D
+ *   reference per-sequence layout [T][H*D] (src/common/compute.rs:370-374,
+ *   :384-386) batched as [B][T][H*D]: stride_b=T*H*D, stride_h=D, stride_t=H*D
+ * lse and the backward workspace are always [B][H][T] contiguous. */
+typedef struct wha_layout {
+  int32_t B, H, T, D;
+  int64_t stride_b, stride_h, stride_t;
+} wha_layout;
+
+/* Thread-local message of this thread's last failed call ("" if none). */
+const char* wha_last_error(void);
+
+/* Library version string. */
+const char* wha_version(void);
+
+/* ---------------------------------------------------------------- device API */
+
+/* Fused causal forward: o = softmax(q k^T * scale, causal) v, per (b,h), and
+ * lse[b][h][t] = log(sum_{j<=t} exp(q_t.k_j*scale)) (natural log).  The T x T
+ * score matrix is never materialised.  lse may be NULL when no backward will
+ * follow.  Replaces the core of attention_cpu (src/common/compute.rs:377-409)
+ * and the host loops of GpuBackend::attention (src/wgpu_tier/dispatch.rs:106-136).
+ * scale is normally 1/sqrt(D) (src/common/compute.rs:362). */
+int wha_attn_fwd(const float* q, const float* k, const float* v, float* o,
+                 float* lse, const wha_layout* layout, float scale,
+                 void* stream);
+
+/* Bytes of device workspace wha_attn_bwd needs for this layout. */
+size_t wha_attn_bwd_workspace_size(const wha_layout* layout);
+
+/* Fused causal backward from the forward's o and lse: recomputes P on chip and
+ * writes dq, dk, dv (overwritten, not accumulated).  workspace may be NULL, in
+ * which case the library uses a cached device buffer of its own, one per
+ * (host thread, device, stream), grown on demand; calls that share a thread
+ * and a stream are ordered by the stream, so they never race on it.  Valid when the att the
+ * caller would have passed is causal softmax(q k^T * scale), which is the only
+ * way the reference produces it.  Replaces attn_backward_scores +
+ * attn_backward_dkv (shaders/attn_backward_scores.wgsl:27-111,
+ * shaders/attn_backward_dkv.wgsl:22-63) as driven by
+ * src/wgpu_tier/dispatch_backward.rs:328-436, and the math of
+ * attention_backward_single (src/cpu/backward.rs:313-363). */
+int wha_attn_bwd(const float* q, const float* k, const float* v,
+                 const float* o, const float* d_o, const float* lse, float* dq,
+                 float* dk, float* dv, void* workspace, size_t workspace_bytes,
+                 const wha_layout* layout, float scale, void* stream);
+
+/* Bytes of device workspace wha_attn_bwd_from_probs needs. */
+size_t wha_attn_bwd_from_probs_workspace_size(const wha_layout* layout);
+
+/* Backward with the reference's exact contract: att [B][H][T][T] (post-softmax
+ * rows, att[b][h][t][j] read only for j <= t) is used as given and never
+ * recomputed, exactly as ComputeBackend::attention_backward
+ * (src/common/compute.rs:163-173, :286-314) and attention_backward_single
+ * (src/cpu/backward.rs:313-363) use it.  d_pre_proj is the gradient flowing
+ * into the pre-c_proj attention output.  Bandwidth-bound on att. */
+int wha_attn_bwd_from_probs(const float* d_pre_proj, const float* q,
+                            const float* k, const float* v, const float* att,
+                            float* dq, float* dk, float* dv, void* workspace,
+                            size_t workspace_bytes, const wha_layout* layout,
+                            float scale, void* stream);
+
+/* Bytes of device workspace wha_decode_fwd needs (split-K partials). */
+size_t wha_decode_workspace_size(const wha_layout* cache_layout);
+
+/* Single-token decode: for each (b,h), one query q[b][h][:] (q and o are
+ * [B][H][D] contiguous) attends to every one of the T cached keys of
+ * k_cache/v_cache (described by cache_layout, T = cache length).  Equals the
+ * last row of a causal pass with T = cache length.  lse ([B][H]) may be NULL.
+ * The reference has no dot-product decode; the nearest analogue is
+ * kv_cache::forward_one (src/common/kv_cache.rs:241-356). */
+int wha_decode_fwd(const float* q, const float* k_cache, const float* v_cache,
+                   float* o, float* lse, void* workspace, size_t workspace_bytes,
+                   const wha_layout* cache_layout, float scale, void* stream);
+
+/* ---------------------------------------------------------------- host API
+ * One sequence in the reference's layout: q, k, v, o, d_pre_proj, dq, dk, dv
+ * are [T][E] row-major host arrays (E = n_head * head_dim), att is
+ * [n_head][T][T].  scale = 1/sqrt(E/n_head) as the reference computes it.
+ * Synchronous; device buffers are staged through a per-thread cache. */
+
+/* Core of attention_cpu (src/common/compute.rs:377-409): o = causal softmax
+ * attention of q,k,v (the c_attn/c_proj linears around it are not included). */
+int wha_host_attention_core_fwd(const float* q, const float* k, const float* v,
+                                int32_t T, int32_t E, int32_t n_head, float* o);
+
+/* ComputeBackend::attention_backward (src/common/compute.rs:163-173) with
+ * CpuBackend's semantics (:286-314): att used as given. */
+int wha_host_attention_backward(const float* d_pre_proj, const float* q,
+                                const float* k, const float* v,
+                                const float* att, int32_t T, int32_t E,
+                                int32_t n_head, float* dq, float* dk,
+                                float* dv);
+
+/* ---------------------------------------------------------------- inputs
+ * Seeded synthetic inputs (host): continues the xorshift64 stream in *state
+ * (the reference's Rng::next_u64/next_f32, src/common/rng.rs:24-34) with
+ * Box-Muller normals times stddev, and advances *state.  Multi-threaded by
+ * jumping ahead in the stream; output identical to the sequential stream.
+ * nthreads <= 0 picks a default.  Returns 0, or -1 for a zero state. */
+int wha_synth_normal(uint64_t* state, float* out, size_t n, double stddev, int nthreads);
+
+/* ---------------------------------------------------------------- timing
+ * Optional per-kernel timing with HIP events recorded on the launch stream
+ * around every kernel the library enqueues (off by default).  Used by the
+ * benchmark to measure each kernel's average duration live. */
+int wha_timing_enable(int on);
+int wha_timing_reset(void);
+/* Synchronises the recorded events and returns the summed duration (ms) and
+ * launch count of the named kernel ("attn_fwd", "attn_bwd_dq", "attn_bwd_dkv",
+ * "attn_bwd_delta", "decode_split", "decode_merge", ...). */
+int wha_timing_read(const char* kernel, double* total_ms, int64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WAVE_HIP_ATTN_H */

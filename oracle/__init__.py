@@ -1,0 +1,263 @@
+"""CPU oracle for wave-engine's dot-product causal attention.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this package, and only as the
+checker (or the timed CPU baseline) -- never as the thing measured or shipped.
+The product library in ``wave-engine_amd/`` does not depend on it.
+
+The arithmetic lives in ``wave_attn_oracle.c`` (built by ``oracle/Makefile``
+into ``liboracle.so``): a reference-order f32 restatement of
+
+* ``attention_cpu`` core, ``src/common/compute.rs:377-409``
+* ``CpuBackend::attention_backward``, ``src/common/compute.rs:286-314``
+* ``attention_backward_single``, ``src/cpu/backward.rs:313-363``
+* ``Rng::next_u64`` / ``next_f32``, ``src/common/rng.rs:24-34``
+
+plus an f64 twin of the same loops (ground truth).  This module only moves
+numpy arrays in and out of it, converting between the device layout
+``[B, H, T, D]`` and the reference's per-sequence ``[T][H*D]`` layout.
+
+Pins (each in ``tests/``): the reference's softmax-backward and
+value-aggregation known-answer tests (``src/common/math/attn_backward.rs:352-379``),
+closed forms (T=1, Q=0, constant V, equal K rows), invariants (row sums,
+sum of dK over keys, causality, linearity in V), an independent matrix-form
+numpy restatement in f64, and a central finite-difference check of the
+backward in f64.  The generator's xorshift step is pinned by its full-period
+property over GF(2); its Box-Muller layer is this build's own definition and is
+pinned by committed check values only.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "liboracle.so"
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+
+
+def build() -> None:
+    """Compile liboracle.so with its Makefile."""
+    subprocess.run(["make", "-s", "-C", str(_HERE), "liboracle.so"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(_LIB_PATH))
+        u64p = ctypes.POINTER(ctypes.c_uint64)
+        L.wao_xorshift64_next.argtypes = [u64p]
+        L.wao_xorshift64_next.restype = ctypes.c_uint64
+        L.wao_next_f32.argtypes = [u64p]
+        L.wao_next_f32.restype = ctypes.c_float
+        L.wao_fill_normal.argtypes = [u64p, _f32p, ctypes.c_size_t, ctypes.c_double]
+        L.wao_fill_normal.restype = None
+        for sfx, p, real in (("f32", _f32p, ctypes.c_float), ("f64", _f64p, ctypes.c_double)):
+            vp = ctypes.c_void_p
+            f = getattr(L, f"wao_attention_core_fwd_{sfx}")
+            f.argtypes = [p, p, p, ctypes.c_int, ctypes.c_int, ctypes.c_int, p, vp, vp]
+            f.restype = None
+            f = getattr(L, f"wao_attention_backward_{sfx}")
+            f.argtypes = [p, p, p, p, p, ctypes.c_int, ctypes.c_int, ctypes.c_int, p, p, p]
+            f.restype = None
+            f = getattr(L, f"wao_softmax_backward_row_{sfx}")
+            f.argtypes = [p, p, ctypes.c_int, p]
+            f.restype = None
+            f = getattr(L, f"wao_value_backward_row_{sfx}")
+            f.argtypes = [p, p, p, ctypes.c_long, p, ctypes.c_int, ctypes.c_int, p]
+            f.restype = None
+            f = getattr(L, f"wao_decode_{sfx}")
+            f.argtypes = [p, p, p, ctypes.c_int, ctypes.c_int, ctypes.c_int, p, vp]
+            f.restype = None
+        L.wao_batch_fwd_bwd_f32.argtypes = [ctypes.c_int] * 4 + [_f32p] * 3 + [ctypes.c_void_p] + \
+            [_f32p] + [ctypes.c_void_p] * 3 + [ctypes.c_int]
+        L.wao_batch_fwd_bwd_f32.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _dt(precision: str):
+    if precision == "f32":
+        return np.float32
+    if precision == "f64":
+        return np.float64
+    raise ValueError(precision)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# ---------------------------------------------------------------- generator
+
+class Xorshift64:
+    """Rng (src/common/rng.rs:5-45) state, advanced by the C restatement."""
+
+    def __init__(self, seed: int = 42):
+        if seed == 0:
+            raise ValueError("xorshift64 seed must be non-zero")
+        self.state = ctypes.c_uint64(seed)
+
+    def next_u64(self) -> int:
+        return int(lib().wao_xorshift64_next(ctypes.byref(self.state)))
+
+    def next_f32(self) -> float:
+        return float(lib().wao_next_f32(ctypes.byref(self.state)))
+
+    def normal(self, n: int, stddev: float = 1.0) -> np.ndarray:
+        out = np.empty(n, dtype=np.float32)
+        lib().wao_fill_normal(ctypes.byref(self.state), out, n, float(stddev))
+        return out
+
+
+def synth_inputs(B: int, H: int, T: int, D: int, seed: int = 42, with_do: bool = True):
+    """BASELINE inputs: Q, K, V ~ N(0,1)/sqrt(D), then dO ~ N(0,1), drawn in that
+    order from one xorshift64 stream, each in [B][H][T][D] row-major order."""
+    rng = Xorshift64(seed)
+    n = B * H * T * D
+    sd = 1.0 / np.sqrt(float(D))
+    q = rng.normal(n, sd).reshape(B, H, T, D)
+    k = rng.normal(n, sd).reshape(B, H, T, D)
+    v = rng.normal(n, sd).reshape(B, H, T, D)
+    if not with_do:
+        return q, k, v
+    do = rng.normal(n, 1.0).reshape(B, H, T, D)
+    return q, k, v, do
+
+
+# ---------------------------------------------------------------- layouts
+
+def bhtd_to_seq(x: np.ndarray) -> np.ndarray:
+    """[B,H,T,D] -> [B,T,H*D] (reference per-sequence layout)."""
+    B, H, T, D = x.shape
+    return np.ascontiguousarray(x.transpose(0, 2, 1, 3).reshape(B, T, H * D))
+
+
+def seq_to_bhtd(x: np.ndarray, H: int) -> np.ndarray:
+    B, T, E = x.shape
+    return np.ascontiguousarray(x.reshape(B, T, H, E // H).transpose(0, 2, 1, 3))
+
+
+# ---------------------------------------------------------------- per sequence
+
+def core_fwd(q, k, v, n_head: int, precision: str = "f32", want_att=False, want_lse=False):
+    """attention_cpu core on one sequence. q,k,v: [T][E]. Returns out (and att
+    [H][T][T], lse [H][T] when asked)."""
+    dt = _dt(precision)
+    q, k, v = _c(q, dt), _c(k, dt), _c(v, dt)
+    T, E = q.shape
+    out = np.empty((T, E), dtype=dt)
+    att = np.empty((n_head, T, T), dtype=dt) if want_att else None
+    lse = np.empty((n_head, T), dtype=dt) if want_lse else None
+    getattr(lib(), f"wao_attention_core_fwd_{precision}")(
+        q, k, v, T, E, n_head, out,
+        att.ctypes.data if att is not None else None,
+        lse.ctypes.data if lse is not None else None)
+    res = [out]
+    if want_att:
+        res.append(att)
+    if want_lse:
+        res.append(lse)
+    return res[0] if len(res) == 1 else tuple(res)
+
+
+def attention_backward(d_pre_proj, q, k, v, att, n_head: int, precision: str = "f32"):
+    """CpuBackend::attention_backward on one sequence. att: [H][T][T]."""
+    dt = _dt(precision)
+    d_pre_proj, q, k, v, att = (_c(a, dt) for a in (d_pre_proj, q, k, v, att))
+    T, E = q.shape
+    dq, dk, dv = (np.empty((T, E), dtype=dt) for _ in range(3))
+    getattr(lib(), f"wao_attention_backward_{precision}")(d_pre_proj, q, k, v, att, T, E, n_head, dq, dk, dv)
+    return dq, dk, dv
+
+
+def softmax_backward_row(att, d_att, precision: str = "f32"):
+    dt = _dt(precision)
+    att, d_att = _c(att, dt), _c(d_att, dt)
+    out = np.empty_like(att)
+    getattr(lib(), f"wao_softmax_backward_row_{precision}")(att, d_att, att.shape[0], out)
+    return out
+
+
+def value_backward_row(d_out, v, dv, att, precision: str = "f32"):
+    """Value-aggregation step for one head and position: returns d_att (length
+    n = len(att)) and accumulates att[ki]*d_out into dv[ki] in place."""
+    dt = _dt(precision)
+    d_out, v, att = _c(d_out, dt), _c(v, dt), _c(att, dt)
+    if dv.dtype != dt or not dv.flags.c_contiguous:
+        raise ValueError("dv must be a C-contiguous array of the working precision")
+    n, D = len(att), d_out.shape[0]
+    d_att = np.empty(n, dtype=dt)
+    getattr(lib(), f"wao_value_backward_row_{precision}")(d_out, v, dv, v.shape[1], att, n, D, d_att)
+    return d_att
+
+
+def decode_one(q, k, v, n_head: int, precision: str = "f32", want_lse=False):
+    """One query [E] against a cache [Tk][E], every key visible."""
+    dt = _dt(precision)
+    q, k, v = _c(q, dt), _c(k, dt), _c(v, dt)
+    Tk, E = k.shape
+    out = np.empty(E, dtype=dt)
+    lse = np.empty(n_head, dtype=dt) if want_lse else None
+    getattr(lib(), f"wao_decode_{precision}")(q, k, v, Tk, E, n_head, out,
+                                              lse.ctypes.data if lse is not None else None)
+    return (out, lse) if want_lse else out
+
+
+# ---------------------------------------------------------------- batched [B,H,T,D]
+
+def fwd_bhtd(q, k, v, precision: str = "f32", want_lse=False):
+    """Forward over a [B,H,T,D] batch, one reference call per sequence.
+    Returns O [B,H,T,D] (and LSE [B,H,T])."""
+    B, H, T, D = q.shape
+    qs, ks, vs = bhtd_to_seq(q), bhtd_to_seq(k), bhtd_to_seq(v)
+    outs, lses = [], []
+    for b in range(B):
+        r = core_fwd(qs[b], ks[b], vs[b], H, precision, want_lse=want_lse)
+        if want_lse:
+            outs.append(r[0])
+            lses.append(r[1])
+        else:
+            outs.append(r)
+    o = seq_to_bhtd(np.stack(outs), H)
+    return (o, np.stack(lses)) if want_lse else o
+
+
+def fwd_bwd_bhtd(q, k, v, do, precision: str = "f32"):
+    """Forward then backward (att from the oracle's own forward) over a
+    [B,H,T,D] batch.  Returns O, dQ, dK, dV in [B,H,T,D] and LSE [B,H,T]."""
+    B, H, T, D = q.shape
+    qs, ks, vs, dos = (bhtd_to_seq(a) for a in (q, k, v, do))
+    O, dQ, dK, dV, L = [], [], [], [], []
+    for b in range(B):
+        o, att, lse = core_fwd(qs[b], ks[b], vs[b], H, precision, want_att=True, want_lse=True)
+        dq, dk, dv = attention_backward(dos[b], qs[b], ks[b], vs[b], att, H, precision)
+        O.append(o); dQ.append(dq); dK.append(dk); dV.append(dv); L.append(lse)
+    cv = lambda xs: seq_to_bhtd(np.stack(xs), H)
+    return cv(O), cv(dQ), cv(dK), cv(dV), np.stack(L)
+
+
+def batch_fwd_bwd_f32_threaded(q_seq, k_seq, v_seq, do_seq, n_head: int, nthreads: int):
+    """Threaded reference-order f32 forward+backward over [B][T][E] sequences
+    (one thread per sequence).  Returns out, dq, dk, dv [B][T][E]."""
+    q_seq, k_seq, v_seq = (_c(a, np.float32) for a in (q_seq, k_seq, v_seq))
+    B, T, E = q_seq.shape
+    out = np.empty_like(q_seq)
+    if do_seq is None:
+        lib().wao_batch_fwd_bwd_f32(B, T, E, n_head, q_seq, k_seq, v_seq, None, out,
+                                    None, None, None, nthreads)
+        return out
+    do_seq = _c(do_seq, np.float32)
+    dq, dk, dv = (np.empty_like(q_seq) for _ in range(3))
+    lib().wao_batch_fwd_bwd_f32(B, T, E, n_head, q_seq, k_seq, v_seq, do_seq.ctypes.data, out,
+                                dq.ctypes.data, dk.ctypes.data, dv.ctypes.data, nthreads)
+    return out, dq, dk, dv

@@ -1,0 +1,119 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function the
+public headers declare, and rejects invalid arguments with the documented
+codes before touching the device."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+
+WHA_ERR_INVALID, WHA_ERR_UNSUPPORTED = -1, -2
+
+
+def declared_functions():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = h.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(wha_\w+)\s*\(", text, flags=re.M):
+            names.add(m.group(1))
+    return names
+
+
+def test_header_declares_expected_entry_points(pkg):
+    names = declared_functions()
+    assert set(pkg.EXPORTED_SYMBOLS) == names
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    L = pkg.lib()
+    for name in declared_functions():
+        assert hasattr(L, name), name
+
+
+def test_version(pkg):
+    assert "gfx950" in pkg.version()
+
+
+def _layout(pkg, B=1, H=2, T=16, D=64):
+    return pkg.layout_bhtd(B, H, T, D)
+
+
+def _call_fwd(pkg, layout, scale=0.125, ptr=1 << 20):
+    p = ctypes.c_void_p(ptr)
+    return pkg.lib().wha_attn_fwd(p, p, p, p, None, ctypes.byref(layout) if layout is not None else None,
+                                  scale, None)
+
+
+def test_invalid_layouts_are_rejected(pkg):
+    L = pkg.lib()
+    assert _call_fwd(pkg, None) == WHA_ERR_INVALID
+    assert b"layout is NULL" in L.wha_last_error()
+    for bad in (dict(B=0), dict(H=-1), dict(T=0), dict(D=0)):
+        assert _call_fwd(pkg, _layout(pkg, **bad)) == WHA_ERR_INVALID
+        assert b"must be positive" in L.wha_last_error()
+    assert _call_fwd(pkg, _layout(pkg, D=129)) == WHA_ERR_UNSUPPORTED
+    assert b"128" in L.wha_last_error()
+    lay = _layout(pkg)
+    lay.stride_t = 32  # < D
+    assert _call_fwd(pkg, lay) == WHA_ERR_INVALID
+    assert b"strides" in L.wha_last_error()
+
+
+def test_invalid_scale_and_null_pointers_are_rejected(pkg):
+    L = pkg.lib()
+    lay = _layout(pkg)
+    for s in (0.0, -1.0, float("inf"), float("nan")):
+        assert _call_fwd(pkg, lay, scale=s) == WHA_ERR_INVALID
+        assert b"scale" in L.wha_last_error()
+    assert _call_fwd(pkg, lay, ptr=0) == WHA_ERR_INVALID
+    assert b"non-NULL" in L.wha_last_error()
+    null = ctypes.c_void_p(0)
+    rc = L.wha_attn_bwd(*([null] * 9), None, 0, ctypes.byref(lay), 0.125, None)
+    assert rc == WHA_ERR_INVALID
+    rc = L.wha_attn_bwd_from_probs(*([null] * 8), None, 0, ctypes.byref(lay), 0.125, None)
+    assert rc == WHA_ERR_INVALID
+    rc = L.wha_decode_fwd(*([null] * 5), None, 0, ctypes.byref(lay), 0.125, None)
+    assert rc == WHA_ERR_INVALID
+
+
+def test_workspace_sizes(pkg):
+    L = pkg.lib()
+    lay = pkg.layout_bhtd(8, 12, 1024, 64)
+    n = L.wha_attn_bwd_workspace_size(ctypes.byref(lay))
+    assert n >= 8 * 12 * 1024 * 4 and n % 256 == 0
+    assert L.wha_attn_bwd_from_probs_workspace_size(ctypes.byref(lay)) >= 8 * 12 * 1024 * 4
+    dec = pkg.layout_bhtd(64, 12, 8192, 64)
+    assert L.wha_decode_workspace_size(ctypes.byref(dec)) > 0
+    bad = pkg.layout_bhtd(0, 1, 1, 1)
+    assert L.wha_attn_bwd_workspace_size(ctypes.byref(bad)) == 0
+
+
+def test_host_entry_points_validate_before_device_use(pkg):
+    L = pkg.lib()
+    f = np.zeros(64, dtype=np.float32)
+    fp = f.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+    assert L.wha_host_attention_core_fwd(fp, fp, fp, 4, 10, 3, fp) == WHA_ERR_INVALID   # 10 % 3 != 0
+    assert b"divisible" in L.wha_last_error()
+    assert L.wha_host_attention_core_fwd(fp, fp, fp, 0, 8, 2, fp) == WHA_ERR_INVALID
+    assert L.wha_host_attention_backward(fp, fp, fp, fp, fp, 4, 8, 0, fp, fp, fp) == WHA_ERR_INVALID
+
+
+def test_backend_mirror_checks_shapes(pkg):
+    be = pkg.HipBackend()
+    q = np.zeros((4, 8), np.float32)
+    with pytest.raises(ValueError):
+        be.attention_backward(q, q, q, q, np.zeros((3, 4, 4), np.float32), 2)  # att heads != n_head
+    with pytest.raises(ValueError):
+        be.attention_core(q[0], q, q, 2)
+    with pytest.raises(RuntimeError):
+        be.attention_core(q, q, q, 3)  # 8 % 3 != 0, rejected by the C ABI as a panic would
+
+
+def test_padded_dims_cover_the_configs():
+    # head_dim of the BASELINE configs: 42, 48, 64, 128 (all <= 128)
+    src = (ROOT / "wave-engine_amd" / "csrc" / "wha_launch.hpp").read_text()
+    assert "D <= 128" in src

@@ -1,0 +1,41 @@
+"""The reference-interface mirrors on the GPU: the C++ HipBackend test program
+(tests/cpp/test_hip_backend.cpp) and the Python HipBackend, both against the
+CPU oracle with the reference's per-sequence [T][n_embd] layout and its
+att-as-given backward contract (src/common/compute.rs:163-173, :286-314)."""
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_parity
+
+pytestmark = pytest.mark.gpu
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def test_cpp_host_mirror_program():
+    exe = ROOT / "tests" / "cpp" / "test_hip_backend"
+    assert exe.exists(), "build it with __graft_entry__.build()"
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=180)
+    print(r.stdout)
+    print(r.stderr)
+    assert r.returncode == 0, r.stdout[-2000:]
+    assert "test result: ok" in r.stdout
+
+
+@pytest.mark.parametrize("T,E,H", [(64, 168, 4), (200, 384, 8), (300, 768, 12), (1, 64, 1)])
+def test_python_host_mirror(pkg, T, E, H):
+    g = oracle.Xorshift64(T + E)
+    D = E // H
+    q, k, v = (g.normal(T * E, 1.0 / np.sqrt(D)).reshape(T, E) for _ in range(3))
+    d = g.normal(T * E, 1.0).reshape(T, E)
+    o_ref, att = oracle.core_fwd(q, k, v, H, "f32", want_att=True)
+    be = pkg.HipBackend()
+    assert_parity("attention_core", be.attention_core(q, k, v, H), o_ref)
+    dq, dk, dv = be.attention_backward(d, q.tolist(), k, v, att, H)  # rows as Vec<Vec<f32>> too
+    rq, rk, rv = oracle.attention_backward(d, q, k, v, att, H, "f32")
+    assert_parity("d_q", dq, rq)
+    assert_parity("d_k", dk, rk)
+    assert_parity("d_v", dv, rv)

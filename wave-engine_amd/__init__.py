@@ -1,0 +1,340 @@
+"""wave-engine_amd: MI355X (gfx950) causal attention tier for wave-engine.
+
+Python host side of the C ABI declared in ``include/wave_hip_attn.h`` and
+implemented by ``libwave_hip_attn.so`` (built in-tree by ``Makefile``).  It binds
+the library with ctypes and hands it device pointers and the current HIP stream
+of torch tensors -- torch is only the allocator and stream provider here; every
+FLOP runs in the hand-written HIP kernels under ``csrc/``.  There is no CPU or
+torch fallback: if the library is missing or the device is not a GPU, calls
+raise.
+
+Two levels mirror the reference interface:
+
+* ``HipBackend`` -- the two attention methods of wave-engine's
+  ``ComputeBackend`` trait (``src/common/compute.rs:42-43``, ``:163-173``) with the
+  reference's per-sequence ``[T][n_embd]`` layout and host arrays, raising
+  ``RuntimeError`` where the reference panics.
+* ``attn_fwd`` / ``attn_bwd`` / ``attn_bwd_from_probs`` / ``decode_fwd`` -- batched
+  device entry points on torch tensors in any strided ``[B,H,T,D]`` view.
+
+The directory name contains a hyphen, so it is loaded by path (see
+``__graft_entry__.load_package``) under the module name ``wave_engine_amd``.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "libwave_hip_attn.so"
+
+# C-ABI symbols declared in include/wave_hip_attn.h
+EXPORTED_SYMBOLS = (
+    "wha_last_error", "wha_version",
+    "wha_attn_fwd", "wha_attn_bwd_workspace_size", "wha_attn_bwd",
+    "wha_attn_bwd_from_probs_workspace_size", "wha_attn_bwd_from_probs",
+    "wha_decode_workspace_size", "wha_decode_fwd",
+    "wha_host_attention_core_fwd", "wha_host_attention_backward",
+    "wha_synth_normal",
+    "wha_timing_enable", "wha_timing_reset", "wha_timing_read",
+)
+
+WHA_OK = 0
+
+
+class WaveLayout(ctypes.Structure):
+    """wha_layout: element (b,h,t,d) at b*stride_b + h*stride_h + t*stride_t + d."""
+    _fields_ = [("B", ctypes.c_int32), ("H", ctypes.c_int32), ("T", ctypes.c_int32),
+                ("D", ctypes.c_int32), ("stride_b", ctypes.c_int64),
+                ("stride_h", ctypes.c_int64), ("stride_t", ctypes.c_int64)]
+
+    def __repr__(self):
+        return (f"WaveLayout(B={self.B}, H={self.H}, T={self.T}, D={self.D}, "
+                f"strides=({self.stride_b}, {self.stride_h}, {self.stride_t}))")
+
+
+def layout_bhtd(B, H, T, D) -> WaveLayout:
+    """Contiguous [B,H,T,D]."""
+    return WaveLayout(B, H, T, D, H * T * D, T * D, D)
+
+
+def layout_seq(B, T, n_head, n_embd) -> WaveLayout:
+    """Reference per-sequence layout [T][n_embd] batched as [B][T][n_embd]."""
+    D = n_embd // n_head
+    return WaveLayout(B, n_head, T, D, T * n_embd, D, n_embd)
+
+
+def build() -> None:
+    """Compile libwave_hip_attn.so for gfx950 with the package Makefile."""
+    subprocess.run(["make", "-s", "-C", str(PKG_DIR), "-j8"], check=True)
+
+
+_lib = None
+
+
+def lib():
+    """The loaded C library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                               f"or `make -C {PKG_DIR}`; there is no fallback path")
+        L = ctypes.CDLL(str(LIB_PATH))
+        vp, f32p, lp = ctypes.c_void_p, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(WaveLayout)
+        sz, i32 = ctypes.c_size_t, ctypes.c_int32
+        L.wha_last_error.restype = ctypes.c_char_p
+        L.wha_version.restype = ctypes.c_char_p
+        L.wha_attn_fwd.argtypes = [vp, vp, vp, vp, vp, lp, ctypes.c_float, vp]
+        L.wha_attn_bwd_workspace_size.argtypes = [lp]
+        L.wha_attn_bwd_workspace_size.restype = sz
+        L.wha_attn_bwd.argtypes = [vp] * 9 + [vp, sz, lp, ctypes.c_float, vp]
+        L.wha_attn_bwd_from_probs_workspace_size.argtypes = [lp]
+        L.wha_attn_bwd_from_probs_workspace_size.restype = sz
+        L.wha_attn_bwd_from_probs.argtypes = [vp] * 8 + [vp, sz, lp, ctypes.c_float, vp]
+        L.wha_decode_workspace_size.argtypes = [lp]
+        L.wha_decode_workspace_size.restype = sz
+        L.wha_decode_fwd.argtypes = [vp] * 5 + [vp, sz, lp, ctypes.c_float, vp]
+        L.wha_host_attention_core_fwd.argtypes = [f32p, f32p, f32p, i32, i32, i32, f32p]
+        L.wha_host_attention_backward.argtypes = [f32p] * 5 + [i32, i32, i32] + [f32p] * 3
+        L.wha_synth_normal.argtypes = [ctypes.POINTER(ctypes.c_uint64), f32p, sz, ctypes.c_double, ctypes.c_int]
+        L.wha_synth_normal.restype = ctypes.c_int
+        L.wha_timing_enable.argtypes = [ctypes.c_int]
+        L.wha_timing_read.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
+                                      ctypes.POINTER(ctypes.c_int64)]
+        for name in EXPORTED_SYMBOLS:
+            if name not in ("wha_last_error", "wha_version") and not name.endswith("_size"):
+                getattr(L, name).restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+class WaveHipError(RuntimeError):
+    def __init__(self, fn, code, msg):
+        super().__init__(f"{fn} failed with code {code}: {msg}")
+        self.code = code
+
+
+def _check(fn, rc):
+    if rc != WHA_OK:
+        raise WaveHipError(fn, rc, lib().wha_last_error().decode())
+
+
+def version() -> str:
+    return lib().wha_version().decode()
+
+
+# ------------------------------------------------------------------ torch plumbing
+
+def _torch():
+    import torch
+    return torch
+
+
+def _stream_ptr(t):
+    torch = _torch()
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def layout_of(t) -> WaveLayout:
+    """Layout of a 4-D [B,H,T,D] float32 cuda tensor view (unit stride on D)."""
+    torch = _torch()
+    if t.dim() != 4:
+        raise ValueError(f"expected a 4-D [B,H,T,D] tensor, got shape {tuple(t.shape)}")
+    if t.dtype != torch.float32:
+        raise TypeError(f"expected float32, got {t.dtype}")
+    if not t.is_cuda:
+        raise ValueError("expected a device (cuda/hip) tensor")
+    if t.stride(3) != 1 and t.shape[3] > 1:
+        raise ValueError("the head dimension must have unit stride")
+    B, H, T, D = t.shape
+    return WaveLayout(B, H, T, D, t.stride(0), t.stride(1), t.stride(2))
+
+
+def _same_layout(L, *ts):
+    for t in ts:
+        l2 = layout_of(t)
+        if (l2.B, l2.H, l2.T, l2.D, l2.stride_b, l2.stride_h, l2.stride_t) != \
+                (L.B, L.H, L.T, L.D, L.stride_b, L.stride_h, L.stride_t):
+            raise ValueError(f"all tensors must share one layout: {L} vs {l2}")
+
+
+def default_scale(D: int) -> float:
+    """1/sqrt(head_dim) rounded to f32, as src/common/compute.rs:362 computes it."""
+    return float(np.float32(1.0) / np.sqrt(np.float32(D)))
+
+
+def attn_fwd(q, k, v, scale=None, want_lse=True, out=None, lse=None):
+    """Fused causal forward on [B,H,T,D] views.  Returns (o, lse) with lse
+    [B,H,T] (natural-log row log-sum-exp), or o alone when want_lse=False."""
+    torch = _torch()
+    L = layout_of(q)
+    _same_layout(L, k, v)
+    if out is None:
+        out = torch.empty_strided(q.shape, q.stride(), dtype=q.dtype, device=q.device)
+    _same_layout(L, out)
+    if want_lse and lse is None:
+        lse = torch.empty((L.B, L.H, L.T), dtype=torch.float32, device=q.device)
+    s = default_scale(L.D) if scale is None else float(scale)
+    _check("wha_attn_fwd", lib().wha_attn_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(out),
+                                              _ptr(lse) if want_lse else None,
+                                              ctypes.byref(L), s, _stream_ptr(q)))
+    return (out, lse) if want_lse else out
+
+
+def attn_bwd(q, k, v, o, do, lse, scale=None, workspace=None, dq=None, dk=None, dv=None):
+    """Fused causal backward (P recomputed from lse).  Returns (dq, dk, dv)."""
+    torch = _torch()
+    L = layout_of(q)
+    _same_layout(L, k, v, o, do)
+    dq = torch.empty_strided(q.shape, q.stride(), dtype=q.dtype, device=q.device) if dq is None else dq
+    dk = torch.empty_strided(q.shape, q.stride(), dtype=q.dtype, device=q.device) if dk is None else dk
+    dv = torch.empty_strided(q.shape, q.stride(), dtype=q.dtype, device=q.device) if dv is None else dv
+    _same_layout(L, dq, dk, dv)
+    s = default_scale(L.D) if scale is None else float(scale)
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check("wha_attn_bwd", lib().wha_attn_bwd(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse.contiguous()), _ptr(dq), _ptr(dk), _ptr(dv),
+        _ptr(workspace), ws_bytes, ctypes.byref(L), s, _stream_ptr(q)))
+    return dq, dk, dv
+
+
+def attn_bwd_workspace_bytes(L: WaveLayout) -> int:
+    return int(lib().wha_attn_bwd_workspace_size(ctypes.byref(L)))
+
+
+def attn_bwd_from_probs(do, q, k, v, att, scale=None, workspace=None):
+    """Backward with att [B,H,T,T] used as given (the reference contract)."""
+    torch = _torch()
+    L = layout_of(q)
+    _same_layout(L, k, v, do)
+    if tuple(att.shape) != (L.B, L.H, L.T, L.T) or not att.is_contiguous():
+        raise ValueError(f"att must be a contiguous [B,H,T,T] tensor, got {tuple(att.shape)}")
+    dq, dk, dv = (torch.empty_strided(q.shape, q.stride(), dtype=q.dtype, device=q.device) for _ in range(3))
+    s = default_scale(L.D) if scale is None else float(scale)
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check("wha_attn_bwd_from_probs", lib().wha_attn_bwd_from_probs(
+        _ptr(do), _ptr(q), _ptr(k), _ptr(v), _ptr(att), _ptr(dq), _ptr(dk), _ptr(dv),
+        _ptr(workspace), ws_bytes, ctypes.byref(L), s, _stream_ptr(q)))
+    return dq, dk, dv
+
+
+def decode_fwd(q, k_cache, v_cache, scale=None, want_lse=False, workspace=None):
+    """Single-token decode: q [B,H,D] against a [B,H,Tk,D] cache view."""
+    torch = _torch()
+    L = layout_of(k_cache)
+    _same_layout(L, v_cache)
+    if tuple(q.shape) != (L.B, L.H, L.D) or not q.is_contiguous():
+        raise ValueError(f"q must be a contiguous [B,H,D] tensor, got {tuple(q.shape)}")
+    o = torch.empty_like(q)
+    lse = torch.empty((L.B, L.H), dtype=torch.float32, device=q.device) if want_lse else None
+    s = default_scale(L.D) if scale is None else float(scale)
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check("wha_decode_fwd", lib().wha_decode_fwd(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(o), _ptr(lse) if want_lse else None,
+        _ptr(workspace), ws_bytes, ctypes.byref(L), s, _stream_ptr(q)))
+    return (o, lse) if want_lse else o
+
+
+# ------------------------------------------------------------------ timing
+
+def timing_enable(on: bool = True):
+    _check("wha_timing_enable", lib().wha_timing_enable(1 if on else 0))
+
+
+def timing_reset():
+    _check("wha_timing_reset", lib().wha_timing_reset())
+
+
+def timing_read(kernel: str):
+    """(total_ms, launches) of a kernel since the last reset."""
+    ms, n = ctypes.c_double(0.0), ctypes.c_int64(0)
+    _check("wha_timing_read", lib().wha_timing_read(kernel.encode(), ctypes.byref(ms), ctypes.byref(n)))
+    return ms.value, n.value
+
+
+# ------------------------------------------------------------------ reference-interface mirror
+
+def _as_2d_f32(x, name):
+    a = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    if a.ndim != 2:
+        raise ValueError(f"{name}: expected [T][n_embd], got shape {a.shape}")
+    return a
+
+
+def _fp(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+class HipBackend:
+    """The attention half of wave-engine's ``ComputeBackend`` on the HIP tier.
+
+    Mirrors ``fn attention_backward(&self, d_pre_proj, q_all, k_all, v_all,
+    att_weights, n_head) -> (d_q, d_k, d_v)`` (``src/common/compute.rs:163-173``)
+    with ``CpuBackend``'s semantics (``:286-314``: att used as given), and the core
+    of ``fn attention`` (``attention_cpu``, ``:377-409``).  Inputs are
+    ``[T][n_embd]`` host arrays (lists of rows or 2-D arrays); outputs are
+    ``[T][n_embd]`` float32 numpy arrays.  Failures raise ``RuntimeError`` where
+    the reference panics."""
+
+    def attention_core(self, q_all, k_all, v_all, n_head: int):
+        q, k, v = (_as_2d_f32(a, n) for a, n in ((q_all, "q_all"), (k_all, "k_all"), (v_all, "v_all")))
+        T, E = q.shape
+        out = np.empty((T, E), dtype=np.float32)
+        _check("wha_host_attention_core_fwd",
+               lib().wha_host_attention_core_fwd(_fp(q), _fp(k), _fp(v), T, E, int(n_head), _fp(out)))
+        return out
+
+    def attention_backward(self, d_pre_proj, q_all, k_all, v_all, att_weights, n_head: int):
+        d, q, k, v = (_as_2d_f32(a, n) for a, n in ((d_pre_proj, "d_pre_proj"), (q_all, "q_all"),
+                                                    (k_all, "k_all"), (v_all, "v_all")))
+        T, E = q.shape
+        att = np.ascontiguousarray(np.asarray(att_weights, dtype=np.float32))
+        if att.shape != (int(n_head), T, T):
+            raise ValueError(f"att_weights: expected [n_head][T][T] = {(n_head, T, T)}, got {att.shape}")
+        dq, dk, dv = (np.empty((T, E), dtype=np.float32) for _ in range(3))
+        _check("wha_host_attention_backward",
+               lib().wha_host_attention_backward(_fp(d), _fp(q), _fp(k), _fp(v), _fp(att), T, E,
+                                                 int(n_head), _fp(dq), _fp(dk), _fp(dv)))
+        return dq, dk, dv
+
+
+# ------------------------------------------------------------------ synthetic inputs
+
+class SynthStream:
+    """Seeded normal draws from the library's generator: xorshift64 exactly as
+    the reference's Rng (src/common/rng.rs:24-34) with Box-Muller pairs
+    (u1 = 1 - next_f32, u2 = next_f32) evaluated in double."""
+
+    def __init__(self, seed: int = 42):
+        if seed == 0:
+            raise ValueError("xorshift64 seed must be non-zero")
+        self.state = ctypes.c_uint64(seed)
+
+    def normal(self, n: int, stddev: float = 1.0, nthreads: int = 0) -> np.ndarray:
+        out = np.empty(n, dtype=np.float32)
+        rc = lib().wha_synth_normal(ctypes.byref(self.state), out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                    n, float(stddev), int(nthreads))
+        if rc != 0:
+            raise ValueError("wha_synth_normal: invalid state")
+        return out
+
+
+def synth_inputs(B: int, H: int, T: int, D: int, seed: int = 42, with_do: bool = True):
+    """BASELINE inputs: Q, K, V ~ N(0,1)/sqrt(D), then dO ~ N(0,1), drawn in that
+    order from one stream, each in [B][H][T][D] row-major order (numpy float32)."""
+    g = SynthStream(seed)
+    n = B * H * T * D
+    sd = 1.0 / math.sqrt(float(D))
+    out = [g.normal(n, sd).reshape(B, H, T, D) for _ in range(3)]
+    if with_do:
+        out.append(g.normal(n, 1.0).reshape(B, H, T, D))
+    return tuple(out)

@@ -1,0 +1,424 @@
+// Causal attention backward for gfx950 (fp32 MFMA).
+//
+// Math (per (b,h); P = causal softmax(Q K^T * scale), dO = upstream gradient):
+//   dV = P^T dO                      dP = dO V^T
+//   dS = P o (dP - Delta),  Delta_t = sum_j P_tj dP_tj  (= dO_t . O_t)
+//   dQ = scale * dS K                dK = scale * dS^T Q
+// which is attention_backward_single (reference src/cpu/backward.rs:313-363)
+// summed over positions by CpuBackend::attention_backward
+// (src/common/compute.rs:286-314).  The reference's wgpu tier splits the same
+// work into attn_backward_scores (dS and dQ per query row,
+// shaders/attn_backward_scores.wgsl:27-111) and attn_backward_dkv (dK, dV per
+// key, shaders/attn_backward_dkv.wgsl:22-63); this file keeps that split but
+// tiles both on MFMA and never materialises dS:
+//   attn_bwd_delta_kernel  Delta_t = dO_t . O_t                 (fused path)
+//   attn_bwd_dq_kernel     query-stationary: recompute P, dP, dS; dQ += dS K
+//   attn_bwd_dkv_kernel    key-stationary:   recompute P, dP, dS; dV += P^T dO, dK += dS^T Q
+// The "from probabilities" variants read P from the caller's att tensor instead
+// of recomputing it (the reference contract, att used as given), and obtain
+// Delta from att and dP (mode kDeltaFromProbs) because O is not an input there.
+//
+// Layouts: in the query-stationary kernel a wave forms S^T/dP^T with keys on
+// MFMA rows and its 16 queries on columns (one query per lane, as in the
+// forward), so dS^T is directly the B operand of dQ^T += K^T dS^T.  In the
+// key-stationary kernel a wave keeps its 16 keys in registers and forms S/dP
+// with queries on rows and its keys on columns, so P and dS are directly the B
+// operands of dV^T += dO^T P and dK^T += Q^T dS.
+#include "wha_launch.hpp"
+
+namespace wha {
+
+enum DqMode { kFused = 0, kProbs = 1, kDeltaFromProbs = 2 };
+
+// Delta_t = sum_d dO[t][d] * O[t][d]; 16 lanes per row, 16 rows per block.
+__global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const float* __restrict__ O,
+                                                             const float* __restrict__ dO,
+                                                             float* __restrict__ Delta, View L) {
+  const int64_t rows = (int64_t)L.B * L.H * L.T;
+  const int64_t r = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  float acc = 0.f;
+  if (r < rows) {
+    const int t = (int)(r % L.T);
+    const int64_t bh = r / L.T;
+    const int b = (int)(bh / L.H), h = (int)(bh % L.H);
+    const int64_t off = (int64_t)b * L.sb + (int64_t)h * L.sh + (int64_t)t * L.st;
+    for (int d = sub; d < L.D; d += 16) acc += dO[off + d] * O[off + d];
+  }
+  acc += __shfl_xor(acc, 8, 16);
+  acc += __shfl_xor(acc, 4, 16);
+  acc += __shfl_xor(acc, 2, 16);
+  acc += __shfl_xor(acc, 1, 16);
+  if (r < rows && sub == 0) Delta[r] = acc;
+}
+
+// Query-stationary kernel: dQ (modes kFused, kProbs) or Delta (kDeltaFromProbs).
+template <int DP, int NW, bool VEC, int MODE>
+__global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, const float* __restrict__ LSE, float* __restrict__ Delta,
+    const float* __restrict__ ATT, float* __restrict__ dQ, View L, float scale, float scale_log2) {
+  constexpr int NT = NW * 64;
+  constexpr int BM = NW * 16;
+  constexpr int BN = 64;
+  constexpr int LD = DP + 4;
+  constexpr int DG = DP / 4;
+  constexpr int NDT = DP / 16;
+  constexpr int NKT = BN / 16;
+  constexpr bool kNeedK = MODE != kDeltaFromProbs;
+  __shared__ __align__(16) float Ks[kNeedK ? BN * LD : 4];
+  __shared__ __align__(16) float Vs[BN * LD];
+
+  const int BH = L.B * L.H;
+  const int n_qt = (L.T + BM - 1) / BM;
+  const int bh = blockIdx.x % BH;
+  const int qt = n_qt - 1 - (int)(blockIdx.x / BH);
+  const int b = bh / L.H, h = bh % L.H;
+  const int64_t base = (int64_t)b * L.sb + (int64_t)h * L.sh;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 15, g = lane >> 4;
+  const int q0 = qt * BM + wave * 16;
+  const int qrow = q0 + lq;
+  const bool row_ok = qrow < L.T;
+
+  float qf[MODE == kFused ? DG : 1];
+  if (MODE == kFused) load_row_frag<DP, VEC>(Q + base, qrow, L.T, L.D, L.st, g, scale_log2, qf);
+  float of[DG];
+  load_row_frag<DP, VEC>(dO + base, qrow, L.T, L.D, L.st, g, 1.f, of);
+  const int64_t rix = (int64_t)bh * L.T + qrow;
+  const float lse2 = (MODE == kFused && row_ok) ? LSE[rix] * kLog2e : 0.f;
+  const float delta = (MODE != kDeltaFromProbs && row_ok) ? Delta[rix] : 0.f;
+  const float* att_row = (MODE != kFused) ? ATT + ((int64_t)bh * L.T + (row_ok ? qrow : 0)) * L.T : nullptr;
+
+  const int q_hi = min(L.T, (qt + 1) * BM);
+  const int n_kt = (q_hi + BN - 1) / BN;
+
+  TileStage<DP, BN, NT, VEC> ks, vs;
+  if (kNeedK) ks.load(K + base, 0, L.T, L.D, L.st, tid);
+  vs.load(V + base, 0, L.T, L.D, L.st, tid);
+
+  floatx4 dqacc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) dqacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float dsum = 0.f;
+
+  for (int kt = 0; kt < n_kt; ++kt) {
+    __syncthreads();
+    if (kNeedK) ks.template store<LD>(Ks, tid);
+    vs.template store<LD>(Vs, tid);
+    __syncthreads();
+    if (kt + 1 < n_kt) {
+      if (kNeedK) ks.load(K + base, (kt + 1) * BN, L.T, L.D, L.st, tid);
+      vs.load(V + base, (kt + 1) * BN, L.T, L.D, L.st, tid);
+    }
+    const int key0 = kt * BN;
+    if (key0 > q0 + 15) continue;
+
+    floatx4 s[NKT], dp[NKT];
+#pragma unroll
+    for (int mt = 0; mt < NKT; ++mt) {
+      s[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      dp[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < DG / 4; ++j) {
+#pragma unroll
+      for (int mt = 0; mt < NKT; ++mt) {
+        if (MODE == kFused) {
+          const float4 a = *reinterpret_cast<const float4*>(&Ks[(16 * mt + lq) * LD + g * DG + 4 * j]);
+          s[mt] = mfma4(a.x, qf[4 * j + 0], s[mt]);
+          s[mt] = mfma4(a.y, qf[4 * j + 1], s[mt]);
+          s[mt] = mfma4(a.z, qf[4 * j + 2], s[mt]);
+          s[mt] = mfma4(a.w, qf[4 * j + 3], s[mt]);
+        }
+        const float4 c = *reinterpret_cast<const float4*>(&Vs[(16 * mt + lq) * LD + g * DG + 4 * j]);
+        dp[mt] = mfma4(c.x, of[4 * j + 0], dp[mt]);
+        dp[mt] = mfma4(c.y, of[4 * j + 1], dp[mt]);
+        dp[mt] = mfma4(c.z, of[4 * j + 2], dp[mt]);
+        dp[mt] = mfma4(c.w, of[4 * j + 3], dp[mt]);
+      }
+    }
+
+    // P (recomputed or read), dS; lane element (mt,i) is key key0+16mt+4g+i of query qrow
+#pragma unroll
+    for (int mt = 0; mt < NKT; ++mt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = key0 + 16 * mt + 4 * g + i;
+        const bool valid = key <= qrow && key < L.T && row_ok;
+        float p;
+        if (MODE == kFused) {
+          p = valid ? fast_exp2(s[mt][i] - lse2) : 0.f;
+        } else {
+          p = valid ? att_row[key] : 0.f;
+        }
+        if (MODE == kDeltaFromProbs) {
+          dsum += p * dp[mt][i];
+        } else {
+          dp[mt][i] = p * (dp[mt][i] - delta);
+        }
+      }
+    }
+
+    if (MODE != kDeltaFromProbs) {
+      // dQ^T[d][query] += K^T[d][key] dS^T[key][query]
+#pragma unroll
+      for (int mt = 0; mt < NKT; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float* krow = &Ks[(16 * mt + 4 * g + i) * LD + lq];
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) dqacc[dt] = mfma4(krow[16 * dt], dp[mt][i], dqacc[dt]);
+        }
+      }
+    }
+  }
+
+  if (MODE == kDeltaFromProbs) {
+    dsum += xor_shfl(dsum, 16);
+    dsum += xor_shfl(dsum, 32);
+    if (g == 0 && row_ok) Delta[rix] = dsum;
+  } else {
+    store_rowT<DP, VEC>(dQ + base, qrow, L.T, L.D, L.st, g, dqacc, scale);
+  }
+}
+
+// Key-stationary kernel: dK and dV for NW*16 consecutive keys of one (b,h).
+template <int DP, int NW, bool VEC, bool PROBS>
+__global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Delta,
+    const float* __restrict__ ATT, float* __restrict__ dK, float* __restrict__ dV, View L,
+    float scale, float scale_log2) {
+  constexpr int NT = NW * 64;
+  constexpr int BNK = NW * 16;  // keys per block
+  constexpr int BMQ = 64;       // queries per tile
+  constexpr int LD = DP + 4;
+  constexpr int DG = DP / 4;
+  constexpr int NDT = DP / 16;
+  constexpr int NQT = BMQ / 16;
+  __shared__ __align__(16) float Qs[BMQ * LD];
+  __shared__ __align__(16) float Os[BMQ * LD];  // dO tile
+  __shared__ float lse_s[BMQ];
+  __shared__ float del_s[BMQ];
+
+  const int BH = L.B * L.H;
+  const int bh = blockIdx.x % BH;
+  const int kt = (int)(blockIdx.x / BH);  // kt = 0 (the most query tiles) first
+  const int b = bh / L.H, h = bh % L.H;
+  const int64_t base = (int64_t)b * L.sb + (int64_t)h * L.sh;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 15, g = lane >> 4;
+  const int k0w = kt * BNK + wave * 16;  // first key of this wave
+  const int krow = k0w + lq;             // this lane's key
+
+  float kf[PROBS ? 1 : DG];
+  if (!PROBS) load_row_frag<DP, VEC>(K + base, krow, L.T, L.D, L.st, g, scale_log2, kf);
+  float vf[DG];
+  load_row_frag<DP, VEC>(V + base, krow, L.T, L.D, L.st, g, 1.f, vf);
+
+  floatx4 dkacc[NDT], dvacc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+    dkacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    dvacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int n_qt = (L.T + BMQ - 1) / BMQ;
+  const int qt0 = (kt * BNK) / BMQ;
+  const int64_t rbase = (int64_t)bh * L.T;
+
+  TileStage<DP, BMQ, NT, VEC> qs, os;
+  float lse_r = 0.f, del_r = 0.f;
+  auto load_tile = [&](int qt) {
+    qs.load(Q + base, qt * BMQ, L.T, L.D, L.st, tid);
+    os.load(dO + base, qt * BMQ, L.T, L.D, L.st, tid);
+    if (tid < BMQ) {
+      const int q = qt * BMQ + tid;
+      lse_r = (!PROBS && q < L.T) ? LSE[rbase + q] * kLog2e : 0.f;
+      del_r = q < L.T ? Delta[rbase + q] : 0.f;
+    }
+  };
+  if (qt0 < n_qt) load_tile(qt0);
+
+  for (int qt = qt0; qt < n_qt; ++qt) {
+    __syncthreads();
+    qs.template store<LD>(Qs, tid);
+    os.template store<LD>(Os, tid);
+    if (tid < BMQ) {
+      lse_s[tid] = lse_r;
+      del_s[tid] = del_r;
+    }
+    __syncthreads();
+    if (qt + 1 < n_qt) load_tile(qt + 1);
+    const int qb = qt * BMQ;
+    if (qb + BMQ - 1 < k0w) continue;  // every query of the tile precedes every key of the wave
+
+    floatx4 s[NQT], dp[NQT];
+#pragma unroll
+    for (int mt = 0; mt < NQT; ++mt) {
+      s[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      dp[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < DG / 4; ++j) {
+#pragma unroll
+      for (int mt = 0; mt < NQT; ++mt) {
+        if (!PROBS) {
+          const float4 a = *reinterpret_cast<const float4*>(&Qs[(16 * mt + lq) * LD + g * DG + 4 * j]);
+          s[mt] = mfma4(a.x, kf[4 * j + 0], s[mt]);
+          s[mt] = mfma4(a.y, kf[4 * j + 1], s[mt]);
+          s[mt] = mfma4(a.z, kf[4 * j + 2], s[mt]);
+          s[mt] = mfma4(a.w, kf[4 * j + 3], s[mt]);
+        }
+        const float4 c = *reinterpret_cast<const float4*>(&Os[(16 * mt + lq) * LD + g * DG + 4 * j]);
+        dp[mt] = mfma4(c.x, vf[4 * j + 0], dp[mt]);
+        dp[mt] = mfma4(c.y, vf[4 * j + 1], dp[mt]);
+        dp[mt] = mfma4(c.z, vf[4 * j + 2], dp[mt]);
+        dp[mt] = mfma4(c.w, vf[4 * j + 3], dp[mt]);
+      }
+    }
+
+    // lane element (mt,i): query qb+16mt+4g+i, key krow
+#pragma unroll
+    for (int mt = 0; mt < NQT; ++mt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int qi = 16 * mt + 4 * g + i;
+        const int q = qb + qi;
+        const bool valid = krow <= q && q < L.T && krow < L.T;
+        float p;
+        if (!PROBS) {
+          p = valid ? fast_exp2(s[mt][i] - lse_s[qi]) : 0.f;
+        } else {
+          p = valid ? ATT[(rbase + q) * L.T + krow] : 0.f;
+        }
+        s[mt][i] = p;
+        dp[mt][i] = p * (dp[mt][i] - del_s[qi]);
+      }
+    }
+
+    // dV^T[d][key] += dO^T[d][query] P[query][key];  dK^T[d][key] += Q^T[d][query] dS[query][key]
+#pragma unroll
+    for (int mt = 0; mt < NQT; ++mt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float* orow = &Os[(16 * mt + 4 * g + i) * LD + lq];
+        const float* qrow = &Qs[(16 * mt + 4 * g + i) * LD + lq];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          dvacc[dt] = mfma4(orow[16 * dt], s[mt][i], dvacc[dt]);
+          dkacc[dt] = mfma4(qrow[16 * dt], dp[mt][i], dkacc[dt]);
+        }
+      }
+    }
+  }
+
+  store_rowT<DP, VEC>(dK + base, krow, L.T, L.D, L.st, g, dkacc, scale);
+  store_rowT<DP, VEC>(dV + base, krow, L.T, L.D, L.st, g, dvacc, 1.f);
+}
+
+namespace {
+
+template <int DP, bool VEC>
+hipError_t bwd_fused_t(const float* q, const float* k, const float* v, const float* o,
+                       const float* d_o, const float* lse, float* dq, float* dk, float* dv,
+                       float* delta, const View& L, float scale, hipStream_t stream) {
+  constexpr int NWQ = 4, NWK = 4;
+  const float sl2 = (float)((double)scale * 1.4426950408889634);
+  const int64_t rows = (int64_t)L.B * L.H * L.T;
+  {
+    TimingScope ts("attn_bwd_delta", stream);
+    hipLaunchKernelGGL(attn_bwd_delta_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, stream,
+                       o, d_o, delta, L);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  {
+    const int n_qt = (L.T + NWQ * 16 - 1) / (NWQ * 16);
+    TimingScope ts("attn_bwd_dq", stream);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<DP, NWQ, VEC, kFused>), dim3((unsigned)(n_qt * L.B * L.H)),
+                       dim3(NWQ * 64), 0, stream, q, k, v, d_o, lse, delta, (const float*)nullptr, dq, L,
+                       scale, sl2);
+  }
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  {
+    const int n_kt = (L.T + NWK * 16 - 1) / (NWK * 16);
+    TimingScope ts("attn_bwd_dkv", stream);
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<DP, NWK, VEC, false>), dim3((unsigned)(n_kt * L.B * L.H)),
+                       dim3(NWK * 64), 0, stream, q, k, v, d_o, lse, (const float*)delta,
+                       (const float*)nullptr, dk, dv, L, scale, sl2);
+  }
+  return hipGetLastError();
+}
+
+template <int DP, bool VEC>
+hipError_t bwd_probs_t(const float* d_o, const float* q, const float* k, const float* v,
+                       const float* att, float* dq, float* dk, float* dv, float* delta,
+                       const View& L, float scale, hipStream_t stream) {
+  constexpr int NWQ = 4, NWK = 4;
+  const int n_qt = (L.T + NWQ * 16 - 1) / (NWQ * 16);
+  const int n_kt = (L.T + NWK * 16 - 1) / (NWK * 16);
+  {
+    TimingScope ts("attn_bwd_probs_delta", stream);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<DP, NWQ, VEC, kDeltaFromProbs>),
+                       dim3((unsigned)(n_qt * L.B * L.H)), dim3(NWQ * 64), 0, stream, q, k, v, d_o,
+                       (const float*)nullptr, delta, att, (float*)nullptr, L, scale, 0.f);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  {
+    TimingScope ts("attn_bwd_probs_dq", stream);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<DP, NWQ, VEC, kProbs>), dim3((unsigned)(n_qt * L.B * L.H)),
+                       dim3(NWQ * 64), 0, stream, q, k, v, d_o, (const float*)nullptr, delta, att, dq, L,
+                       scale, 0.f);
+  }
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  {
+    TimingScope ts("attn_bwd_probs_dkv", stream);
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<DP, NWK, VEC, true>), dim3((unsigned)(n_kt * L.B * L.H)),
+                       dim3(NWK * 64), 0, stream, q, k, v, d_o, (const float*)nullptr,
+                       (const float*)delta, att, dk, dv, L, scale, 0.f);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const float* o,
+                           const float* d_o, const float* lse, float* dq, float* dk, float* dv,
+                           float* delta, const View& L, bool vec, float scale, hipStream_t stream) {
+#define WHA_BWD(DP)                                                                         \
+  return vec ? bwd_fused_t<DP, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, L, scale, stream) \
+             : bwd_fused_t<DP, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, L, scale, stream)
+  switch (padded_dim(L.D)) {
+    case 48: WHA_BWD(48);
+    case 64: WHA_BWD(64);
+    case 128: WHA_BWD(128);
+    default: return hipErrorInvalidValue;
+  }
+#undef WHA_BWD
+}
+
+hipError_t launch_attn_bwd_probs(const float* d_o, const float* q, const float* k, const float* v,
+                                 const float* att, float* dq, float* dk, float* dv, float* delta,
+                                 const View& L, bool vec, float scale, hipStream_t stream) {
+#define WHA_BWDP(DP)                                                                            \
+  return vec ? bwd_probs_t<DP, true>(d_o, q, k, v, att, dq, dk, dv, delta, L, scale, stream) \
+             : bwd_probs_t<DP, false>(d_o, q, k, v, att, dq, dk, dv, delta, L, scale, stream)
+  switch (padded_dim(L.D)) {
+    case 48: WHA_BWDP(48);
+    case 64: WHA_BWDP(64);
+    case 128: WHA_BWDP(128);
+    default: return hipErrorInvalidValue;
+  }
+#undef WHA_BWDP
+}
+
+}  // namespace wha

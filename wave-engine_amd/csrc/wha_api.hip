@@ -1,0 +1,467 @@
+// C ABI of the gfx950 attention tier: argument validation, error reporting,
+// workspace management, host-pointer entry points and optional event timing.
+// Declarations and contracts: include/wave_hip_attn.h.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/wave_hip_attn.h"
+#include "wha_launch.hpp"
+
+#ifndef WHA_VERSION
+#define WHA_VERSION "0.1.0"
+#endif
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(WHA_ERR_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+bool aligned16(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Validates a layout; on success fills the kernel view.
+int check_layout(const wha_layout* L, wha::View* v, const char* fn) {
+  if (L == nullptr) return fail(WHA_ERR_INVALID, "%s: layout is NULL", fn);
+  if (L->B <= 0 || L->H <= 0 || L->T <= 0 || L->D <= 0)
+    return fail(WHA_ERR_INVALID, "%s: B, H, T, D must be positive (got %d, %d, %d, %d)", fn, L->B, L->H,
+                L->T, L->D);
+  if (wha::padded_dim(L->D) == 0)
+    return fail(WHA_ERR_UNSUPPORTED, "%s: head_dim %d exceeds the supported maximum of 128", fn, L->D);
+  if (L->stride_t < L->D || L->stride_h < 0 || L->stride_b < 0)
+    return fail(WHA_ERR_INVALID, "%s: invalid strides (b=%lld, h=%lld, t=%lld) for D=%d", fn,
+                (long long)L->stride_b, (long long)L->stride_h, (long long)L->stride_t, L->D);
+  if ((int64_t)L->B * L->H * L->T > (int64_t)1 << 31)
+    return fail(WHA_ERR_UNSUPPORTED, "%s: B*H*T too large", fn);
+  v->B = L->B;
+  v->H = L->H;
+  v->T = L->T;
+  v->D = L->D;
+  v->sb = L->stride_b;
+  v->sh = L->stride_h;
+  v->st = L->stride_t;
+  return WHA_OK;
+}
+
+bool vec_ok(const wha::View& v, std::initializer_list<const void*> ptrs) {
+  if (v.D % 4 || v.st % 4 || v.sh % 4 || v.sb % 4) return false;
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return false;
+  return true;
+}
+
+int check_scale(float scale, const char* fn) {
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(WHA_ERR_INVALID, "%s: scale must be positive and finite (got %g)", fn, (double)scale);
+  return WHA_OK;
+}
+
+size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// ---------------------------------------------------------------- workspace cache
+// One growable device buffer per (host thread, device, stream): concurrent
+// callers on different threads or streams never share scratch memory.
+struct WsEntry {
+  int device;
+  hipStream_t stream;
+  void* ptr;
+  size_t bytes;
+};
+struct WsCache {
+  std::vector<WsEntry> entries;
+  ~WsCache() {
+    for (auto& e : entries)
+      if (e.ptr) (void)hipFree(e.ptr);
+  }
+};
+thread_local WsCache g_ws;
+
+int cached_workspace(size_t bytes, hipStream_t stream, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  for (auto& w : g_ws.entries) {
+    if (w.device == dev && w.stream == stream) {
+      if (w.bytes < bytes) {
+        // the previous user of this buffer was enqueued on the same stream, so
+        // freeing after a stream sync is safe
+        e = hipStreamSynchronize(stream);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+        (void)hipFree(w.ptr);
+        w.ptr = nullptr;
+        w.bytes = 0;
+        e = hipMalloc(&w.ptr, bytes);
+        if (e != hipSuccess) return fail(WHA_ERR_NOMEM, "workspace hipMalloc(%zu) failed", bytes);
+        w.bytes = bytes;
+      }
+      *out = w.ptr;
+      return WHA_OK;
+    }
+  }
+  WsEntry w{dev, stream, nullptr, 0};
+  e = hipMalloc(&w.ptr, bytes);
+  if (e != hipSuccess) return fail(WHA_ERR_NOMEM, "workspace hipMalloc(%zu) failed", bytes);
+  w.bytes = bytes;
+  g_ws.entries.push_back(w);
+  *out = w.ptr;
+  return WHA_OK;
+}
+
+int resolve_workspace(void* ws, size_t ws_bytes, size_t need, hipStream_t stream, const char* fn,
+                      void** out) {
+  if (ws == nullptr) return cached_workspace(need, stream, out);
+  if (ws_bytes < need)
+    return fail(WHA_ERR_WORKSPACE, "%s: workspace of %zu bytes is smaller than the %zu required", fn,
+                ws_bytes, need);
+  if (!aligned16(ws)) return fail(WHA_ERR_INVALID, "%s: workspace must be 16-byte aligned", fn);
+  *out = ws;
+  return WHA_OK;
+}
+
+// ---------------------------------------------------------------- timing
+struct TimingRec {
+  std::string name;
+  hipEvent_t start, stop;
+};
+struct TimingState {
+  std::mutex mu;
+  bool on = false;
+  std::vector<TimingRec> pending;
+  std::map<std::string, std::pair<double, int64_t>> totals;
+};
+TimingState& timing() {
+  static TimingState* s = new TimingState();  // never destroyed: usable during exit
+  return *s;
+}
+
+int drain_timing_locked(TimingState& st) {
+  int rc = WHA_OK;
+  for (auto& r : st.pending) {
+    hipError_t e = hipEventSynchronize(r.stop);
+    float ms = 0.f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.start, r.stop);
+    if (e != hipSuccess) {
+      rc = hip_fail(e, "timing event");
+    } else {
+      auto& t = st.totals[r.name];
+      t.first += ms;
+      t.second += 1;
+    }
+    (void)hipEventDestroy(r.start);
+    (void)hipEventDestroy(r.stop);
+  }
+  st.pending.clear();
+  return rc;
+}
+
+// ---------------------------------------------------------------- host staging
+// Per-thread device buffer and stream for the host-pointer entry points.
+struct HostStage {
+  int device = -1;
+  hipStream_t stream = nullptr;
+  void* buf = nullptr;
+  size_t bytes = 0;
+  ~HostStage() {
+    if (buf) (void)hipFree(buf);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+};
+thread_local HostStage g_host;
+
+int host_stage(size_t bytes, float** base, hipStream_t* stream) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (g_host.device != dev) {
+    if (g_host.buf) (void)hipFree(g_host.buf);
+    if (g_host.stream) (void)hipStreamDestroy(g_host.stream);
+    g_host.buf = nullptr;
+    g_host.bytes = 0;
+    g_host.stream = nullptr;
+    e = hipStreamCreateWithFlags(&g_host.stream, hipStreamNonBlocking);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamCreateWithFlags");
+    g_host.device = dev;
+  }
+  if (g_host.bytes < bytes) {
+    if (g_host.buf) {
+      (void)hipStreamSynchronize(g_host.stream);
+      (void)hipFree(g_host.buf);
+    }
+    g_host.buf = nullptr;
+    g_host.bytes = 0;
+    e = hipMalloc(&g_host.buf, bytes);
+    if (e != hipSuccess) return fail(WHA_ERR_NOMEM, "host staging hipMalloc(%zu) failed", bytes);
+    g_host.bytes = bytes;
+  }
+  *base = static_cast<float*>(g_host.buf);
+  *stream = g_host.stream;
+  return WHA_OK;
+}
+
+int check_host_seq(const char* fn, int32_t T, int32_t E, int32_t n_head, wha::View* v) {
+  if (T <= 0 || E <= 0 || n_head <= 0)
+    return fail(WHA_ERR_INVALID, "%s: T, E, n_head must be positive (got %d, %d, %d)", fn, T, E, n_head);
+  if (E % n_head != 0)
+    return fail(WHA_ERR_INVALID, "%s: n_embd %d is not divisible by n_head %d", fn, E, n_head);
+  wha_layout L{1, n_head, T, E / n_head, (int64_t)T * E, (int64_t)(E / n_head), (int64_t)E};
+  return check_layout(&L, v, fn);
+}
+
+}  // namespace
+
+namespace wha {
+
+TimingScope::TimingScope(const char* name, hipStream_t s) : token(nullptr), stream(s) {
+  TimingState& st = timing();
+  std::lock_guard<std::mutex> lk(st.mu);
+  if (!st.on) return;
+  TimingRec* r = new TimingRec();
+  r->name = name;
+  if (hipEventCreate(&r->start) != hipSuccess || hipEventCreate(&r->stop) != hipSuccess ||
+      hipEventRecord(r->start, s) != hipSuccess) {
+    delete r;
+    return;
+  }
+  token = r;
+}
+
+TimingScope::~TimingScope() {
+  if (!token) return;
+  TimingRec* r = static_cast<TimingRec*>(token);
+  TimingState& st = timing();
+  std::lock_guard<std::mutex> lk(st.mu);
+  if (hipEventRecord(r->stop, stream) == hipSuccess) {
+    st.pending.push_back(*r);
+  } else {
+    (void)hipEventDestroy(r->start);
+    (void)hipEventDestroy(r->stop);
+  }
+  delete r;
+}
+
+}  // namespace wha
+
+extern "C" {
+
+const char* wha_last_error(void) { return g_err; }
+
+const char* wha_version(void) { return WHA_VERSION " gfx950"; }
+
+int wha_attn_fwd(const float* q, const float* k, const float* v, float* o, float* lse,
+                 const wha_layout* layout, float scale, void* stream) {
+  static const char* fn = "wha_attn_fwd";
+  wha::View V;
+  int rc = check_layout(layout, &V, fn);
+  if (rc) return rc;
+  if ((rc = check_scale(scale, fn))) return rc;
+  if (!q || !k || !v || !o) return fail(WHA_ERR_INVALID, "%s: q, k, v and o must be non-NULL", fn);
+  const bool vec = vec_ok(V, {q, k, v, o});
+  hipError_t e = wha::launch_attn_fwd(q, k, v, o, lse, V, vec, scale, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "wha_attn_fwd launch");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+size_t wha_attn_bwd_workspace_size(const wha_layout* layout) {
+  if (!layout || layout->B <= 0 || layout->H <= 0 || layout->T <= 0) return 0;
+  return round256((size_t)layout->B * layout->H * layout->T * sizeof(float));
+}
+
+int wha_attn_bwd(const float* q, const float* k, const float* v, const float* o, const float* d_o,
+                 const float* lse, float* dq, float* dk, float* dv, void* workspace,
+                 size_t workspace_bytes, const wha_layout* layout, float scale, void* stream) {
+  static const char* fn = "wha_attn_bwd";
+  wha::View V;
+  int rc = check_layout(layout, &V, fn);
+  if (rc) return rc;
+  if ((rc = check_scale(scale, fn))) return rc;
+  if (!q || !k || !v || !o || !d_o || !lse || !dq || !dk || !dv)
+    return fail(WHA_ERR_INVALID, "%s: every tensor pointer must be non-NULL", fn);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  if ((rc = resolve_workspace(workspace, workspace_bytes, wha_attn_bwd_workspace_size(layout), s, fn, &ws)))
+    return rc;
+  const bool vec = vec_ok(V, {q, k, v, o, d_o, dq, dk, dv});
+  hipError_t e = wha::launch_attn_bwd(q, k, v, o, d_o, lse, dq, dk, dv, static_cast<float*>(ws), V, vec,
+                                      scale, s);
+  if (e != hipSuccess) return hip_fail(e, "wha_attn_bwd launch");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+size_t wha_attn_bwd_from_probs_workspace_size(const wha_layout* layout) {
+  return wha_attn_bwd_workspace_size(layout);
+}
+
+int wha_attn_bwd_from_probs(const float* d_pre_proj, const float* q, const float* k, const float* v,
+                            const float* att, float* dq, float* dk, float* dv, void* workspace,
+                            size_t workspace_bytes, const wha_layout* layout, float scale,
+                            void* stream) {
+  static const char* fn = "wha_attn_bwd_from_probs";
+  wha::View V;
+  int rc = check_layout(layout, &V, fn);
+  if (rc) return rc;
+  if ((rc = check_scale(scale, fn))) return rc;
+  if (!d_pre_proj || !q || !k || !v || !att || !dq || !dk || !dv)
+    return fail(WHA_ERR_INVALID, "%s: every tensor pointer must be non-NULL", fn);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  if ((rc = resolve_workspace(workspace, workspace_bytes, wha_attn_bwd_from_probs_workspace_size(layout), s,
+                              fn, &ws)))
+    return rc;
+  const bool vec = vec_ok(V, {d_pre_proj, q, k, v, dq, dk, dv});
+  hipError_t e = wha::launch_attn_bwd_probs(d_pre_proj, q, k, v, att, dq, dk, dv, static_cast<float*>(ws),
+                                            V, vec, scale, s);
+  if (e != hipSuccess) return hip_fail(e, "wha_attn_bwd_from_probs launch");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+size_t wha_decode_workspace_size(const wha_layout* layout) {
+  wha::View V;
+  if (!layout || check_layout(layout, &V, "wha_decode_workspace_size") != WHA_OK) return 0;
+  return round256(wha::decode_workspace_floats(V) * sizeof(float));
+}
+
+int wha_decode_fwd(const float* q, const float* k_cache, const float* v_cache, float* o, float* lse,
+                   void* workspace, size_t workspace_bytes, const wha_layout* cache_layout, float scale,
+                   void* stream) {
+  static const char* fn = "wha_decode_fwd";
+  wha::View V;
+  int rc = check_layout(cache_layout, &V, fn);
+  if (rc) return rc;
+  if ((rc = check_scale(scale, fn))) return rc;
+  if (!q || !k_cache || !v_cache || !o)
+    return fail(WHA_ERR_INVALID, "%s: q, k_cache, v_cache and o must be non-NULL", fn);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  if ((rc = resolve_workspace(workspace, workspace_bytes, wha_decode_workspace_size(cache_layout), s, fn,
+                              &ws)))
+    return rc;
+  const bool vec = vec_ok(V, {k_cache, v_cache});
+  hipError_t e = wha::launch_decode(q, k_cache, v_cache, o, lse, static_cast<float*>(ws), V, vec, scale, s);
+  if (e != hipSuccess) return hip_fail(e, "wha_decode_fwd launch");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+int wha_host_attention_core_fwd(const float* q, const float* k, const float* v, int32_t T, int32_t E,
+                                int32_t n_head, float* o) {
+  static const char* fn = "wha_host_attention_core_fwd";
+  wha::View V;
+  int rc = check_host_seq(fn, T, E, n_head, &V);
+  if (rc) return rc;
+  if (!q || !k || !v || !o) return fail(WHA_ERR_INVALID, "%s: q, k, v and o must be non-NULL", fn);
+  const size_t n = (size_t)T * E;
+  const size_t nb = round256(n * sizeof(float)) / sizeof(float);
+  float* base = nullptr;
+  hipStream_t s = nullptr;
+  if ((rc = host_stage(4 * nb * sizeof(float), &base, &s))) return rc;
+  float *dq = base, *dk = base + nb, *dv = base + 2 * nb, *dout = base + 3 * nb;
+  hipError_t e = hipSuccess;
+  const float* srcs[3] = {q, k, v};
+  float* dsts[3] = {dq, dk, dv};
+  for (int i = 0; i < 3 && e == hipSuccess; ++i)
+    e = hipMemcpyAsync(dsts[i], srcs[i], n * sizeof(float), hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync H2D");
+  const float scale = 1.0f / sqrtf((float)(E / n_head));  // src/common/compute.rs:362
+  e = wha::launch_attn_fwd(dq, dk, dv, dout, nullptr, V, vec_ok(V, {dq, dk, dv, dout}), scale, s);
+  if (e != hipSuccess) return hip_fail(e, "attention forward launch");
+  e = hipMemcpyAsync(o, dout, n * sizeof(float), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync D2H");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+int wha_host_attention_backward(const float* d_pre_proj, const float* q, const float* k, const float* v,
+                                const float* att, int32_t T, int32_t E, int32_t n_head, float* dq,
+                                float* dk, float* dv) {
+  static const char* fn = "wha_host_attention_backward";
+  wha::View V;
+  int rc = check_host_seq(fn, T, E, n_head, &V);
+  if (rc) return rc;
+  if (!d_pre_proj || !q || !k || !v || !att || !dq || !dk || !dv)
+    return fail(WHA_ERR_INVALID, "%s: every pointer must be non-NULL", fn);
+  const size_t n = (size_t)T * E;
+  const size_t nb = round256(n * sizeof(float)) / sizeof(float);
+  const size_t na = round256((size_t)n_head * T * T * sizeof(float)) / sizeof(float);
+  const size_t nd = round256((size_t)n_head * T * sizeof(float)) / sizeof(float);
+  float* base = nullptr;
+  hipStream_t s = nullptr;
+  if ((rc = host_stage((7 * nb + na + nd) * sizeof(float), &base, &s))) return rc;
+  float* d_do = base;
+  float* d_q = base + nb;
+  float* d_k = base + 2 * nb;
+  float* d_v = base + 3 * nb;
+  float* d_dq = base + 4 * nb;
+  float* d_dk = base + 5 * nb;
+  float* d_dv = base + 6 * nb;
+  float* d_att = base + 7 * nb;
+  float* d_delta = d_att + na;
+  hipError_t e = hipSuccess;
+  const float* srcs[4] = {d_pre_proj, q, k, v};
+  float* dsts[4] = {d_do, d_q, d_k, d_v};
+  for (int i = 0; i < 4 && e == hipSuccess; ++i)
+    e = hipMemcpyAsync(dsts[i], srcs[i], n * sizeof(float), hipMemcpyHostToDevice, s);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(d_att, att, (size_t)n_head * T * T * sizeof(float), hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync H2D");
+  const float scale = 1.0f / sqrtf((float)(E / n_head));  // src/cpu/backward.rs:326
+  e = wha::launch_attn_bwd_probs(d_do, d_q, d_k, d_v, d_att, d_dq, d_dk, d_dv, d_delta, V,
+                                 vec_ok(V, {d_do, d_q, d_k, d_v, d_dq, d_dk, d_dv}), scale, s);
+  if (e != hipSuccess) return hip_fail(e, "attention backward launch");
+  float* outs[3] = {dq, dk, dv};
+  const float* douts[3] = {d_dq, d_dk, d_dv};
+  for (int i = 0; i < 3 && e == hipSuccess; ++i)
+    e = hipMemcpyAsync(outs[i], douts[i], n * sizeof(float), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync D2H");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+int wha_timing_enable(int on) {
+  TimingState& st = timing();
+  std::lock_guard<std::mutex> lk(st.mu);
+  st.on = on != 0;
+  return WHA_OK;
+}
+
+int wha_timing_reset(void) {
+  TimingState& st = timing();
+  std::lock_guard<std::mutex> lk(st.mu);
+  int rc = drain_timing_locked(st);
+  st.totals.clear();
+  return rc;
+}
+
+int wha_timing_read(const char* kernel, double* total_ms, int64_t* launches) {
+  if (!kernel || !total_ms || !launches) return fail(WHA_ERR_INVALID, "wha_timing_read: NULL argument");
+  TimingState& st = timing();
+  std::lock_guard<std::mutex> lk(st.mu);
+  int rc = drain_timing_locked(st);
+  auto it = st.totals.find(kernel);
+  *total_ms = it == st.totals.end() ? 0.0 : it->second.first;
+  *launches = it == st.totals.end() ? 0 : it->second.second;
+  return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,139 @@
+// Device-side building blocks shared by the attention kernels (gfx950 only).
+//
+// MFMA operand layout used throughout (v_mfma_f32_16x16x4_f32, wave64):
+//   A (16x4):  lane l supplies A[m = l%16][k = l/16]
+//   B (4x16):  lane l supplies B[k = l/16][n = l%16]
+//   D (16x16): lane l holds    D[m = 4*(l/16) + i][n = l%16], i = 0..3
+// The contraction index k can be mapped to any physical index as long as A and
+// B agree.  For contractions over the head dimension, lane group g = l/16 owns
+// the d-range [g*DP/4, (g+1)*DP/4) and MFMA step s uses d = g*DP/4 + s, so a
+// lane reads its A operand for four consecutive steps with one 128-bit LDS
+// load.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wha {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.69314718055994531f;
+
+// Strided [B,H,T,D] view (unit stride on d), shared by every [T][D] tensor of a call.
+struct View {
+  int B, H, T, D;
+  int64_t sb, sh, st;
+};
+
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// exp2 on the transcendental unit (v_exp_f32).  Arguments here are <= 0
+// (scores minus a running max or minus the row LSE), so results lie in [0, 1];
+// results below 2^-126 flush to zero, which changes no sum at fp32 precision.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float xor_shfl(float x, int mask) { return __shfl_xor(x, mask, 64); }
+
+// Cooperative global -> register -> LDS staging of a ROWS x DP tile of one
+// (b,h) matrix, rows [row0, row0+ROWS), zero-filled past T and past D.
+// VEC: 128-bit global loads (requires D, all strides and the base 16-byte
+// aligned in floats, checked on the host); otherwise 32-bit loads.
+template <int DP, int ROWS, int NT, bool VEC>
+struct TileStage {
+  static constexpr int C4 = DP / 4;             // float4 per row
+  static constexpr int NF4 = ROWS * C4;         // float4 per tile
+  static constexpr int PER = (NF4 + NT - 1) / NT;
+  float4 r[PER];
+
+  __device__ __forceinline__ void load(const float* __restrict__ base, int row0, int T, int D,
+                                       int64_t st, int tid) {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int idx = tid + p * NT;
+      const int row = idx / C4;
+      const int c = (idx % C4) * 4;
+      float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
+      if ((NF4 % NT == 0 || idx < NF4) && row0 + row < T) {
+        const float* src = base + (int64_t)(row0 + row) * st + c;
+        if (VEC) {
+          if (c < D) val = *reinterpret_cast<const float4*>(src);
+        } else {
+          if (c + 0 < D) val.x = src[0];
+          if (c + 1 < D) val.y = src[1];
+          if (c + 2 < D) val.z = src[2];
+          if (c + 3 < D) val.w = src[3];
+        }
+      }
+      r[p] = val;
+    }
+  }
+
+  template <int LD>
+  __device__ __forceinline__ void store(float* lds, int tid) const {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int idx = tid + p * NT;
+      if (NF4 % NT == 0 || idx < NF4) {
+        const int row = idx / C4;
+        const int c = (idx % C4) * 4;
+        *reinterpret_cast<float4*>(lds + row * LD + c) = r[p];
+      }
+    }
+  }
+};
+
+// Per-lane operand fragment of one row: lane group g = lane/16 holds
+// x[row][g*DP/4 + s], s = 0 .. DP/4-1, multiplied by mul; zero past T and D.
+template <int DP, bool VEC>
+__device__ __forceinline__ void load_row_frag(const float* __restrict__ base, int row, int T, int D,
+                                              int64_t st, int g, float mul, float* frag) {
+  constexpr int DG = DP / 4;
+  const int c0 = g * DG;
+  if (row < T) {
+    const float* src = base + (int64_t)row * st + c0;
+    if (VEC) {
+#pragma unroll
+      for (int j = 0; j < DG / 4; ++j) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c0 + 4 * j < D) v = *reinterpret_cast<const float4*>(src + 4 * j);
+        frag[4 * j + 0] = v.x * mul;
+        frag[4 * j + 1] = v.y * mul;
+        frag[4 * j + 2] = v.z * mul;
+        frag[4 * j + 3] = v.w * mul;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < DG; ++s) frag[s] = (c0 + s < D) ? src[s] * mul : 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < DG; ++s) frag[s] = 0.f;
+  }
+}
+
+// Writes an accumulator laid out as X^T (d on MFMA rows, the row index of X on
+// MFMA columns): acc[dt][i] = X[row][16*dt + 4*g + i].  Scaled by mul.
+template <int DP, bool VEC>
+__device__ __forceinline__ void store_rowT(float* __restrict__ base, int row, int T, int D, int64_t st,
+                                           int g, const floatx4* acc, float mul) {
+  if (row >= T) return;
+  float* dst = base + (int64_t)row * st;
+#pragma unroll
+  for (int dt = 0; dt < DP / 16; ++dt) {
+    const int c = 16 * dt + 4 * g;
+    if (VEC) {
+      if (c < D)
+        *reinterpret_cast<float4*>(dst + c) =
+            make_float4(acc[dt][0] * mul, acc[dt][1] * mul, acc[dt][2] * mul, acc[dt][3] * mul);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (c + i < D) dst[c + i] = acc[dt][i] * mul;
+    }
+  }
+}
+
+}  // namespace wha

@@ -1,0 +1,50 @@
+// Host-side launch interface between the C ABI (wha_api.hip) and the kernel
+// translation units.  Each launcher validates nothing (wha_api.hip does), picks
+// the template instance for the padded head dimension and vector mode, and
+// enqueues on `stream`.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "wha_device.hpp"
+
+namespace wha {
+
+// Padded head dimension used by the kernels for a given D (0 = unsupported).
+inline int padded_dim(int D) {
+  if (D <= 0) return 0;
+  if (D <= 48) return 48;
+  if (D <= 64) return 64;
+  if (D <= 128) return 128;
+  return 0;
+}
+
+// Optional per-kernel HIP-event timing (implemented in wha_api.hip).
+struct TimingScope {
+  TimingScope(const char* name, hipStream_t stream);
+  ~TimingScope();
+  void* token;
+  hipStream_t stream;
+};
+
+hipError_t launch_attn_fwd(const float* q, const float* k, const float* v, float* o, float* lse,
+                           const View& L, bool vec, float scale, hipStream_t stream);
+
+// Fused backward: Delta pre-pass, dQ (query-stationary) and dK/dV
+// (key-stationary).  delta: [B*H*T] device scratch.
+hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const float* o,
+                           const float* d_o, const float* lse, float* dq, float* dk, float* dv,
+                           float* delta, const View& L, bool vec, float scale, hipStream_t stream);
+
+// Backward from given probabilities att [B][H][T][T].  delta: [B*H*T] scratch.
+hipError_t launch_attn_bwd_probs(const float* d_o, const float* q, const float* k, const float* v,
+                                 const float* att, float* dq, float* dk, float* dv, float* delta,
+                                 const View& L, bool vec, float scale, hipStream_t stream);
+
+// Split-K decode.  Workspace layout and size: decode_workspace_floats().
+size_t decode_workspace_floats(const View& cache);
+hipError_t launch_decode(const float* q, const float* kc, const float* vc, float* o, float* lse,
+                         float* ws, const View& cache, bool vec, float scale, hipStream_t stream);
+
+}  // namespace wha
