@@ -48,10 +48,11 @@ def credited_flops(B, H, T, D):
             "total": 12 * B * H * D * P}
 
 
-def cpu_baseline(cfg, seed=42, max_threads=None):
+def cpu_baseline(cfg, seed=42, max_threads=None, min_seconds=10.0):
     """Reference-order f32 oracle (test infrastructure, the CPU baseline only):
     forward core + backward from att, one thread per sequence as the reference's
-    training loop runs one thread per batch element."""
+    training loop runs one thread per batch element.  The sample (one sequence
+    per thread) is repeated until at least min_seconds of CPU work have run."""
     import numpy as np
     import oracle
     B, H, T, D = cfg["B"], cfg["H"], cfg["T"], cfg["D"]
@@ -60,14 +61,19 @@ def cpu_baseline(cfg, seed=42, max_threads=None):
     nseq = nthreads  # one sequence per thread: a bounded sample of the same workload
     q, k, v, do = oracle.synth_inputs(nseq, H, T, D, seed=seed)
     qs, ks, vs, dos = (oracle.bhtd_to_seq(a) for a in (q, k, v, do))
+    reps = 0
     t0 = time.perf_counter()
-    oracle.batch_fwd_bwd_f32_threaded(qs, ks, vs, dos, H, nthreads=nthreads)
-    dt = time.perf_counter() - t0
+    while True:
+        oracle.batch_fwd_bwd_f32_threaded(qs, ks, vs, dos, H, nthreads=nthreads)
+        reps += 1
+        if time.perf_counter() - t0 >= min_seconds:
+            break
+    dt = (time.perf_counter() - t0) / reps
     flops = credited_flops(nseq, H, T, D)["total"]
     return {"value": nseq * T / dt, "unit": "tokens/s", "cores": nthreads, "kind": "port",
             "sample": f"{nseq} of the {B} sequences ({nseq}x{T} tokens, {H} heads, D={D}), fwd+bwd, "
-                      f"one thread per sequence; host has {ncpu} cores",
-            "seconds": dt, "tflops": flops / dt / 1e12}
+                      f"one thread per sequence, repeated {reps}x; host has {ncpu} cores",
+            "seconds_per_rep": dt, "tflops": flops / dt / 1e12}
 
 
 def run_attention(args, cfg, pkg, torch):
@@ -201,6 +207,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="768", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="first run a plain device copy (y = 2*x, torch elementwise kernel) of this many "
+                         "MiB five times, as the known-size reference for rocprofv3 byte counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; the (b,h) units shard across GPUs with no "
@@ -214,6 +223,14 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     cfg = CONFIGS[args.config]
+    if args.copy_mb:
+        n = args.copy_mb * (1 << 20) // 4
+        x = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        y = torch.empty_like(x)
+        for _ in range(5):
+            torch.mul(x, 2.0, out=y)
+        torch.cuda.synchronize()
+        del x, y
     if args.config == "decode":
         res = run_decode(args, cfg, pkg, torch)
     else:

@@ -84,6 +84,14 @@ def lib():
         if not LIB_PATH.exists():
             raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
                                f"or `make -C {PKG_DIR}`; there is no fallback path")
+        # torch bundles its own HIP runtime under the same soname
+        # (libamdhip64.so.7).  Load it first so that this library binds to the
+        # runtime torch allocates with; loading /opt/rocm's copy first leaves
+        # torch unable to see the device.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = ctypes.CDLL(str(LIB_PATH))
         vp, f32p, lp = ctypes.c_void_p, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(WaveLayout)
         sz, i32 = ctypes.c_size_t, ctypes.c_int32
