@@ -84,11 +84,11 @@ def run_attention(args, cfg, pkg, torch):
     o = torch.empty_like(tq)
     lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
     dq, dk, dv = (torch.empty_like(tq) for _ in range(3))
-    ws = torch.empty(pkg.attn_bwd_workspace_bytes(pkg.layout_of(tq)) // 4, dtype=torch.float32, device=dev)
+    plan = pkg.AttnPlan(tq, tk, tv, o, lse, tdo, dq, dk, dv)  # pointers and layouts bound once
 
     def step():
-        pkg.attn_fwd(tq, tk, tv, out=o, lse=lse)
-        pkg.attn_bwd(tq, tk, tv, o, tdo, lse, workspace=ws, dq=dq, dk=dk, dv=dv)
+        plan.fwd()
+        plan.bwd()
 
     for _ in range(args.warmup):
         step()

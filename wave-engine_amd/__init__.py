@@ -252,6 +252,49 @@ def decode_fwd(q, k_cache, v_cache, scale=None, want_lse=False, workspace=None):
     return (o, lse) if want_lse else o
 
 
+class AttnPlan:
+    """Launches bound once to a fixed set of [B,H,T,D] tensors: layouts, pointers,
+    scale, workspace and stream are validated and marshalled at construction, so
+    fwd() and bwd() are one C call each (for training loops and benchmarks where
+    per-call Python checks would cost as much as the kernels)."""
+
+    def __init__(self, q, k, v, o, lse, do=None, dq=None, dk=None, dv=None, workspace=None, scale=None):
+        torch = _torch()
+        L = layout_of(q)
+        _same_layout(L, k, v, o)
+        if tuple(lse.shape) != (L.B, L.H, L.T) or not lse.is_contiguous():
+            raise ValueError("lse must be a contiguous [B,H,T] tensor")
+        self.layout = L
+        self._keep = [q, k, v, o, lse, do, dq, dk, dv, workspace]
+        s = ctypes.c_float(default_scale(L.D) if scale is None else float(scale))
+        st = _stream_ptr(q)
+        self._fwd_args = (_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), ctypes.byref(L), s, st)
+        self._bwd_args = None
+        if do is not None:
+            _same_layout(L, do, dq, dk, dv)
+            need = attn_bwd_workspace_bytes(L)
+            if workspace is None:
+                workspace = torch.empty(need // 4, dtype=torch.float32, device=q.device)
+                self._keep.append(workspace)
+            ws_bytes = workspace.numel() * workspace.element_size()
+            self._bwd_args = (_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse), _ptr(dq), _ptr(dk),
+                              _ptr(dv), _ptr(workspace), ctypes.c_size_t(ws_bytes), ctypes.byref(L), s, st)
+        self._f = lib().wha_attn_fwd
+        self._b = lib().wha_attn_bwd
+
+    def fwd(self):
+        rc = self._f(*self._fwd_args)
+        if rc:
+            _check("wha_attn_fwd", rc)
+
+    def bwd(self):
+        if self._bwd_args is None:
+            raise ValueError("this plan was built without backward tensors")
+        rc = self._b(*self._bwd_args)
+        if rc:
+            _check("wha_attn_bwd", rc)
+
+
 # ------------------------------------------------------------------ timing
 
 def timing_enable(on: bool = True):

@@ -163,14 +163,15 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
     }
 
     if (MODE != kDeltaFromProbs) {
-      // dQ^T[d][query] += K^T[d][key] dS^T[key][query]
+      // dQ^T[d][query] += K^T[d][key] dS^T[key][query]  (d = NDT*m + dt on MFMA rows)
 #pragma unroll
       for (int mt = 0; mt < NKT; ++mt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float* krow = &Ks[(16 * mt + 4 * g + i) * LD + lq];
+          float ka[NDT];
+          lds_read_vec<NDT>(&Ks[(16 * mt + 4 * g + i) * LD + NDT * lq], ka);
 #pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) dqacc[dt] = mfma4(krow[16 * dt], dp[mt][i], dqacc[dt]);
+          for (int dt = 0; dt < NDT; ++dt) dqacc[dt] = mfma4(ka[dt], dp[mt][i], dqacc[dt]);
         }
       }
     }
@@ -181,7 +182,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
     dsum += xor_shfl(dsum, 32);
     if (g == 0 && row_ok) Delta[rix] = dsum;
   } else {
-    store_rowT<DP, VEC>(dQ + base, qrow, L.T, L.D, L.st, g, dqacc, scale);
+    store_row_frag<DP, VEC>(dQ + base, qrow, L.T, L.D, L.st, g, dqacc, scale);
   }
 }
 
@@ -303,23 +304,25 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
     }
 
     // dV^T[d][key] += dO^T[d][query] P[query][key];  dK^T[d][key] += Q^T[d][query] dS[query][key]
+    // (d = NDT*m + dt on MFMA rows: one LDS read per operand row feeds all d-tiles)
 #pragma unroll
     for (int mt = 0; mt < NQT; ++mt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float* orow = &Os[(16 * mt + 4 * g + i) * LD + lq];
-        const float* qrow = &Qs[(16 * mt + 4 * g + i) * LD + lq];
+        float oa[NDT], qa[NDT];
+        lds_read_vec<NDT>(&Os[(16 * mt + 4 * g + i) * LD + NDT * lq], oa);
+        lds_read_vec<NDT>(&Qs[(16 * mt + 4 * g + i) * LD + NDT * lq], qa);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
-          dvacc[dt] = mfma4(orow[16 * dt], s[mt][i], dvacc[dt]);
-          dkacc[dt] = mfma4(qrow[16 * dt], dp[mt][i], dkacc[dt]);
+          dvacc[dt] = mfma4(oa[dt], s[mt][i], dvacc[dt]);
+          dkacc[dt] = mfma4(qa[dt], dp[mt][i], dkacc[dt]);
         }
       }
     }
   }
 
-  store_rowT<DP, VEC>(dK + base, krow, L.T, L.D, L.st, g, dkacc, scale);
-  store_rowT<DP, VEC>(dV + base, krow, L.T, L.D, L.st, g, dvacc, 1.f);
+  store_row_frag<DP, VEC>(dK + base, krow, L.T, L.D, L.st, g, dkacc, scale);
+  store_row_frag<DP, VEC>(dV + base, krow, L.T, L.D, L.st, g, dvacc, 1.f);
 }
 
 namespace {

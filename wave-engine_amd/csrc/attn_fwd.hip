@@ -36,7 +36,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
   constexpr int BN = 64;        // keys per tile
   constexpr int LD = DP + 4;    // LDS row pitch (floats): conflict-free b128 and b32 reads
   constexpr int DG = DP / 4;    // head-dim slice per lane group
-  constexpr int NDT = DP / 16;  // 16-row d tiles of O^T
+  constexpr int NDT = DP / 16;  // 16-row d tiles of O^T (row m of tile dt is d = NDT*m + dt)
   constexpr int NKT = BN / 16;  // 16-key sub-tiles of a tile
   __shared__ __align__(16) float Ks[BN * LD];
   __shared__ __align__(16) float Vs[BN * LD];
@@ -81,20 +81,24 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
     const int key0 = kt * BN;
     if (key0 > q0 + 15) continue;  // every key of the tile is after every query of the wave
 
-    // S^T[key][query] (already in log2 units)
+    // S^T[key][query] (already in log2 units); four independent accumulator chains
     floatx4 s[NKT];
 #pragma unroll
     for (int mt = 0; mt < NKT; ++mt) s[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < DG / 4; ++j) {
+      float4 a[NKT];
 #pragma unroll
-      for (int mt = 0; mt < NKT; ++mt) {
-        const float4 a = *reinterpret_cast<const float4*>(&Ks[(16 * mt + lq) * LD + g * DG + 4 * j]);
-        s[mt] = mfma4(a.x, qf[4 * j + 0], s[mt]);
-        s[mt] = mfma4(a.y, qf[4 * j + 1], s[mt]);
-        s[mt] = mfma4(a.z, qf[4 * j + 2], s[mt]);
-        s[mt] = mfma4(a.w, qf[4 * j + 3], s[mt]);
-      }
+      for (int mt = 0; mt < NKT; ++mt)
+        a[mt] = *reinterpret_cast<const float4*>(&Ks[(16 * mt + lq) * LD + g * DG + 4 * j]);
+#pragma unroll
+      for (int mt = 0; mt < NKT; ++mt) s[mt] = mfma4(a[mt].x, qf[4 * j + 0], s[mt]);
+#pragma unroll
+      for (int mt = 0; mt < NKT; ++mt) s[mt] = mfma4(a[mt].y, qf[4 * j + 1], s[mt]);
+#pragma unroll
+      for (int mt = 0; mt < NKT; ++mt) s[mt] = mfma4(a[mt].z, qf[4 * j + 2], s[mt]);
+#pragma unroll
+      for (int mt = 0; mt < NKT; ++mt) s[mt] = mfma4(a[mt].w, qf[4 * j + 3], s[mt]);
     }
 
     // causal / tail mask, running max (one query per lane; keys over 16 values
@@ -133,14 +137,16 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
 
-    // O^T[d][query] += V^T[d][key] P^T[key][query]; MFMA k-index g <-> key 16*mt + 4*g + i
+    // O^T[d][query] += V^T[d][key] P^T[key][query]; MFMA k-index g <-> key 16*mt + 4*g + i,
+    // MFMA row m of d-tile dt <-> d = NDT*m + dt (one LDS read feeds all d-tiles)
 #pragma unroll
     for (int mt = 0; mt < NKT; ++mt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float* vrow = &Vs[(16 * mt + 4 * g + i) * LD + lq];
+        float va[NDT];
+        lds_read_vec<NDT>(&Vs[(16 * mt + 4 * g + i) * LD + NDT * lq], va);
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma4(vrow[16 * dt], s[mt][i], oacc[dt]);
+        for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma4(va[dt], s[mt][i], oacc[dt]);
       }
     }
   }
@@ -152,7 +158,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
 #pragma unroll
     for (int i = 0; i < 4; ++i) oacc[dt][i] = oacc[dt][i] / l_sum;
   }
-  store_rowT<DP, VEC>(O + base, qrow, L.T, L.D, L.st, g, oacc, 1.f);
+  store_row_frag<DP, VEC>(O + base, qrow, L.T, L.D, L.st, g, oacc, 1.f);
   if (LSE != nullptr && g == 0 && qrow < L.T)
     LSE[(int64_t)bh * L.T + qrow] = (m_i + log2f(l_sum)) * kLn2;
 }

@@ -114,24 +114,53 @@ __device__ __forceinline__ void load_row_frag(const float* __restrict__ base, in
   }
 }
 
-// Writes an accumulator laid out as X^T (d on MFMA rows, the row index of X on
-// MFMA columns): acc[dt][i] = X[row][16*dt + 4*g + i].  Scaled by mul.
+// Reads N consecutive floats from LDS (128-bit reads when N is a multiple of 4
+// and the address is 16-byte aligned, which holds for every call site with
+// N = 4 or 8).
+template <int N>
+__device__ __forceinline__ void lds_read_vec(const float* p, float* out) {
+  if (N % 4 == 0) {
+#pragma unroll
+    for (int c = 0; c < N / 4; ++c) {
+      const float4 v = *reinterpret_cast<const float4*>(p + 4 * c);
+      out[4 * c + 0] = v.x;
+      out[4 * c + 1] = v.y;
+      out[4 * c + 2] = v.z;
+      out[4 * c + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < N; ++c) out[c] = p[c];
+  }
+}
+
+// Accumulators of a contraction X^T[d][r] += A^T[d][k] B[k][r] whose MFMA row m
+// of d-tile dt stands for d = NDT*m + dt (NDT = DP/16).  With that
+// permutation lane (lq, g) reads its A operands for all NDT d-tiles as NDT
+// consecutive floats A[k][NDT*lq ...], and holds X[r][NDT*(4g+i) + dt] in
+// acc[dt][i]: the contiguous d-range [g*DP/4, (g+1)*DP/4) of row r, the same
+// range load_row_frag gives that lane.  Writes it scaled by mul.
 template <int DP, bool VEC>
-__device__ __forceinline__ void store_rowT(float* __restrict__ base, int row, int T, int D, int64_t st,
-                                           int g, const floatx4* acc, float mul) {
+__device__ __forceinline__ void store_row_frag(float* __restrict__ base, int row, int T, int D, int64_t st,
+                                               int g, const floatx4* acc, float mul) {
+  constexpr int NDT = DP / 16;
   if (row >= T) return;
   float* dst = base + (int64_t)row * st;
 #pragma unroll
-  for (int dt = 0; dt < DP / 16; ++dt) {
-    const int c = 16 * dt + 4 * g;
-    if (VEC) {
-      if (c < D)
-        *reinterpret_cast<float4*>(dst + c) =
-            make_float4(acc[dt][0] * mul, acc[dt][1] * mul, acc[dt][2] * mul, acc[dt][3] * mul);
+  for (int i = 0; i < 4; ++i) {
+    const int c0 = NDT * (4 * g + i);
+    if (VEC && NDT % 4 == 0) {
+#pragma unroll
+      for (int c4 = 0; c4 < NDT / 4; ++c4) {
+        const int c = c0 + 4 * c4;
+        if (c < D)
+          *reinterpret_cast<float4*>(dst + c) = make_float4(acc[4 * c4 + 0][i] * mul, acc[4 * c4 + 1][i] * mul,
+                                                            acc[4 * c4 + 2][i] * mul, acc[4 * c4 + 3][i] * mul);
+      }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (c + i < D) dst[c + i] = acc[dt][i] * mul;
+      for (int dt = 0; dt < NDT; ++dt)
+        if (c0 + dt < D) dst[c0 + dt] = acc[dt][i] * mul;
     }
   }
 }
