@@ -142,15 +142,18 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
     }
 
     // P (recomputed or read), dS; lane element (mt,i) is key key0+16mt+4g+i of query qrow
+    // keys above key_lim are masked (and every key of a row past T): compare + select
+    const int key_lim = (row_ok ? min(qrow, L.T - 1) : -1) - key0;
 #pragma unroll
     for (int mt = 0; mt < NKT; ++mt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int key = key0 + 16 * mt + 4 * g + i;
-        const bool valid = key <= qrow && key < L.T && row_ok;
+        const bool valid = 16 * mt + 4 * g + i <= key_lim;
         float p;
         if (MODE == kFused) {
-          p = valid ? fast_exp2(s[mt][i] - lse2) : 0.f;
+          p = fast_exp2(s[mt][i] - lse2);
+          p = valid ? p : 0.f;
         } else {
           p = valid ? att_row[key] : 0.f;
         }
@@ -202,8 +205,8 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
   constexpr int NQT = BMQ / 16;
   __shared__ __align__(16) float Qs[BMQ * LD];
   __shared__ __align__(16) float Os[BMQ * LD];  // dO tile
-  __shared__ float lse_s[BMQ];
-  __shared__ float del_s[BMQ];
+  __shared__ __align__(16) float lse_s[BMQ];
+  __shared__ __align__(16) float del_s[BMQ];
 
   const int BH = L.B * L.H;
   const int bh = blockIdx.x % BH;
@@ -258,6 +261,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
     if (qt + 1 < n_qt) load_tile(qt + 1);
     const int qb = qt * BMQ;
     if (qb + BMQ - 1 < k0w) continue;  // every query of the tile precedes every key of the wave
+    const int q_end = krow < L.T ? L.T : 0;  // valid queries: krow <= q < q_end
 
     floatx4 s[NQT], dp[NQT];
 #pragma unroll
@@ -284,22 +288,28 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
       }
     }
 
-    // lane element (mt,i): query qb+16mt+4g+i, key krow
+    // lane element (mt,i): query qb+16mt+4g+i, key krow.  The row statistics of
+    // the four queries 16mt+4g+0..3 come in one 128-bit LDS broadcast read; masking
+    // is a select, so no branch sits between the MFMA blocks.
 #pragma unroll
     for (int mt = 0; mt < NQT; ++mt) {
+      const float4 l4 = *reinterpret_cast<const float4*>(&lse_s[16 * mt + 4 * g]);
+      const float4 d4 = *reinterpret_cast<const float4*>(&del_s[16 * mt + 4 * g]);
+      const float lq4[4] = {l4.x, l4.y, l4.z, l4.w};
+      const float dq4[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int qi = 16 * mt + 4 * g + i;
-        const int q = qb + qi;
-        const bool valid = krow <= q && q < L.T && krow < L.T;
+        const int q = qb + 16 * mt + 4 * g + i;
+        const bool valid = (q >= krow) & (q < q_end);
         float p;
         if (!PROBS) {
-          p = valid ? fast_exp2(s[mt][i] - lse_s[qi]) : 0.f;
+          p = fast_exp2(s[mt][i] - lq4[i]);
+          p = valid ? p : 0.f;
         } else {
           p = valid ? ATT[(rbase + q) * L.T + krow] : 0.f;
         }
         s[mt][i] = p;
-        dp[mt][i] = p * (dp[mt][i] - del_s[qi]);
+        dp[mt][i] = p * (dp[mt][i] - dq4[i]);
       }
     }
 

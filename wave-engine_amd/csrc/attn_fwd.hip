@@ -103,17 +103,14 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
 
     // causal / tail mask, running max (one query per lane; keys over 16 values
     // in the lane and the 4 lane groups)
-    const bool need_mask = (key0 + BN - 1 > q0) || (key0 + BN > L.T);
+    // keys above key_lim are masked: one compare and a select per score, no branch
+    const int key_lim = min(qrow, L.T - 1) - key0;
     float mx = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < NKT; ++mt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float x = s[mt][i];
-        if (need_mask) {
-          const int key = key0 + 16 * mt + 4 * g + i;
-          if (key > qrow || key >= L.T) x = -INFINITY;
-        }
+        const float x = (16 * mt + 4 * g + i > key_lim) ? -INFINITY : s[mt][i];
         s[mt][i] = x;
         mx = fmaxf(mx, x);
       }

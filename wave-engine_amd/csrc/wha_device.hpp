@@ -50,6 +50,19 @@ struct TileStage {
 
   __device__ __forceinline__ void load(const float* __restrict__ base, int row0, int T, int D,
                                        int64_t st, int tid) {
+    if (VEC && row0 + ROWS <= T && D == DP) {
+      // whole tile in bounds (block-uniform): unpredicated 128-bit loads
+#pragma unroll
+      for (int p = 0; p < PER; ++p) {
+        const int idx = tid + p * NT;
+        if (NF4 % NT == 0 || idx < NF4) {
+          const int row = idx / C4;
+          const int c = (idx % C4) * 4;
+          r[p] = *reinterpret_cast<const float4*>(base + (int64_t)(row0 + row) * st + c);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int p = 0; p < PER; ++p) {
       const int idx = tid + p * NT;
