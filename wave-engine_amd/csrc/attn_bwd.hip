@@ -14,6 +14,14 @@
 //   attn_bwd_delta_kernel  Delta_t = dO_t . O_t                 (fused path)
 //   attn_bwd_dq_kernel     query-stationary: recompute P, dP, dS; dQ += dS K
 //   attn_bwd_dkv_kernel    key-stationary:   recompute P, dP, dS; dV += P^T dO, dK += dS^T Q
+// Default fused path: the key-stationary kernel also writes its dS tiles (fp32)
+// to the workspace, and attn_bwd_dq_ds_kernel forms dQ = scale * dS K with one
+// MFMA contraction per tile instead of recomputing S and dP (the reference's
+// wgpu tier likewise hands d_score from one kernel to the other through a
+// scratch buffer, src/wgpu_tier/dispatch_backward.rs:367).  dS buffer layout
+// per (b,h): column block kt (keys 64kt..64kt+63) holds rows q = 64kt..T-1,
+// 64 floats each, blocks back to back (ds_block_row below).  When that buffer
+// would be too large, attn_bwd_dq_kernel recomputes S and dP instead.
 // The "from probabilities" variants read P from the caller's att tensor instead
 // of recomputing it (the reference contract, att used as given), and obtain
 // Delta from att and dP (mode kDeltaFromProbs) because O is not an input there.
@@ -29,6 +37,13 @@
 namespace wha {
 
 enum DqMode { kFused = 0, kProbs = 1, kDeltaFromProbs = 2 };
+
+// First row of dS column block kt: sum_{j<kt} (T - 64 j).
+__host__ __device__ __forceinline__ int64_t ds_block_row(int kt, int T) {
+  return (int64_t)kt * T - (int64_t)32 * kt * (kt - 1);
+}
+// Rows of dS per (b,h).
+__host__ __device__ __forceinline__ int64_t ds_rows(int T) { return ds_block_row((T + 63) / 64, T); }
 
 // Delta_t = sum_d dO[t][d] * O[t][d]; 16 lanes per row, 16 rows per block.
 __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const float* __restrict__ O,
@@ -189,13 +204,14 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
   }
 }
 
-// Key-stationary kernel: dK and dV for NW*16 consecutive keys of one (b,h).
-template <int DP, int NW, bool VEC, bool PROBS>
+// Key-stationary kernel: dK and dV for NW*16 consecutive keys of one (b,h);
+// with DS_OUT also writes the dS tiles it forms to DS (layout: ds_block_row).
+template <int DP, int NW, bool VEC, bool PROBS, bool DS_OUT>
 __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Delta,
-    const float* __restrict__ ATT, float* __restrict__ dK, float* __restrict__ dV, View L,
-    float scale, float scale_log2) {
+    const float* __restrict__ ATT, float* __restrict__ dK, float* __restrict__ dV,
+    float* __restrict__ DS, View L, float scale, float scale_log2) {
   constexpr int NT = NW * 64;
   constexpr int BNK = NW * 16;  // keys per block
   constexpr int BMQ = 64;       // queries per tile
@@ -203,6 +219,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
   constexpr int DG = DP / 4;
   constexpr int NDT = DP / 16;
   constexpr int NQT = BMQ / 16;
+  static_assert(!DS_OUT || BNK == 64, "a dS column block is 64 keys wide");
   __shared__ __align__(16) float Qs[BMQ * LD];
   __shared__ __align__(16) float Os[BMQ * LD];  // dO tile
   __shared__ __align__(16) float lse_s[BMQ];
@@ -313,6 +330,20 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
       }
     }
 
+    if (DS_OUT) {
+      // dS[q][64kt + 16*wave + lq] for this lane's 16 queries
+      float* dsb = DS + ((int64_t)bh * ds_rows(L.T) + ds_block_row(kt, L.T) - (int64_t)64 * kt) * 64 +
+                   wave * 16 + lq;
+#pragma unroll
+      for (int mt = 0; mt < NQT; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int q = qb + 16 * mt + 4 * g + i;
+          if (q < L.T) dsb[(int64_t)q * 64] = dp[mt][i];
+        }
+      }
+    }
+
     // dV^T[d][key] += dO^T[d][query] P[query][key];  dK^T[d][key] += Q^T[d][query] dS[query][key]
     // (d = NDT*m + dt on MFMA rows: one LDS read per operand row feeds all d-tiles)
 #pragma unroll
@@ -335,15 +366,93 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
   store_row_frag<DP, VEC>(dV + base, krow, L.T, L.D, L.st, g, dvacc, 1.f);
 }
 
+// Query-stationary dQ from stored dS: dQ^T[d][q] += K^T[d][key] dS^T[key][q] over
+// the causal 64-key tiles; K tiles staged through LDS (A operand, d = NDT*m + dt
+// on MFMA rows), dS read from the workspace with 128-bit loads straight into the
+// B operand (k-step (c, e) <-> key 16c + 4g + e), one tile ahead.
+template <int DP, int NW, bool VEC>
+__global__ __launch_bounds__(NW * 64) void attn_bwd_dq_ds_kernel(const float* __restrict__ K,
+                                                                 const float* __restrict__ DS,
+                                                                 float* __restrict__ dQ, View L, float scale) {
+  constexpr int NT = NW * 64;
+  constexpr int BM = NW * 16;
+  constexpr int BN = 64;
+  constexpr int LD = DP + 4;
+  constexpr int NDT = DP / 16;
+  __shared__ __align__(16) float Ks[BN * LD];
+
+  const int BH = L.B * L.H;
+  const int n_qt = (L.T + BM - 1) / BM;
+  const int bh = blockIdx.x % BH;
+  const int qt = n_qt - 1 - (int)(blockIdx.x / BH);
+  const int b = bh / L.H, h = bh % L.H;
+  const int64_t base = (int64_t)b * L.sb + (int64_t)h * L.sh;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 15, g = lane >> 4;
+  const int q0 = qt * BM + wave * 16;
+  const int qrow = q0 + lq;
+  const bool row_ok = qrow < L.T;
+
+  const float* dsh = DS + (int64_t)bh * ds_rows(L.T) * 64;
+  auto load_ds = [&](int kt, float4* dsv) {
+    const float* src = dsh + (ds_block_row(kt, L.T) + qrow - 64 * kt) * 64 + 4 * g;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      dsv[c] = row_ok ? *reinterpret_cast<const float4*>(src + 16 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+
+  const int q_hi = min(L.T, (qt + 1) * BM);
+  const int n_kt = (q_hi + BN - 1) / BN;
+
+  TileStage<DP, BN, NT, VEC> ks;
+  ks.load(K + base, 0, L.T, L.D, L.st, tid);
+  float4 dcur[4], dnext[4];
+  load_ds(0, dcur);
+
+  floatx4 acc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kt = 0; kt < n_kt; ++kt) {
+    __syncthreads();
+    ks.template store<LD>(Ks, tid);
+    __syncthreads();
+    if (kt + 1 < n_kt) {
+      ks.load(K + base, (kt + 1) * BN, L.T, L.D, L.st, tid);
+      load_ds(kt + 1, dnext);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (kt * BN + 16 * c <= q0 + 15) {  // else the chunk is after every query of the wave (dS = 0)
+        const float de[4] = {dcur[c].x, dcur[c].y, dcur[c].z, dcur[c].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float ka[NDT];
+          lds_read_vec<NDT>(&Ks[(16 * c + 4 * g + e) * LD + NDT * lq], ka);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma4(ka[dt], de[e], acc[dt]);
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) dcur[c] = dnext[c];
+  }
+  store_row_frag<DP, VEC>(dQ + base, qrow, L.T, L.D, L.st, g, acc, scale);
+}
+
 namespace {
 
 template <int DP, bool VEC>
 hipError_t bwd_fused_t(const float* q, const float* k, const float* v, const float* o,
                        const float* d_o, const float* lse, float* dq, float* dk, float* dv,
-                       float* delta, const View& L, float scale, hipStream_t stream) {
+                       float* delta, float* ds, const View& L, float scale, hipStream_t stream) {
   constexpr int NWQ = 4, NWK = 4;
   const float sl2 = (float)((double)scale * 1.4426950408889634);
   const int64_t rows = (int64_t)L.B * L.H * L.T;
+  const int n_qt = (L.T + NWQ * 16 - 1) / (NWQ * 16);
+  const int n_kt = (L.T + NWK * 16 - 1) / (NWK * 16);
   {
     TimingScope ts("attn_bwd_delta", stream);
     hipLaunchKernelGGL(attn_bwd_delta_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, stream,
@@ -351,8 +460,21 @@ hipError_t bwd_fused_t(const float* q, const float* k, const float* v, const flo
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (ds != nullptr) {
+    {
+      TimingScope ts("attn_bwd_dkv", stream);
+      hipLaunchKernelGGL((attn_bwd_dkv_kernel<DP, NWK, VEC, false, true>), dim3((unsigned)(n_kt * L.B * L.H)),
+                         dim3(NWK * 64), 0, stream, q, k, v, d_o, lse, (const float*)delta,
+                         (const float*)nullptr, dk, dv, ds, L, scale, sl2);
+    }
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    TimingScope ts("attn_bwd_dq", stream);
+    hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<DP, NWQ, VEC>), dim3((unsigned)(n_qt * L.B * L.H)),
+                       dim3(NWQ * 64), 0, stream, k, (const float*)ds, dq, L, scale);
+    return hipGetLastError();
+  }
   {
-    const int n_qt = (L.T + NWQ * 16 - 1) / (NWQ * 16);
     TimingScope ts("attn_bwd_dq", stream);
     hipLaunchKernelGGL((attn_bwd_dq_kernel<DP, NWQ, VEC, kFused>), dim3((unsigned)(n_qt * L.B * L.H)),
                        dim3(NWQ * 64), 0, stream, q, k, v, d_o, lse, delta, (const float*)nullptr, dq, L,
@@ -361,11 +483,10 @@ hipError_t bwd_fused_t(const float* q, const float* k, const float* v, const flo
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   {
-    const int n_kt = (L.T + NWK * 16 - 1) / (NWK * 16);
     TimingScope ts("attn_bwd_dkv", stream);
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<DP, NWK, VEC, false>), dim3((unsigned)(n_kt * L.B * L.H)),
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<DP, NWK, VEC, false, false>), dim3((unsigned)(n_kt * L.B * L.H)),
                        dim3(NWK * 64), 0, stream, q, k, v, d_o, lse, (const float*)delta,
-                       (const float*)nullptr, dk, dv, L, scale, sl2);
+                       (const float*)nullptr, dk, dv, (float*)nullptr, L, scale, sl2);
   }
   return hipGetLastError();
 }
@@ -395,21 +516,24 @@ hipError_t bwd_probs_t(const float* d_o, const float* q, const float* k, const f
   if (e != hipSuccess) return e;
   {
     TimingScope ts("attn_bwd_probs_dkv", stream);
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<DP, NWK, VEC, true>), dim3((unsigned)(n_kt * L.B * L.H)),
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<DP, NWK, VEC, true, false>), dim3((unsigned)(n_kt * L.B * L.H)),
                        dim3(NWK * 64), 0, stream, q, k, v, d_o, (const float*)nullptr,
-                       (const float*)delta, att, dk, dv, L, scale, 0.f);
+                       (const float*)delta, att, dk, dv, (float*)nullptr, L, scale, 0.f);
   }
   return hipGetLastError();
 }
 
 }  // namespace
 
+size_t bwd_ds_floats(const View& L) { return (size_t)L.B * L.H * (size_t)ds_rows(L.T) * 64; }
+
 hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const float* o,
                            const float* d_o, const float* lse, float* dq, float* dk, float* dv,
-                           float* delta, const View& L, bool vec, float scale, hipStream_t stream) {
-#define WHA_BWD(DP)                                                                         \
-  return vec ? bwd_fused_t<DP, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, L, scale, stream) \
-             : bwd_fused_t<DP, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, L, scale, stream)
+                           float* delta, float* ds, const View& L, bool vec, float scale,
+                           hipStream_t stream) {
+#define WHA_BWD(DP)                                                                                 \
+  return vec ? bwd_fused_t<DP, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream) \
+             : bwd_fused_t<DP, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream)
   switch (padded_dim(L.D)) {
     case 48: WHA_BWD(48);
     case 64: WHA_BWD(64);

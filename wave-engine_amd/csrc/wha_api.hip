@@ -279,9 +279,23 @@ int wha_attn_fwd(const float* q, const float* k, const float* v, float* o, float
   return WHA_OK;
 }
 
+// Largest dS buffer the fused backward materialises; beyond it (very long
+// sequences) the dQ kernel recomputes S and dP instead.
+static constexpr size_t kMaxDsBytes = (size_t)8 << 30;
+
+static size_t delta_bytes(const wha_layout* layout) {
+  return round256((size_t)layout->B * layout->H * layout->T * sizeof(float));
+}
+
+static size_t ds_bytes(const wha_layout* layout) {
+  wha::View V{layout->B, layout->H, layout->T, layout->D, 0, 0, 0};
+  const size_t n = wha::bwd_ds_floats(V) * sizeof(float);
+  return n <= kMaxDsBytes ? round256(n) : 0;
+}
+
 size_t wha_attn_bwd_workspace_size(const wha_layout* layout) {
   if (!layout || layout->B <= 0 || layout->H <= 0 || layout->T <= 0) return 0;
-  return round256((size_t)layout->B * layout->H * layout->T * sizeof(float));
+  return delta_bytes(layout) + ds_bytes(layout);
 }
 
 int wha_attn_bwd(const float* q, const float* k, const float* v, const float* o, const float* d_o,
@@ -299,15 +313,18 @@ int wha_attn_bwd(const float* q, const float* k, const float* v, const float* o,
   if ((rc = resolve_workspace(workspace, workspace_bytes, wha_attn_bwd_workspace_size(layout), s, fn, &ws)))
     return rc;
   const bool vec = vec_ok(V, {q, k, v, o, d_o, dq, dk, dv});
-  hipError_t e = wha::launch_attn_bwd(q, k, v, o, d_o, lse, dq, dk, dv, static_cast<float*>(ws), V, vec,
-                                      scale, s);
+  float* delta = static_cast<float*>(ws);
+  const size_t dsb = ds_bytes(layout);
+  float* ds = dsb ? reinterpret_cast<float*>(static_cast<char*>(ws) + delta_bytes(layout)) : nullptr;
+  hipError_t e = wha::launch_attn_bwd(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, V, vec, scale, s);
   if (e != hipSuccess) return hip_fail(e, "wha_attn_bwd launch");
   g_err[0] = 0;
   return WHA_OK;
 }
 
 size_t wha_attn_bwd_from_probs_workspace_size(const wha_layout* layout) {
-  return wha_attn_bwd_workspace_size(layout);
+  if (!layout || layout->B <= 0 || layout->H <= 0 || layout->T <= 0) return 0;
+  return delta_bytes(layout);
 }
 
 int wha_attn_bwd_from_probs(const float* d_pre_proj, const float* q, const float* k, const float* v,

@@ -31,11 +31,18 @@ struct TimingScope {
 hipError_t launch_attn_fwd(const float* q, const float* k, const float* v, float* o, float* lse,
                            const View& L, bool vec, float scale, hipStream_t stream);
 
-// Fused backward: Delta pre-pass, dQ (query-stationary) and dK/dV
-// (key-stationary).  delta: [B*H*T] device scratch.
+// Floats of the dS buffer the fused backward uses (the causal half of the
+// score matrix in 64-key column blocks, fp32).
+size_t bwd_ds_floats(const View& L);
+
+// Fused backward: Delta pre-pass, then either (ds != nullptr) the key-stationary
+// dK/dV kernel writing dS to ds and a query-stationary dQ = dS K kernel, or
+// (ds == nullptr) a query-stationary dQ kernel that recomputes S and dP and the
+// key-stationary dK/dV kernel.  Both deterministic.  delta: [B*H*T] scratch.
 hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const float* o,
                            const float* d_o, const float* lse, float* dq, float* dk, float* dv,
-                           float* delta, const View& L, bool vec, float scale, hipStream_t stream);
+                           float* delta, float* ds, const View& L, bool vec, float scale,
+                           hipStream_t stream);
 
 // Backward from given probabilities att [B][H][T][T].  delta: [B*H*T] scratch.
 hipError_t launch_attn_bwd_probs(const float* d_o, const float* q, const float* k, const float* v,
