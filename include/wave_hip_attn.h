@@ -116,6 +116,35 @@ int wha_decode_fwd(const float* q, const float* k_cache, const float* v_cache,
                    float* o, float* lse, void* workspace, size_t workspace_bytes,
                    const wha_layout* cache_layout, float scale, void* stream);
 
+/* ---------------------------------------------------------------- projections
+ * The c_attn / c_proj linears around the core (fp32 MFMA GEMM).  A batch of M
+ * rows is one call; rows of x / y / dy / dx have the given strides (floats),
+ * w is [N][K] row-major ([out_dim][in_dim], LinearWeights src/common/model.rs:175-180). */
+
+/* y[m][n] = b[n] + sum_k w[n][k] x[m][k]  (b may be NULL: no bias).
+ * ComputeBackend::linear_batch / linear_no_bias_batch (src/common/compute.rs:56-61,
+ * :441-468); one row is linear (src/common/model.rs:144-151). */
+int wha_linear_fwd(const float* x, int64_t ldx, const float* w, const float* b,
+                   float* y, int64_t ldy, int64_t M, int32_t N, int32_t K,
+                   void* stream);
+
+/* dx[m][k] = sum_n dy[m][n] w[n][k].  ComputeBackend::linear_backward_dx_batch
+ * (src/common/compute.rs:150, linear_backward_dx_only src/common/math/backward.rs:36-46). */
+int wha_linear_bwd_dx(const float* dy, int64_t lddy, const float* w, float* dx,
+                      int64_t lddx, int64_t M, int32_t N, int32_t K,
+                      void* stream);
+
+/* Bytes of device workspace wha_linear_bwd_dw needs. */
+size_t wha_linear_bwd_dw_workspace_size(int64_t M, int32_t N, int32_t K);
+
+/* dw[n][k] = sum_m dy[m][n] x[m][k] and, when db != NULL, db[n] = sum_m dy[m][n]
+ * (overwritten, summed in a fixed order).  ComputeBackend::outer_product_accum
+ * (src/common/compute.rs:153-161, :263-282) with compute_bias = (db != NULL).
+ * workspace may be NULL (library-cached, as for wha_attn_bwd). */
+int wha_linear_bwd_dw(const float* dy, int64_t lddy, const float* x, int64_t ldx,
+                      float* dw, float* db, int64_t M, int32_t N, int32_t K,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------- host API
  * One sequence in the reference's layout: q, k, v, o, d_pre_proj, dq, dk, dv
  * are [T][E] row-major host arrays (E = n_head * head_dim), att is
@@ -126,6 +155,15 @@ int wha_decode_fwd(const float* q, const float* k_cache, const float* v_cache,
  * attention of q,k,v (the c_attn/c_proj linears around it are not included). */
 int wha_host_attention_core_fwd(const float* q, const float* k, const float* v,
                                 int32_t T, int32_t E, int32_t n_head, float* o);
+
+/* ComputeBackend::attention (src/common/compute.rs:42-43) = attention_cpu
+ * (:357-414) end to end: qkv = c_attn(x) (:368-375), causal attention core,
+ * out = c_proj(o) (:411-413).  x, out: [T][E]; c_attn_w [3E][E], c_attn_b [3E],
+ * c_proj_w [E][E], c_proj_b [E] (AttentionWeights, src/common/model.rs:189-195). */
+int wha_host_attention(const float* x, const float* c_attn_w,
+                       const float* c_attn_b, const float* c_proj_w,
+                       const float* c_proj_b, int32_t T, int32_t E,
+                       int32_t n_head, float* out);
 
 /* ComputeBackend::attention_backward (src/common/compute.rs:163-173) with
  * CpuBackend's semantics (:286-314): att used as given. */

@@ -12,13 +12,18 @@ into ``liboracle.so``): a reference-order f32 restatement of
 * ``CpuBackend::attention_backward``, ``src/common/compute.rs:286-314``
 * ``attention_backward_single``, ``src/cpu/backward.rs:313-363``
 * ``Rng::next_u64`` / ``next_f32``, ``src/common/rng.rs:24-34``
+* the projections: ``linear_batch_cpu`` (``src/common/compute.rs:441-468``),
+  ``linear_backward_dx_only`` (``src/common/math/backward.rs:36-46``),
+  ``outer_product_accum`` (``src/common/compute.rs:263-282``) and ``attention_cpu``
+  end to end (``:357-414``)
 
 plus an f64 twin of the same loops (ground truth).  This module only moves
 numpy arrays in and out of it, converting between the device layout
 ``[B, H, T, D]`` and the reference's per-sequence ``[T][H*D]`` layout.
 
-Pins (each in ``tests/``): the reference's softmax-backward and
-value-aggregation known-answer tests (``src/common/math/attn_backward.rs:352-379``),
+Pins (each in ``tests/``): the reference's softmax-backward,
+value-aggregation and out-projection-backward known-answer tests
+(``src/common/math/attn_backward.rs:336-379``),
 closed forms (T=1, Q=0, constant V, equal K rows), invariants (row sums,
 sum of dK over keys, causality, linearity in V), an independent matrix-form
 numpy restatement in f64, and a central finite-difference check of the
@@ -74,6 +79,18 @@ def lib():
             f.restype = None
             f = getattr(L, f"wao_value_backward_row_{sfx}")
             f.argtypes = [p, p, p, ctypes.c_long, p, ctypes.c_int, ctypes.c_int, p]
+            f.restype = None
+            f = getattr(L, f"wao_linear_{sfx}")
+            f.argtypes = [p, p, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, p]
+            f.restype = None
+            f = getattr(L, f"wao_linear_backward_dx_{sfx}")
+            f.argtypes = [p, p, ctypes.c_int, ctypes.c_int, ctypes.c_int, p]
+            f.restype = None
+            f = getattr(L, f"wao_outer_product_accum_{sfx}")
+            f.argtypes = [p, p, ctypes.c_int, ctypes.c_int, ctypes.c_int, p, vp]
+            f.restype = None
+            f = getattr(L, f"wao_attention_full_{sfx}")
+            f.argtypes = [p, p, p, p, p, ctypes.c_int, ctypes.c_int, ctypes.c_int, p]
             f.restype = None
             f = getattr(L, f"wao_decode_{sfx}")
             f.argtypes = [p, p, p, ctypes.c_int, ctypes.c_int, ctypes.c_int, p, vp]
@@ -211,6 +228,54 @@ def decode_one(q, k, v, n_head: int, precision: str = "f32", want_lse=False):
     getattr(lib(), f"wao_decode_{precision}")(q, k, v, Tk, E, n_head, out,
                                               lse.ctypes.data if lse is not None else None)
     return (out, lse) if want_lse else out
+
+
+# ---------------------------------------------------------------- projections
+
+def linear(x, w, b=None, precision: str = "f32"):
+    """linear_batch_cpu: y[m] = b + W x[m] for the rows of x [M][K]; w [N][K]."""
+    dt = _dt(precision)
+    x, w = _c(x, dt), _c(w, dt)
+    M, K = x.shape
+    N = w.shape[0]
+    y = np.empty((M, N), dtype=dt)
+    bb = _c(b, dt) if b is not None else None
+    getattr(lib(), f"wao_linear_{precision}")(x, w, bb.ctypes.data if bb is not None else None, M, N, K, y)
+    return y
+
+
+def linear_backward_dx(dy, w, precision: str = "f32"):
+    """linear_backward_dx_only per row: dx[m] = W^T dy[m]."""
+    dt = _dt(precision)
+    dy, w = _c(dy, dt), _c(w, dt)
+    M, N = dy.shape
+    K = w.shape[1]
+    dx = np.empty((M, K), dtype=dt)
+    getattr(lib(), f"wao_linear_backward_dx_{precision}")(dy, w, M, N, K, dx)
+    return dx
+
+
+def outer_product_accum(dy, x, compute_bias: bool, precision: str = "f32"):
+    """CpuBackend::outer_product_accum: (d_w [N][K], d_b [N])."""
+    dt = _dt(precision)
+    dy, x = _c(dy, dt), _c(x, dt)
+    M, N = dy.shape
+    K = x.shape[1]
+    dw = np.empty((N, K), dtype=dt)
+    db = np.zeros(N, dtype=dt)
+    getattr(lib(), f"wao_outer_product_accum_{precision}")(dy, x, M, N, K, dw,
+                                                          db.ctypes.data if compute_bias else None)
+    return dw, db
+
+
+def attention_full(x, wa, ba, wp, bp, n_head: int, precision: str = "f32"):
+    """attention_cpu end to end (c_attn, core, c_proj) on one sequence x [T][E]."""
+    dt = _dt(precision)
+    x, wa, ba, wp, bp = (_c(a, dt) for a in (x, wa, ba, wp, bp))
+    T, E = x.shape
+    out = np.empty((T, E), dtype=dt)
+    getattr(lib(), f"wao_attention_full_{precision}")(x, wa, ba, wp, bp, T, E, n_head, out)
+    return out
 
 
 # ---------------------------------------------------------------- batched [B,H,T,D]

@@ -18,6 +18,8 @@ extern "C" {
 void wao_fill_normal(uint64_t* state, float* out, size_t n, double stddev);
 void wao_attention_core_fwd_f32(const float* q, const float* k, const float* v, int T, int E, int H,
                                 float* out, float* att_out, float* lse_out);
+void wao_attention_full_f32(const float* x, const float* wa, const float* ba, const float* wp, const float* bp,
+                            int T, int E, int H, float* out);
 void wao_attention_backward_f32(const float* d_pre_proj, const float* q, const float* k, const float* v,
                                 const float* att, int T, int E, int H, float* dq, float* dk, float* dv);
 }
@@ -165,6 +167,27 @@ void test_attention_core_matches_cpu() {
   }
 }
 
+void test_attention_with_projections() {
+  // ComputeBackend::attention(weights, x): c_attn, core, c_proj (src/common/compute.rs:357-414)
+  for (auto cfg : {std::vector<size_t>{64, 168, 4}, std::vector<size_t>{150, 768, 12}}) {
+    const size_t T = cfg[0], E = cfg[1], H = cfg[2];
+    uint64_t st = 1234 + T;
+    auto draw = [&](size_t n, double sd) {
+      std::vector<float> v(n);
+      wao_fill_normal(&st, v.data(), n, sd);
+      return v;
+    };
+    const auto x = draw(T * E, 1.0), wa = draw(3 * E * E, 1.0 / std::sqrt((double)E)), ba = draw(3 * E, 0.1);
+    const auto wp = draw(E * E, 1.0 / std::sqrt((double)E)), bp = draw(E, 0.1);
+    wave_hip::AttentionWeights w{{rows_of(wa, 3 * E, E), ba}, {rows_of(wp, E, E), bp}, H};
+    wave_hip::HipBackend be;
+    Rows out = be.attention(w, rows_of(x, T, E));
+    std::vector<float> ref(T * E);
+    wao_attention_full_f32(x.data(), wa.data(), ba.data(), wp.data(), bp.data(), (int)T, (int)E, (int)H, ref.data());
+    assert_parity(flat_of(out), ref, "attention out");
+  }
+}
+
 void test_bad_head_count_panics() {
   wave_hip::HipBackend be;
   Rows x(4, std::vector<float>(10, 0.f));
@@ -214,6 +237,7 @@ int main() {
   run("attention_backward_384_dim", test_attention_backward_384_dim);
   run("attention_backward_768_dim", test_attention_backward_768_dim);
   run("attention_core_matches_cpu", test_attention_core_matches_cpu);
+  run("attention_with_projections", test_attention_with_projections);
   run("bad_head_count_panics", test_bad_head_count_panics);
   run("concurrent_callers", test_concurrent_callers);
   std::printf("test result: %s. %d failed\n", g_failures ? "FAILED" : "ok", g_failures);

@@ -11,7 +11,8 @@ raise.
 Two levels mirror the reference interface:
 
 * ``HipBackend`` -- the two attention methods of wave-engine's
-  ``ComputeBackend`` trait (``src/common/compute.rs:42-43``, ``:163-173``) with the
+  ``ComputeBackend`` trait (``src/common/compute.rs:42-43``, ``:163-173``), projections
+  included, with the
   reference's per-sequence ``[T][n_embd]`` layout and host arrays, raising
   ``RuntimeError`` where the reference panics.
 * ``attn_fwd`` / ``attn_bwd`` / ``attn_bwd_from_probs`` / ``decode_fwd`` -- batched
@@ -39,7 +40,8 @@ EXPORTED_SYMBOLS = (
     "wha_attn_fwd", "wha_attn_bwd_workspace_size", "wha_attn_bwd",
     "wha_attn_bwd_from_probs_workspace_size", "wha_attn_bwd_from_probs",
     "wha_decode_workspace_size", "wha_decode_fwd",
-    "wha_host_attention_core_fwd", "wha_host_attention_backward",
+    "wha_linear_fwd", "wha_linear_bwd_dx", "wha_linear_bwd_dw_workspace_size", "wha_linear_bwd_dw",
+    "wha_host_attention_core_fwd", "wha_host_attention_backward", "wha_host_attention",
     "wha_synth_normal",
     "wha_timing_enable", "wha_timing_reset", "wha_timing_read",
 )
@@ -107,6 +109,13 @@ def lib():
         L.wha_decode_workspace_size.argtypes = [lp]
         L.wha_decode_workspace_size.restype = sz
         L.wha_decode_fwd.argtypes = [vp] * 5 + [vp, sz, lp, ctypes.c_float, vp]
+        i64 = ctypes.c_int64
+        L.wha_linear_fwd.argtypes = [vp, i64, vp, vp, vp, i64, i64, i32, i32, vp]
+        L.wha_linear_bwd_dx.argtypes = [vp, i64, vp, vp, i64, i64, i32, i32, vp]
+        L.wha_linear_bwd_dw_workspace_size.argtypes = [i64, i32, i32]
+        L.wha_linear_bwd_dw_workspace_size.restype = sz
+        L.wha_linear_bwd_dw.argtypes = [vp, i64, vp, i64, vp, vp, i64, i32, i32, vp, sz, vp]
+        L.wha_host_attention.argtypes = [f32p] * 5 + [i32, i32, i32, f32p]
         L.wha_host_attention_core_fwd.argtypes = [f32p, f32p, f32p, i32, i32, i32, f32p]
         L.wha_host_attention_backward.argtypes = [f32p] * 5 + [i32, i32, i32] + [f32p] * 3
         L.wha_synth_normal.argtypes = [ctypes.POINTER(ctypes.c_uint64), f32p, sz, ctypes.c_double, ctypes.c_int]
@@ -252,6 +261,59 @@ def decode_fwd(q, k_cache, v_cache, scale=None, want_lse=False, workspace=None):
     return (o, lse) if want_lse else o
 
 
+def _rows_of(t, name):
+    """(rows, row stride) of a 2-D float32 device tensor with unit column stride."""
+    torch = _torch()
+    if t.dim() != 2 or t.dtype != torch.float32 or not t.is_cuda:
+        raise ValueError(f"{name}: expected a 2-D float32 device tensor, got {tuple(t.shape)} {t.dtype}")
+    if t.stride(1) != 1 and t.shape[1] > 1:
+        raise ValueError(f"{name}: columns must be contiguous")
+    return t.shape[0], t.stride(0)
+
+
+def linear_fwd(x, w, b=None, out=None):
+    """y[m] = b + W x[m] for the rows of x [M][K] (w [N][K] contiguous, b [N] or None)."""
+    torch = _torch()
+    M, ldx = _rows_of(x, "x")
+    N, K = w.shape
+    if not w.is_contiguous() or x.shape[1] != K:
+        raise ValueError("w must be a contiguous [N][K] tensor matching x's columns")
+    y = torch.empty((M, N), dtype=torch.float32, device=x.device) if out is None else out
+    _, ldy = _rows_of(y, "out")
+    _check("wha_linear_fwd", lib().wha_linear_fwd(_ptr(x), ldx, _ptr(w), _ptr(b) if b is not None else None,
+                                                  _ptr(y), ldy, M, N, K, _stream_ptr(x)))
+    return y
+
+
+def linear_bwd_dx(dy, w, out=None):
+    """dx[m] = W^T dy[m] (linear_backward_dx_batch)."""
+    torch = _torch()
+    M, lddy = _rows_of(dy, "dy")
+    N, K = w.shape
+    dx = torch.empty((M, K), dtype=torch.float32, device=dy.device) if out is None else out
+    _, lddx = _rows_of(dx, "out")
+    _check("wha_linear_bwd_dx", lib().wha_linear_bwd_dx(_ptr(dy), lddy, _ptr(w), _ptr(dx), lddx, M, N, K,
+                                                        _stream_ptr(dy)))
+    return dx
+
+
+def linear_bwd_dw(dy, x, compute_bias=True, workspace=None):
+    """(d_w [N][K], d_b [N] or None) = outer_product_accum(dy, x, compute_bias)."""
+    torch = _torch()
+    M, lddy = _rows_of(dy, "dy")
+    M2, ldx = _rows_of(x, "x")
+    if M2 != M:
+        raise ValueError("dy and x must have the same number of rows")
+    N, K = dy.shape[1], x.shape[1]
+    dw = torch.empty((N, K), dtype=torch.float32, device=dy.device)
+    db = torch.empty(N, dtype=torch.float32, device=dy.device) if compute_bias else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check("wha_linear_bwd_dw", lib().wha_linear_bwd_dw(
+        _ptr(dy), lddy, _ptr(x), ldx, _ptr(dw), _ptr(db) if db is not None else None, M, N, K,
+        _ptr(workspace), ws_bytes, _stream_ptr(dy)))
+    return dw, db
+
+
 class AttnPlan:
     """Launches bound once to a fixed set of [B,H,T,D] tensors: layouts, pointers,
     scale, workspace and stream are validated and marshalled at construction, so
@@ -325,6 +387,21 @@ def _fp(a):
     return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
 
 
+class LinearWeights:
+    """LinearWeights (src/common/model.rs:175-180): w [out_dim][in_dim], b [out_dim]."""
+
+    def __init__(self, w, b):
+        self.w = np.ascontiguousarray(np.asarray(w, dtype=np.float32))
+        self.b = np.ascontiguousarray(np.asarray(b, dtype=np.float32))
+
+
+class AttentionWeights:
+    """AttentionWeights (src/common/model.rs:189-195): c_attn [3E][E], c_proj [E][E], n_head."""
+
+    def __init__(self, c_attn: LinearWeights, c_proj: LinearWeights, n_head: int):
+        self.c_attn, self.c_proj, self.n_head = c_attn, c_proj, int(n_head)
+
+
 class HipBackend:
     """The attention half of wave-engine's ``ComputeBackend`` on the HIP tier.
 
@@ -335,6 +412,19 @@ class HipBackend:
     ``[T][n_embd]`` host arrays (lists of rows or 2-D arrays); outputs are
     ``[T][n_embd]`` float32 numpy arrays.  Failures raise ``RuntimeError`` where
     the reference panics."""
+
+    def attention(self, weights: "AttentionWeights", x):
+        """fn attention(&self, weights, x) (src/common/compute.rs:42-43): c_attn,
+        causal attention core and c_proj on one sequence x [T][n_embd]."""
+        xs = _as_2d_f32(x, "x")
+        T, E = xs.shape
+        wa, wp = weights.c_attn, weights.c_proj
+        if wa.w.shape != (3 * E, E) or wa.b.shape != (3 * E,) or wp.w.shape != (E, E) or wp.b.shape != (E,):
+            raise ValueError("weights: c_attn must be [3E][E] + [3E], c_proj [E][E] + [E]")
+        out = np.empty((T, E), dtype=np.float32)
+        _check("wha_host_attention", lib().wha_host_attention(_fp(xs), _fp(wa.w), _fp(wa.b), _fp(wp.w), _fp(wp.b),
+                                                              T, E, weights.n_head, _fp(out)))
+        return out
 
     def attention_core(self, q_all, k_all, v_all, n_head: int):
         q, k, v = (_as_2d_f32(a, n) for a, n in ((q_all, "q_all"), (k_all, "k_all"), (v_all, "v_all")))

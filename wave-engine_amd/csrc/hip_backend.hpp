@@ -66,6 +66,25 @@ inline Rows unflatten(const std::vector<float>& flat, size_t T, size_t E) {
 
 class HipBackend {
  public:
+  // ComputeBackend::attention (src/common/compute.rs:42-43), i.e. attention_cpu
+  // (:357-414) end to end: c_attn, causal attention core, c_proj.  x: [T][n_embd].
+  Rows attention(const AttentionWeights& w, const Rows& x) const {
+    const size_t T = x.size();
+    if (T == 0) throw Panic("attention: empty sequence");
+    const size_t E = x[0].size();
+    if (w.c_attn.w.size() != 3 * E || w.c_attn.b.size() != 3 * E || w.c_proj.w.size() != E ||
+        w.c_proj.b.size() != E)
+      throw Panic("attention: c_attn must be [3E][E] + [3E] and c_proj [E][E] + [E]");
+    const auto xf = detail::flatten(x, T, E, "x");
+    const auto wa = detail::flatten(w.c_attn.w, 3 * E, E, "c_attn.w");
+    const auto wp = detail::flatten(w.c_proj.w, E, E, "c_proj.w");
+    std::vector<float> out(T * E);
+    detail::check(wha_host_attention(xf.data(), wa.data(), w.c_attn.b.data(), wp.data(), w.c_proj.b.data(),
+                                     (int32_t)T, (int32_t)E, (int32_t)w.n_head, out.data()),
+                  "attention");
+    return detail::unflatten(out, T, E);
+  }
+
   // Core of attention_cpu (src/common/compute.rs:377-409): causal softmax
   // attention of already-projected q_all, k_all, v_all ([T][n_embd] each).
   Rows attention_core(const Rows& q_all, const Rows& k_all, const Rows& v_all, size_t n_head) const {

@@ -1,0 +1,309 @@
+// fp32 MFMA GEMM for the c_attn / c_proj projections around the attention core
+// (gfx950), forward and backward.
+//
+// Reference semantics (one position at a time, sequential f32 sums):
+//   linear / linear_batch      y[i] = b[i] + sum_j w[i][j] x[j]     src/common/compute.rs:441-453, model.rs:144-151
+//   linear_backward_dx         d_x[j] = sum_i d_y[i] w[i][j]        src/common/math/backward.rs:36-46
+//   outer_product_accum        d_w[i][j] = sum_pos d_y[pos][i] x[pos][j],  d_b[i] = sum_pos d_y[pos][i]
+//                                                                   src/common/compute.rs:263-282
+// Here all positions of a batch form one GEMM C[m][n] = bias[n] + sum_k A(m,k) B(k,n)
+// with A and B given by strides, so the same kernel serves y = X W^T + b,
+// dX = dY W and dW = dY^T X.
+//
+// Tiling: 128 x 128 output tile per 256-thread block, 2 x 2 waves of 64 x 64,
+// 16-deep k stages staged through LDS with k contiguous (operands transposed on
+// the way in when the source is not k-contiguous), register prefetch of the
+// next stage.  MFMA rows are output columns n and MFMA columns are output rows m,
+// so each lane ends with 4 consecutive n of one row: 128-bit stores, bias added
+// as a float4.  Lane group g covers k = 4g..4g+3 of a stage, so one 128-bit LDS
+// read supplies four MFMA steps.  Split-K writes per-split partial tiles that a
+// second kernel sums in a fixed order (deterministic).
+#include "wha_launch.hpp"
+
+namespace wha {
+
+namespace {
+constexpr int kGBM = 128, kGBN = 128, kGKT = 16, kGLD = kGKT + 4;
+}
+
+struct GemmArgs {
+  const float* a;
+  int64_t a_sm, a_sk;  // A(m,k) = a[m*a_sm + k*a_sk]
+  const float* b;
+  int64_t b_sn, b_sk;  // B(k,n) = b[n*b_sn + k*b_sk]
+  float* c;
+  int64_t ldc;         // C(m,n) = c[m*ldc + n]  (or the split-K partial [z][M][N])
+  const float* bias;   // [N] or nullptr
+  int M, N, K;
+  int k_chunk;         // k range per split (multiple of 16)
+  bool c_vec;          // c and ldc allow 128-bit stores
+};
+
+// Staging of one 128 x 16 operand tile (rows r = m or n, k contiguous in LDS);
+// element (r, k) of the source is p[r*s_r + k*s_k].  KC: s_k == 1 (rows of the
+// tile are source rows); otherwise s_r == 1 and the tile is transposed on the
+// way in.
+template <bool KC>
+struct GemmStage {
+  float4 v[2];
+  __device__ __forceinline__ void load(const float* __restrict__ p, int64_t s_r, int64_t s_k, int r0, int R,
+                                       int k0, int k_end, int tid) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int idx = tid + 256 * q;
+      float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (KC) {
+        const int rr = idx >> 2, c = (idx & 3) * 4;
+        const int r = r0 + rr, k = k0 + c;
+        if (r < R) {
+          const float* src = p + (int64_t)r * s_r + (int64_t)k * s_k;
+          if (k + 3 < k_end && (((uintptr_t)src) & 15) == 0) {
+            val = *reinterpret_cast<const float4*>(src);
+          } else {
+            if (k + 0 < k_end) val.x = src[0];
+            if (k + 1 < k_end) val.y = src[1];
+            if (k + 2 < k_end) val.z = src[2];
+            if (k + 3 < k_end) val.w = src[3];
+          }
+        }
+      } else {
+        const int kr = idx >> 5, rc = (idx & 31) * 4;
+        const int r = r0 + rc, k = k0 + kr;
+        if (k < k_end) {
+          const float* src = p + (int64_t)k * s_k + (int64_t)r * s_r;
+          if (r + 3 < R && (((uintptr_t)src) & 15) == 0) {
+            val = *reinterpret_cast<const float4*>(src);
+          } else {
+            if (r + 0 < R) val.x = src[0];
+            if (r + 1 < R) val.y = src[1];
+            if (r + 2 < R) val.z = src[2];
+            if (r + 3 < R) val.w = src[3];
+          }
+        }
+      }
+      v[q] = val;
+    }
+  }
+  __device__ __forceinline__ void store(float* lds, int tid) const {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int idx = tid + 256 * q;
+      if (KC) {
+        const int rr = idx >> 2, c = (idx & 3) * 4;
+        *reinterpret_cast<float4*>(lds + rr * kGLD + c) = v[q];
+      } else {
+        const int kr = idx >> 5, rc = (idx & 31) * 4;
+        lds[(rc + 0) * kGLD + kr] = v[q].x;
+        lds[(rc + 1) * kGLD + kr] = v[q].y;
+        lds[(rc + 2) * kGLD + kr] = v[q].z;
+        lds[(rc + 3) * kGLD + kr] = v[q].w;
+      }
+    }
+  }
+};
+
+template <bool A_KC, bool B_KC, bool PARTIAL>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+  __shared__ __align__(16) float As[kGBM * kGLD];
+  __shared__ __align__(16) float Bs[kGBN * kGLD];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 15, gq = lane >> 4;
+  const int wn = wave & 1, wm = wave >> 1;
+  const int n0 = blockIdx.x * kGBN, m0 = blockIdx.y * kGBM;
+  const int k_begin = blockIdx.z * g.k_chunk;
+  const int k_end = min(g.K, k_begin + g.k_chunk);
+
+  floatx4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  GemmStage<A_KC> sa;
+  GemmStage<B_KC> sb;
+  if (k_begin < k_end) {
+    sa.load(g.a, g.a_sm, g.a_sk, m0, g.M, k_begin, k_end, tid);
+    sb.load(g.b, g.b_sn, g.b_sk, n0, g.N, k_begin, k_end, tid);
+  }
+  for (int kk = k_begin; kk < k_end; kk += kGKT) {
+    __syncthreads();
+    sa.store(As, tid);
+    sb.store(Bs, tid);
+    __syncthreads();
+    if (kk + kGKT < k_end) {
+      sa.load(g.a, g.a_sm, g.a_sk, m0, g.M, kk + kGKT, k_end, tid);
+      sb.load(g.b, g.b_sn, g.b_sk, n0, g.N, kk + kGKT, k_end, tid);
+    }
+    float4 bv[4], av[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      bv[t] = *reinterpret_cast<const float4*>(&Bs[(64 * wn + 16 * t + lq) * kGLD + 4 * gq]);
+      av[t] = *reinterpret_cast<const float4*>(&As[(64 * wm + 16 * t + lq) * kGLD + 4 * gq]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const float bvals[4] = {bv[nt].x, bv[nt].y, bv[nt].z, bv[nt].w};
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          const float avals[4] = {av[mt].x, av[mt].y, av[mt].z, av[mt].w};
+          acc[nt][mt] = mfma4(bvals[e], avals[e], acc[nt][mt]);
+        }
+      }
+    }
+  }
+
+  // acc[nt][mt][i] = C[m = m0+64wm+16mt+lq][n = n0+64wn+16nt+4gq+i]
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int m = m0 + 64 * wm + 16 * mt + lq;
+    if (m >= g.M) continue;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int n = n0 + 64 * wn + 16 * nt + 4 * gq;
+      if (n >= g.N) continue;
+      float4 r = make_float4(acc[nt][mt][0], acc[nt][mt][1], acc[nt][mt][2], acc[nt][mt][3]);
+      float* dst;
+      if (PARTIAL) {
+        dst = g.c + ((int64_t)blockIdx.z * g.M + m) * g.N + n;
+      } else {
+        dst = g.c + (int64_t)m * g.ldc + n;
+        if (g.bias != nullptr) {
+          r.x = (n + 0 < g.N ? g.bias[n + 0] : 0.f) + r.x;
+          r.y = (n + 1 < g.N ? g.bias[n + 1] : 0.f) + r.y;
+          r.z = (n + 2 < g.N ? g.bias[n + 2] : 0.f) + r.z;
+          r.w = (n + 3 < g.N ? g.bias[n + 3] : 0.f) + r.w;
+        }
+      }
+      const bool vec = PARTIAL ? (g.N % 4 == 0) : g.c_vec;
+      if (vec && n + 3 < g.N) {
+        *reinterpret_cast<float4*>(dst) = r;
+      } else {
+        dst[0] = r.x;
+        if (n + 1 < g.N) dst[1] = r.y;
+        if (n + 2 < g.N) dst[2] = r.z;
+        if (n + 3 < g.N) dst[3] = r.w;
+      }
+    }
+  }
+}
+
+// C[m][n] = bias[n] + sum_z part[z][m][n], z in increasing order.
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part, int splits,
+                                                                 const float* __restrict__ bias,
+                                                                 float* __restrict__ c, int64_t ldc, int M,
+                                                                 int N) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)M * N) return;
+  const int m = (int)(i / N), n = (int)(i % N);
+  float s = 0.f;
+  for (int z = 0; z < splits; ++z) s += part[(int64_t)z * M * N + i];
+  c[(int64_t)m * ldc + n] = (bias != nullptr ? bias[n] : 0.f) + s;
+}
+
+// out[n] = sum_m y[m][n] (column sums, for the bias gradient): rows split over
+// blockIdx.y into fixed chunks whose partials are then added in order.
+__global__ __launch_bounds__(256) void colsum_partial_kernel(const float* __restrict__ y, int64_t ldy, int M,
+                                                             int N, int rows_per, float* __restrict__ part) {
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  const int r0 = blockIdx.y * rows_per, r1 = min(M, r0 + rows_per);
+  float s = 0.f;
+  for (int m = r0; m < r1; ++m) s += y[(int64_t)m * ldy + n];
+  part[(int64_t)blockIdx.y * N + n] = s;
+}
+
+__global__ __launch_bounds__(256) void colsum_final_kernel(const float* __restrict__ part, int chunks, int N,
+                                                           float* __restrict__ out) {
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  float s = 0.f;
+  for (int z = 0; z < chunks; ++z) s += part[(int64_t)z * N + n];
+  out[n] = s;
+}
+
+namespace {
+
+int gemm_splits(int M, int N, int K) {
+  const int tiles = ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
+  int splits = 1;
+  // aim for >= 512 blocks while keeping >= 256 k per split
+  while (tiles * splits < 512 && (K / (splits * 2)) >= 256) splits *= 2;
+  return splits;
+}
+
+int colsum_chunks(int M) { return M >= 4096 ? 64 : (M >= 256 ? 16 : 1); }
+
+template <bool A_KC, bool B_KC>
+hipError_t gemm_t(GemmArgs g, float* ws, const char* name, hipStream_t stream) {
+  const int splits = ws ? gemm_splits(g.M, g.N, g.K) : 1;
+  const dim3 grid((g.N + kGBN - 1) / kGBN, (g.M + kGBM - 1) / kGBM, splits);
+  TimingScope ts(name, stream);
+  if (splits == 1) {
+    g.k_chunk = ((g.K + kGKT - 1) / kGKT) * kGKT;
+    hipLaunchKernelGGL((gemm_kernel<A_KC, B_KC, false>), grid, dim3(256), 0, stream, g);
+    return hipGetLastError();
+  }
+  const int per = (g.K + splits - 1) / splits;
+  GemmArgs p = g;
+  p.k_chunk = ((per + kGKT - 1) / kGKT) * kGKT;
+  p.c = ws;
+  p.bias = nullptr;
+  hipLaunchKernelGGL((gemm_kernel<A_KC, B_KC, true>), grid, dim3(256), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t total = (int64_t)g.M * g.N;
+  hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                     (const float*)ws, splits, g.bias, g.c, g.ldc, g.M, g.N);
+  return hipGetLastError();
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+size_t linear_dw_workspace_floats(int N, int K, int64_t M) {
+  // split-K partials of the [N][K] weight gradient plus column-sum partials
+  const int splits = gemm_splits(N, K, (int)(M > 0x7fffffff ? 0x7fffffff : M));
+  const size_t part = splits > 1 ? (size_t)splits * N * K : 0;
+  return part + (size_t)colsum_chunks((int)M) * N + 64;
+}
+
+hipError_t launch_linear_fwd(const float* x, int64_t ldx, const float* w, const float* b, float* y, int64_t ldy,
+                             int M, int N, int K, hipStream_t stream) {
+  GemmArgs g{x, ldx, 1, w, (int64_t)K, 1, y, ldy, b, M, N, K, 0, aligned16(y) && ldy % 4 == 0};
+  return gemm_t<true, true>(g, nullptr, "linear_fwd", stream);
+}
+
+hipError_t launch_linear_bwd_dx(const float* dy, int64_t lddy, const float* w, float* dx, int64_t lddx, int M,
+                                int N, int K, hipStream_t stream) {
+  // dx[m][k] = sum_n dy[m][n] w[n][k]: GEMM with (M, N=K_in, K=N_out)
+  GemmArgs g{dy, lddy, 1, w, 1, (int64_t)K, dx, lddx, nullptr, M, K, N, 0, aligned16(dx) && lddx % 4 == 0};
+  return gemm_t<true, false>(g, nullptr, "linear_bwd_dx", stream);
+}
+
+hipError_t launch_linear_bwd_dw(const float* dy, int64_t lddy, const float* x, int64_t ldx, float* dw, float* db,
+                                int M, int N, int K, float* ws, hipStream_t stream) {
+  // dw[n][k] = sum_m dy[m][n] x[m][k]: GEMM with (M=N_out, N=K_in, K=M rows), both operands
+  // contiguous along the output index
+  GemmArgs g{dy, 1, lddy, x, 1, ldx, dw, (int64_t)K, nullptr, N, K, M, 0, aligned16(dw) && K % 4 == 0};
+  const int splits = gemm_splits(N, K, M);
+  float* part = splits > 1 ? ws : nullptr;
+  hipError_t e = gemm_t<false, false>(g, part, "linear_bwd_dw", stream);
+  if (e != hipSuccess || db == nullptr) return e;
+  float* cs = ws + (splits > 1 ? (size_t)splits * N * K : 0);
+  const int chunks = colsum_chunks(M);
+  const int rows_per = (M + chunks - 1) / chunks;
+  TimingScope ts("linear_bwd_db", stream);
+  hipLaunchKernelGGL(colsum_partial_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)chunks), dim3(256), 0,
+                     stream, dy, lddy, M, N, rows_per, cs);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, stream,
+                     (const float*)cs, chunks, N, db);
+  return hipGetLastError();
+}
+
+}  // namespace wha

@@ -455,6 +455,120 @@ int wha_host_attention_backward(const float* d_pre_proj, const float* q, const f
   return WHA_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+int check_linear(const char* fn, int64_t M, int32_t N, int32_t K) {
+  if (M <= 0 || N <= 0 || K <= 0)
+    return fail(WHA_ERR_INVALID, "%s: M, N, K must be positive (got %lld, %d, %d)", fn, (long long)M, N, K);
+  if (M > (int64_t)65535 * 128)
+    return fail(WHA_ERR_UNSUPPORTED, "%s: M = %lld rows exceeds %d", fn, (long long)M, 65535 * 128);
+  return WHA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wha_linear_fwd(const float* x, int64_t ldx, const float* w, const float* b, float* y, int64_t ldy, int64_t M,
+                   int32_t N, int32_t K, void* stream) {
+  static const char* fn = "wha_linear_fwd";
+  int rc = check_linear(fn, M, N, K);
+  if (rc) return rc;
+  if (!x || !w || !y) return fail(WHA_ERR_INVALID, "%s: x, w and y must be non-NULL", fn);
+  if (ldx < K || ldy < N) return fail(WHA_ERR_INVALID, "%s: ldx must be >= K and ldy >= N", fn);
+  hipError_t e = wha::launch_linear_fwd(x, ldx, w, b, y, ldy, (int)M, N, K, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "wha_linear_fwd launch");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+int wha_linear_bwd_dx(const float* dy, int64_t lddy, const float* w, float* dx, int64_t lddx, int64_t M, int32_t N,
+                      int32_t K, void* stream) {
+  static const char* fn = "wha_linear_bwd_dx";
+  int rc = check_linear(fn, M, N, K);
+  if (rc) return rc;
+  if (!dy || !w || !dx) return fail(WHA_ERR_INVALID, "%s: dy, w and dx must be non-NULL", fn);
+  if (lddy < N || lddx < K) return fail(WHA_ERR_INVALID, "%s: lddy must be >= N and lddx >= K", fn);
+  hipError_t e = wha::launch_linear_bwd_dx(dy, lddy, w, dx, lddx, (int)M, N, K, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "wha_linear_bwd_dx launch");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+size_t wha_linear_bwd_dw_workspace_size(int64_t M, int32_t N, int32_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return round256(wha::linear_dw_workspace_floats(N, K, M) * sizeof(float));
+}
+
+int wha_linear_bwd_dw(const float* dy, int64_t lddy, const float* x, int64_t ldx, float* dw, float* db, int64_t M,
+                      int32_t N, int32_t K, void* workspace, size_t workspace_bytes, void* stream) {
+  static const char* fn = "wha_linear_bwd_dw";
+  int rc = check_linear(fn, M, N, K);
+  if (rc) return rc;
+  if (!dy || !x || !dw) return fail(WHA_ERR_INVALID, "%s: dy, x and dw must be non-NULL", fn);
+  if (lddy < N || ldx < K) return fail(WHA_ERR_INVALID, "%s: lddy must be >= N and ldx >= K", fn);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  if ((rc = resolve_workspace(workspace, workspace_bytes, wha_linear_bwd_dw_workspace_size(M, N, K), s, fn, &ws)))
+    return rc;
+  hipError_t e = wha::launch_linear_bwd_dw(dy, lddy, x, ldx, dw, db, (int)M, N, K, static_cast<float*>(ws), s);
+  if (e != hipSuccess) return hip_fail(e, "wha_linear_bwd_dw launch");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+int wha_host_attention(const float* x, const float* c_attn_w, const float* c_attn_b, const float* c_proj_w,
+                       const float* c_proj_b, int32_t T, int32_t E, int32_t n_head, float* out) {
+  static const char* fn = "wha_host_attention";
+  wha::View V;
+  int rc = check_host_seq(fn, T, E, n_head, &V);
+  if (rc) return rc;
+  if (!x || !c_attn_w || !c_attn_b || !c_proj_w || !c_proj_b || !out)
+    return fail(WHA_ERR_INVALID, "%s: every pointer must be non-NULL", fn);
+  const size_t E3 = (size_t)3 * E;
+  auto fl = [](size_t n) { return round256(n * sizeof(float)) / sizeof(float); };
+  const size_t n_x = fl((size_t)T * E), n_wa = fl(E3 * E), n_ba = fl(E3), n_wp = fl((size_t)E * E), n_bp = fl(E);
+  const size_t n_qkv = fl((size_t)T * E3);
+  float* base = nullptr;
+  hipStream_t s = nullptr;
+  if ((rc = host_stage((2 * n_x + n_wa + n_ba + n_wp + n_bp + 2 * n_qkv) * sizeof(float), &base, &s))) return rc;
+  float* d_x = base;
+  float* d_wa = d_x + n_x;
+  float* d_ba = d_wa + n_wa;
+  float* d_wp = d_ba + n_ba;
+  float* d_bp = d_wp + n_wp;
+  float* d_qkv = d_bp + n_bp;
+  float* d_o = d_qkv + n_qkv;  // [T][3E] pitch, first E columns used
+  float* d_out = d_o + n_qkv;
+  struct Copy { float* dst; const float* src; size_t n; } copies[] = {
+      {d_x, x, (size_t)T * E}, {d_wa, c_attn_w, E3 * E}, {d_ba, c_attn_b, E3},
+      {d_wp, c_proj_w, (size_t)E * E}, {d_bp, c_proj_b, (size_t)E}};
+  hipError_t e = hipSuccess;
+  for (const Copy& c : copies)
+    if (e == hipSuccess) e = hipMemcpyAsync(c.dst, c.src, c.n * sizeof(float), hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync H2D");
+  // qkv = c_attn(x)  (src/common/compute.rs:368-375)
+  e = wha::launch_linear_fwd(d_x, E, d_wa, d_ba, d_qkv, (int64_t)E3, T, (int)E3, E, s);
+  if (e != hipSuccess) return hip_fail(e, "c_attn launch");
+  // core on the q, k, v column blocks of qkv, read in place
+  const int D = E / n_head;
+  wha::View Vq{1, n_head, T, D, (int64_t)T * (int64_t)E3, D, (int64_t)E3};
+  const float scale = 1.0f / sqrtf((float)D);  // src/common/compute.rs:362
+  e = wha::launch_attn_fwd(d_qkv, d_qkv + E, d_qkv + 2 * E, d_o, nullptr, Vq,
+                           vec_ok(Vq, {d_qkv, d_qkv + E, d_qkv + 2 * E, d_o}), scale, s);
+  if (e != hipSuccess) return hip_fail(e, "attention core launch");
+  // out = c_proj(o)  (:411-413)
+  e = wha::launch_linear_fwd(d_o, (int64_t)E3, d_wp, d_bp, d_out, E, T, E, E, s);
+  if (e != hipSuccess) return hip_fail(e, "c_proj launch");
+  e = hipMemcpyAsync(out, d_out, (size_t)T * E * sizeof(float), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync D2H");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
 int wha_timing_enable(int on) {
   TimingState& st = timing();
   std::lock_guard<std::mutex> lk(st.mu);

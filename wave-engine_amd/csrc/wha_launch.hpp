@@ -54,4 +54,17 @@ size_t decode_workspace_floats(const View& cache);
 hipError_t launch_decode(const float* q, const float* kc, const float* vc, float* o, float* lse,
                          float* ws, const View& cache, bool vec, float scale, hipStream_t stream);
 
+// Projections (fp32 MFMA GEMM).  x: [M][K] rows with stride ldx, w: [N][K]
+// row-major, b: [N] or nullptr, y: [M][N] rows with stride ldy.
+hipError_t launch_linear_fwd(const float* x, int64_t ldx, const float* w, const float* b, float* y, int64_t ldy,
+                             int M, int N, int K, hipStream_t stream);
+// dx[m][k] = sum_n dy[m][n] w[n][k]
+hipError_t launch_linear_bwd_dx(const float* dy, int64_t lddy, const float* w, float* dx, int64_t lddx, int M,
+                                int N, int K, hipStream_t stream);
+// dw[n][k] = sum_m dy[m][n] x[m][k]; db[n] = sum_m dy[m][n] (db may be nullptr).
+// ws: linear_dw_workspace_floats(N, K, M) floats.
+size_t linear_dw_workspace_floats(int N, int K, int64_t M);
+hipError_t launch_linear_bwd_dw(const float* dy, int64_t lddy, const float* x, int64_t ldx, float* dw, float* db,
+                                int M, int N, int K, float* ws, hipStream_t stream);
+
 }  // namespace wha
