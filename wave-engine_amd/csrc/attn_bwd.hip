@@ -196,8 +196,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
   }
 
   if (MODE == kDeltaFromProbs) {
-    dsum += xor_shfl(dsum, 16);
-    dsum += xor_shfl(dsum, 32);
+    dsum = pair_sum32(pair_sum16(dsum));
     if (g == 0 && row_ok) Delta[rix] = dsum;
   } else {
     store_row_frag<DP, VEC>(dQ + base, qrow, L.T, L.D, L.st, g, dqacc, scale);

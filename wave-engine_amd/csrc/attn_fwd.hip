@@ -17,8 +17,8 @@
 //            prefetch of the next tile while the current one is consumed).
 // Per tile a wave forms S^T = K Q^T (keys on MFMA rows, its 16 queries on
 // columns).  That layout leaves every lane with one query, so the running max
-// needs only two cross-lane steps, the running sum stays lane-local until the
-// end, and the probabilities are already in the B-operand layout of
+// needs only two cross-lane steps (VALU lane swaps), the running sum stays
+// lane-local until the end, and the probabilities are already in the B-operand layout of
 // O^T += V^T P^T -- no transpose through LDS.
 #include "wha_launch.hpp"
 
@@ -115,8 +115,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
         mx = fmaxf(mx, x);
       }
     }
-    mx = fmaxf(mx, xor_shfl(mx, 16));
-    mx = fmaxf(mx, xor_shfl(mx, 32));
+    mx = pair_max32(pair_max16(mx));
     const float m_new = fmaxf(m_i, mx);
     const float alpha = fast_exp2(m_i - m_new);
     float rs = 0.f;
@@ -148,8 +147,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
     }
   }
 
-  float l_sum = l_i + xor_shfl(l_i, 16);
-  l_sum += xor_shfl(l_sum, 32);
+  const float l_sum = pair_sum32(pair_sum16(l_i));
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll

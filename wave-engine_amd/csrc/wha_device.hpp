@@ -37,6 +37,28 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 __device__ __forceinline__ float xor_shfl(float x, int mask) { return __shfl_xor(x, mask, 64); }
 
+// Reductions over lane pairs (l, l^16) and (l, l^32) with the gfx950 VALU lane
+// swaps instead of an LDS permute.  With both operands = x,
+// v_permlane16_swap leaves lane l holding {x[l], x[l^16]} (in some order) and
+// v_permlane32_swap {x[l], x[l^32]}; max and + are commutative, so both lanes of
+// a pair get bit-identical results.
+__device__ __forceinline__ float pair_max16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_max32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair_sum32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Cooperative global -> register -> LDS staging of a ROWS x DP tile of one
 // (b,h) matrix, rows [row0, row0+ROWS), zero-filled past T and past D.
 // VEC: 128-bit global loads (requires D, all strides and the base 16-byte
