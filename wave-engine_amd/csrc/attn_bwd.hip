@@ -76,7 +76,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
   constexpr int NT = NW * 64;
   constexpr int BM = NW * 16;
   constexpr int BN = 64;
-  constexpr int LD = DP + 4;
+  constexpr int LD = DP + WHA_LDS_PAD;
   constexpr int DG = DP / 4;
   constexpr int NDT = DP / 16;
   constexpr int NKT = BN / 16;
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
   constexpr int NT = NW * 64;
   constexpr int BNK = NW * 16;  // keys per block
   constexpr int BMQ = 64;       // queries per tile
-  constexpr int LD = DP + 4;
+  constexpr int LD = DP + WHA_LDS_PAD;
   constexpr int DG = DP / 4;
   constexpr int NDT = DP / 16;
   constexpr int NQT = BMQ / 16;
@@ -285,22 +285,26 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
       s[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
       dp[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
+    // S and dP: 2*NQT independent accumulator chains, interleaved step by step
 #pragma unroll
     for (int j = 0; j < DG / 4; ++j) {
+      float4 a[NQT], c[NQT];
 #pragma unroll
       for (int mt = 0; mt < NQT; ++mt) {
-        if (!PROBS) {
-          const float4 a = *reinterpret_cast<const float4*>(&Qs[(16 * mt + lq) * LD + g * DG + 4 * j]);
-          s[mt] = mfma4(a.x, kf[4 * j + 0], s[mt]);
-          s[mt] = mfma4(a.y, kf[4 * j + 1], s[mt]);
-          s[mt] = mfma4(a.z, kf[4 * j + 2], s[mt]);
-          s[mt] = mfma4(a.w, kf[4 * j + 3], s[mt]);
+        if (!PROBS) a[mt] = *reinterpret_cast<const float4*>(&Qs[(16 * mt + lq) * LD + g * DG + 4 * j]);
+        c[mt] = *reinterpret_cast<const float4*>(&Os[(16 * mt + lq) * LD + g * DG + 4 * j]);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+#pragma unroll
+        for (int mt = 0; mt < NQT; ++mt) {
+          if (!PROBS) {
+            const float av[4] = {a[mt].x, a[mt].y, a[mt].z, a[mt].w};
+            s[mt] = mfma4(av[e], kf[4 * j + e], s[mt]);
+          }
+          const float cv[4] = {c[mt].x, c[mt].y, c[mt].z, c[mt].w};
+          dp[mt] = mfma4(cv[e], vf[4 * j + e], dp[mt]);
         }
-        const float4 c = *reinterpret_cast<const float4*>(&Os[(16 * mt + lq) * LD + g * DG + 4 * j]);
-        dp[mt] = mfma4(c.x, vf[4 * j + 0], dp[mt]);
-        dp[mt] = mfma4(c.y, vf[4 * j + 1], dp[mt]);
-        dp[mt] = mfma4(c.z, vf[4 * j + 2], dp[mt]);
-        dp[mt] = mfma4(c.w, vf[4 * j + 3], dp[mt]);
       }
     }
 
@@ -376,7 +380,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_ds_kernel(const float* __
   constexpr int NT = NW * 64;
   constexpr int BM = NW * 16;
   constexpr int BN = 64;
-  constexpr int LD = DP + 4;
+  constexpr int LD = DP + WHA_LDS_PAD;
   constexpr int NDT = DP / 16;
   __shared__ __align__(16) float Ks[BN * LD];
 
@@ -410,9 +414,13 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_ds_kernel(const float* __
   float4 dcur[4], dnext[4];
   load_ds(0, dcur);
 
-  floatx4 acc[NDT];
+  // even and odd 16-key chunks accumulate separately: 2*NDT independent chains
+  floatx4 acc[NDT], acc2[NDT];
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int dt = 0; dt < NDT; ++dt) {
+    acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    acc2[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
 
   for (int kt = 0; kt < n_kt; ++kt) {
     __syncthreads();
@@ -423,21 +431,31 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_ds_kernel(const float* __
       load_ds(kt + 1, dnext);
     }
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (kt * BN + 16 * c <= q0 + 15) {  // else the chunk is after every query of the wave (dS = 0)
-        const float de[4] = {dcur[c].x, dcur[c].y, dcur[c].z, dcur[c].w};
+    for (int c = 0; c < 4; c += 2) {
+      // chunks after every query of the wave hold dS = 0 and are skipped
+      const bool on0 = kt * BN + 16 * c <= q0 + 15;
+      const bool on1 = kt * BN + 16 * (c + 1) <= q0 + 15;
+      if (on0) {
+        const float d0[4] = {dcur[c].x, dcur[c].y, dcur[c].z, dcur[c].w};
+        const float d1[4] = {dcur[c + 1].x, dcur[c + 1].y, dcur[c + 1].z, dcur[c + 1].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          float ka[NDT];
+          float ka[NDT], kb[NDT];
           lds_read_vec<NDT>(&Ks[(16 * c + 4 * g + e) * LD + NDT * lq], ka);
+          lds_read_vec<NDT>(&Ks[(16 * (c + 1) + 4 * g + e) * LD + NDT * lq], kb);
 #pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma4(ka[dt], de[e], acc[dt]);
+          for (int dt = 0; dt < NDT; ++dt) {
+            acc[dt] = mfma4(ka[dt], d0[e], acc[dt]);
+            acc2[dt] = mfma4(kb[dt], on1 ? d1[e] : 0.f, acc2[dt]);
+          }
         }
       }
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) dcur[c] = dnext[c];
   }
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) acc[dt] += acc2[dt];
   store_row_frag<DP, VEC>(dQ + base, qrow, L.T, L.D, L.st, g, acc, scale);
 }
 
@@ -469,8 +487,10 @@ hipError_t bwd_fused_t(const float* q, const float* k, const float* v, const flo
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     TimingScope ts("attn_bwd_dq", stream);
-    hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<DP, NWQ, VEC>), dim3((unsigned)(n_qt * L.B * L.H)),
-                       dim3(NWQ * 64), 0, stream, k, (const float*)ds, dq, L, scale);
+    constexpr int NWD = WHA_DQ_NW;
+    const int n_qt_d = (L.T + NWD * 16 - 1) / (NWD * 16);
+    hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<DP, NWD, VEC>), dim3((unsigned)(n_qt_d * L.B * L.H)),
+                       dim3(NWD * 64), 0, stream, k, (const float*)ds, dq, L, scale);
     return hipGetLastError();
   }
   {

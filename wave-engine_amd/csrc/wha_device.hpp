@@ -13,6 +13,20 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// LDS row padding (floats) of the staged [rows][head_dim] tiles; a multiple of
+// 4 keeps 128-bit LDS accesses aligned.
+#ifndef WHA_LDS_PAD
+#define WHA_LDS_PAD 4
+#endif
+// Waves per block of the forward and query-stationary backward kernels
+// (16 queries per wave).
+#ifndef WHA_FWD_NW
+#define WHA_FWD_NW 4
+#endif
+#ifndef WHA_DQ_NW
+#define WHA_DQ_NW 4
+#endif
+
 namespace wha {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
