@@ -116,6 +116,18 @@ int wha_decode_fwd(const float* q, const float* k_cache, const float* v_cache,
                    float* o, float* lse, void* workspace, size_t workspace_bytes,
                    const wha_layout* cache_layout, float scale, void* stream);
 
+/* Rows of the attention probabilities on demand, for consumers of materialised
+ * P: the head monitor reads the last row of every head
+ * (src/monitors/attn_monitor.rs:26-80) and the softmax_rows value contract
+ * checks rows in [0, 1] that sum to 1 (src/monitors/junctions/value_range.rs:117-121).
+ * Recomputed from q, k and the forward's lse:
+ *   out[b][h][r][j] = exp(q_t . k_j * scale - lse[b][h][t]) for j <= t = rows[r], 0 for j > t.
+ * rows is a host array of n_rows (1..256) query indices in [0, T); out is
+ * [B][H][n_rows][T] contiguous. */
+int wha_attn_probs_rows(const float* q, const float* k, const float* lse,
+                        const int32_t* rows, int32_t n_rows, float* out,
+                        const wha_layout* layout, float scale, void* stream);
+
 /* ---------------------------------------------------------------- projections
  * The c_attn / c_proj linears around the core (fp32 MFMA GEMM).  A batch of M
  * rows is one call; rows of x / y / dy / dx have the given strides (floats),

@@ -117,3 +117,25 @@ def test_padded_dims_cover_the_configs():
     # head_dim of the BASELINE configs: 42, 48, 64, 128 (all <= 128)
     src = (ROOT / "wave-engine_amd" / "csrc" / "wha_launch.hpp").read_text()
     assert "D <= 128" in src
+
+
+def test_probs_rows_validates_rows(pkg):
+    L = pkg.lib()
+    lay = pkg.layout_bhtd(1, 2, 16, 64)
+    p = ctypes.c_void_p(1 << 20)
+    rows = (ctypes.c_int32 * 2)(3, 16)  # 16 is outside [0, 16)
+    assert L.wha_attn_probs_rows(p, p, p, rows, 2, p, ctypes.byref(lay), 0.125, None) == WHA_ERR_INVALID
+    assert b"outside" in L.wha_last_error()
+    assert L.wha_attn_probs_rows(p, p, p, rows, 0, p, ctypes.byref(lay), 0.125, None) == WHA_ERR_INVALID
+    assert L.wha_attn_probs_rows(p, p, p, rows, 257, p, ctypes.byref(lay), 0.125, None) == WHA_ERR_INVALID
+
+
+def test_head_stats_follow_the_monitor_definitions(pkg):
+    """analyze_attention (src/monitors/attn_monitor.rs:26-80) on hand-made rows."""
+    rows = np.array([[0.25, 0.25, 0.5, 0.0], [0.0, 0.0, 0.0, 1.0], [0.4, 0.2, 0.4, 0.0]], np.float32)
+    st = pkg.attention_head_stats(rows)
+    ent0 = -(0.25 * np.log(0.25) * 2 + 0.5 * np.log(0.5))
+    np.testing.assert_allclose(st["entropy"], [ent0, 0.0, -(2 * 0.4 * np.log(0.4) + 0.2 * np.log(0.2))], rtol=1e-6)
+    np.testing.assert_array_equal(st["top_position"], [2, 3, 0])   # first maximum wins ties
+    np.testing.assert_allclose(st["max_weight"], [0.5, 1.0, 0.4])
+    np.testing.assert_allclose(st["self_attn_frac"], [0.0, 1.0, 0.0])

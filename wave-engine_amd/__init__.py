@@ -39,7 +39,7 @@ EXPORTED_SYMBOLS = (
     "wha_last_error", "wha_version",
     "wha_attn_fwd", "wha_attn_bwd_workspace_size", "wha_attn_bwd",
     "wha_attn_bwd_from_probs_workspace_size", "wha_attn_bwd_from_probs",
-    "wha_decode_workspace_size", "wha_decode_fwd",
+    "wha_decode_workspace_size", "wha_decode_fwd", "wha_attn_probs_rows",
     "wha_linear_fwd", "wha_linear_bwd_dx", "wha_linear_bwd_dw_workspace_size", "wha_linear_bwd_dw",
     "wha_host_attention_core_fwd", "wha_host_attention_backward", "wha_host_attention",
     "wha_synth_normal",
@@ -118,6 +118,7 @@ def lib():
         L.wha_host_attention.argtypes = [f32p] * 5 + [i32, i32, i32, f32p]
         L.wha_host_attention_core_fwd.argtypes = [f32p, f32p, f32p, i32, i32, i32, f32p]
         L.wha_host_attention_backward.argtypes = [f32p] * 5 + [i32, i32, i32] + [f32p] * 3
+        L.wha_attn_probs_rows.argtypes = [vp, vp, vp, ctypes.POINTER(ctypes.c_int32), i32, vp, lp, ctypes.c_float, vp]
         L.wha_synth_normal.argtypes = [ctypes.POINTER(ctypes.c_uint64), f32p, sz, ctypes.c_double, ctypes.c_int]
         L.wha_synth_normal.restype = ctypes.c_int
         L.wha_timing_enable.argtypes = [ctypes.c_int]
@@ -222,6 +223,37 @@ def attn_bwd(q, k, v, o, do, lse, scale=None, workspace=None, dq=None, dk=None, 
         _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse.contiguous()), _ptr(dq), _ptr(dk), _ptr(dv),
         _ptr(workspace), ws_bytes, ctypes.byref(L), s, _stream_ptr(q)))
     return dq, dk, dv
+
+
+def attn_probs_rows(q, k, lse, rows, scale=None):
+    """Rows of P recomputed from q, k and the forward's lse: returns [B,H,len(rows),T]
+    with out[b,h,r,j] = softmax row rows[r] (zeros past the causal limit)."""
+    torch = _torch()
+    L = layout_of(q)
+    _same_layout(L, k)
+    rows = [int(r) for r in rows]
+    arr = (ctypes.c_int32 * len(rows))(*rows)
+    out = torch.empty((L.B, L.H, len(rows), L.T), dtype=torch.float32, device=q.device)
+    s = default_scale(L.D) if scale is None else float(scale)
+    _check("wha_attn_probs_rows", lib().wha_attn_probs_rows(_ptr(q), _ptr(k), _ptr(lse.contiguous()), arr, len(rows),
+                                                            _ptr(out), ctypes.byref(L), s, _stream_ptr(q)))
+    return out
+
+
+def attention_head_stats(last_rows):
+    """Per-head statistics of attention rows, as analyze_attention computes them
+    for the last position (src/monitors/attn_monitor.rs:26-80): for each row
+    (..., T) holding position t = T-1's weights, entropy = sum(-p ln p) over p > 0,
+    the first maximum weight and its position, and the self-attention weight p[t].
+    Returns a dict of numpy arrays shaped like last_rows without the last axis."""
+    p = np.asarray(last_rows, dtype=np.float32)
+    pos = p.shape[-1] - 1
+    with np.errstate(divide="ignore", invalid="ignore"):
+        ent = np.where(p > 0, -p * np.log(p), 0.0).astype(np.float32).sum(-1)
+    top = p.argmax(-1)
+    mx = np.take_along_axis(p, top[..., None], -1)[..., 0]
+    mx = np.maximum(mx, 0.0)
+    return {"entropy": ent, "max_weight": mx, "top_position": top, "self_attn_frac": p[..., pos]}
 
 
 def attn_bwd_workspace_bytes(L: WaveLayout) -> int:

@@ -351,6 +351,29 @@ int wha_attn_bwd_from_probs(const float* d_pre_proj, const float* q, const float
   return WHA_OK;
 }
 
+int wha_attn_probs_rows(const float* q, const float* k, const float* lse, const int32_t* rows, int32_t n_rows,
+                        float* out, const wha_layout* layout, float scale, void* stream) {
+  static const char* fn = "wha_attn_probs_rows";
+  wha::View V;
+  int rc = check_layout(layout, &V, fn);
+  if (rc) return rc;
+  if ((rc = check_scale(scale, fn))) return rc;
+  if (!q || !k || !lse || !rows || !out) return fail(WHA_ERR_INVALID, "%s: every pointer must be non-NULL", fn);
+  if (n_rows < 1 || n_rows > wha::kMaxProbRows)
+    return fail(WHA_ERR_INVALID, "%s: n_rows must be in [1, %d] (got %d)", fn, wha::kMaxProbRows, n_rows);
+  wha::RowList rl;
+  rl.n = n_rows;
+  for (int i = 0; i < n_rows; ++i) {
+    if (rows[i] < 0 || rows[i] >= V.T)
+      return fail(WHA_ERR_INVALID, "%s: rows[%d] = %d is outside [0, %d)", fn, i, rows[i], V.T);
+    rl.rows[i] = rows[i];
+  }
+  hipError_t e = wha::launch_attn_probs_rows(q, k, lse, rl, out, V, scale, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "wha_attn_probs_rows launch");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
 size_t wha_decode_workspace_size(const wha_layout* layout) {
   wha::View V;
   if (!layout || check_layout(layout, &V, "wha_decode_workspace_size") != WHA_OK) return 0;

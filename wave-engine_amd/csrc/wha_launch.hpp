@@ -54,6 +54,15 @@ size_t decode_workspace_floats(const View& cache);
 hipError_t launch_decode(const float* q, const float* kc, const float* vc, float* o, float* lse,
                          float* ws, const View& cache, bool vec, float scale, hipStream_t stream);
 
+// Rows of P recomputed from q, k and the forward's LSE (kernel argument by value).
+constexpr int kMaxProbRows = 256;
+struct RowList {
+  int n;
+  int rows[kMaxProbRows];
+};
+hipError_t launch_attn_probs_rows(const float* q, const float* k, const float* lse, const RowList& rl, float* out,
+                                  const View& L, float scale, hipStream_t stream);
+
 // Projections (fp32 MFMA GEMM).  x: [M][K] rows with stride ldx, w: [N][K]
 // row-major, b: [N] or nullptr, y: [M][N] rows with stride ldy.
 hipError_t launch_linear_fwd(const float* x, int64_t ldx, const float* w, const float* b, float* y, int64_t ldy,
