@@ -185,6 +185,94 @@ int wha_host_attention_backward(const float* d_pre_proj, const float* q,
                                 int32_t n_head, float* dq, float* dk,
                                 float* dv);
 
+/* ---------------------------------------------------------------- wave attention
+ * The harmonic coherence attention the reference trains with
+ * (src/common/attn.rs:72-430; callers src/cpu/forward.rs:113 and
+ * src/cpu/model_backward.rs:380-395).  Device pointers, batched over B
+ * sequences of T positions, input x [B][T][n_embd] contiguous (the normed
+ * hidden state the reference passes in). */
+
+/* Shape.  content_dim C = rows of each head's content projection (0 = none,
+ * the reference's backward-compatible mode; at most 30); head_dim =
+ * n_embd / n_head must be at most 128. */
+typedef struct wha_wave_shape {
+  int32_t B, T, n_embd, n_head, content_dim;
+} wha_wave_shape;
+
+/* Weights (WaveAttnWeights, attn.rs:17-46), device pointers, fp32:
+ *   harmonic_raw [n_head]
+ *   proj_w [n_head][2 + C][n_embd]: row 0 / 1 = phase_proj_w[0] / [1] (r, s),
+ *          rows 2 .. 1+C = content_proj_w   (one GEMM computes all of them)
+ *   proj_b [n_head][2 + C]: phase_proj_b then content_proj_b
+ *   v_w [n_head][head_dim][head_dim], v_b [n_head][head_dim]
+ *   out_w [n_embd][n_embd], out_b [n_embd] */
+typedef struct wha_wave_weights {
+  const float* harmonic_raw;
+  const float* proj_w;
+  const float* proj_b;
+  const float* v_w;
+  const float* v_b;
+  const float* out_w;
+  const float* out_b;
+} wha_wave_weights;
+
+/* Forward intermediates kept for the backward (the role of WaveAttnCache,
+ * attn.rs:48-70), caller-allocated device buffers:
+ *   proj   [B][T][n_head][2 + C]  r, s and the content vector
+ *   values [B][T][n_embd]         per-head value projections (head h at columns h*head_dim)
+ *   feat   [B][n_head][T][32]     cos(n phi), sin(n phi), content, zeros (16-byte aligned)
+ *   phase  [B][n_head][T]         phi = atan2(s, r)
+ *   bucket [B][n_head][T]         phase_to_bucket(phi) (kv_cache.rs:66-70)
+ *   merged [B][T][n_embd]         head outputs before out_proj (out_merged)
+ *   lse    [B][n_head][T]         natural-log row log-sum-exp of the scores */
+typedef struct wha_wave_cache {
+  float* proj;
+  float* values;
+  float* feat;
+  float* phase;
+  int32_t* bucket;
+  float* merged;
+  float* lse;
+} wha_wave_cache;
+
+/* wave_attention_forward (attn.rs:90-305): out [B][T][n_embd] and the cache.
+ * The reference's att_weights_all is not materialised; wha_wave_probs_rows
+ * recomputes any rows of it from the cache. */
+int wha_wave_fwd(const float* x, const wha_wave_weights* w, const wha_wave_shape* shape, float* out,
+                 const wha_wave_cache* cache, void* stream);
+
+/* Gradients.  d_x [B][T][n_embd] (d_normed) is required; the weight
+ * gradients (same layouts as wha_wave_weights, summed over the B sequences)
+ * are either all non-NULL (wave_attention_backward_full, attn.rs:346-430) or
+ * all NULL (wave_attention_backward_pathway, attn.rs:432-511: d_x only). */
+typedef struct wha_wave_grads {
+  float* d_x;
+  float* d_harmonic_raw;
+  float* d_proj_w;
+  float* d_proj_b;
+  float* d_v_w;
+  float* d_v_b;
+  float* d_out_w;
+  float* d_out_b;
+} wha_wave_grads;
+
+/* Workspace bytes of wha_wave_bwd (0 for an invalid shape). */
+size_t wha_wave_bwd_workspace_size(const wha_wave_shape* shape);
+
+/* Backward from d_out = d_attn_out [B][T][n_embd] (the gradient of out), the
+ * forward's x and cache.  Deterministic (no atomics). */
+int wha_wave_bwd(const float* x, const float* d_out, const wha_wave_weights* w, const wha_wave_shape* shape,
+                 const wha_wave_cache* cache, const wha_wave_grads* grads, void* workspace,
+                 size_t workspace_bytes, void* stream);
+
+/* Rows of att_weights_all (attn.rs:240, :259-269) on demand, from the cache:
+ * out[b][h][r][j] for query t = rows[r] is the post-softmax weight of key j
+ * (0 where the bucket mask excludes j <= t, -inf for j > t as in the
+ * reference's rows).  rows: host array, n_rows in 1..256, each in [0, T);
+ * out [B][n_head][n_rows][T] contiguous. */
+int wha_wave_probs_rows(const wha_wave_cache* cache, const wha_wave_shape* shape, const int32_t* rows,
+                        int32_t n_rows, float* out, void* stream);
+
 /* ---------------------------------------------------------------- inputs
  * Seeded synthetic inputs (host): continues the xorshift64 stream in *state
  * (the reference's Rng::next_u64/next_f32, src/common/rng.rs:24-34) with

@@ -326,3 +326,180 @@ def batch_fwd_bwd_f32_threaded(q_seq, k_seq, v_seq, do_seq, n_head: int, nthread
     lib().wao_batch_fwd_bwd_f32(B, T, E, n_head, q_seq, k_seq, v_seq, do_seq.ctypes.data, out,
                                 dq.ctypes.data, dk.ctypes.data, dv.ctypes.data, nthreads)
     return out, dq, dk, dv
+
+
+# ---------------------------------------------------------------- wave attention
+# Restatement of src/common/attn.rs:72-430 and src/common/math/attn_backward.rs
+# (C body in wave_core.inc).  Weights are a dict of arrays in the flattened layout
+#   hraw [H], proj_w [H][2+C][E] (rows r, s, then content), proj_b [H][2+C],
+#   v_w [H][hd][hd], v_b [H][hd], out_w [E][E], out_b [E].
+
+_WAVE_KEYS = ("hraw", "proj_w", "proj_b", "v_w", "v_b", "out_w", "out_b")
+
+
+def _ptr(a):
+    return None if a is None else ctypes.c_void_p(a.ctypes.data)
+
+
+def _wave_fn(name, precision, restype=None):
+    f = getattr(lib(), f"{name}_{precision}")
+    f.restype = restype
+    return f
+
+
+def wave_dims(w):
+    H, P, E = w["proj_w"].shape
+    return H, P - 2, E
+
+
+def phase_bucket(phase: float, precision: str = "f32") -> int:
+    """phase_to_bucket (src/common/kv_cache.rs:66-70)."""
+    real = ctypes.c_float if precision == "f32" else ctypes.c_double
+    f = _wave_fn("wao_phase_bucket", precision, ctypes.c_int)
+    f.argtypes = [real]
+    return int(f(phase))
+
+
+def wave_fwd(x, w, precision: str = "f32", phase_in=None):
+    """wave_attention_forward on one sequence x [T][E].  phase_in [H][T]
+    (optional) replays given phases.  Returns a dict with out, merged, att
+    ([H][T][T], -inf after the diagonal as in the reference), phase [H][T],
+    rs [H][T][2], content [H][T][C], values [H][T][hd], lse [H][T]."""
+    dt = _dt(precision)
+    x = _c(x, dt)
+    ww = {k: _c(w[k], dt) for k in _WAVE_KEYS}
+    H, C, E = wave_dims(ww)
+    T = x.shape[0]
+    hd = E // H
+    ph_in = _c(phase_in, dt) if phase_in is not None else None
+    r = dict(out=np.empty((T, E), dt), merged=np.empty((T, E), dt), att=np.empty((H, T, T), dt),
+             phase=np.empty((H, T), dt), rs=np.empty((H, T, 2), dt), content=np.empty((H, T, max(C, 0)), dt),
+             values=np.empty((H, T, hd), dt), lse=np.empty((H, T), dt))
+    _wave_fn("wao_wave_fwd", precision)(
+        _ptr(x), T, E, H, C, *(_ptr(ww[k]) for k in _WAVE_KEYS), _ptr(ph_in), _ptr(r["out"]), _ptr(r["merged"]),
+        _ptr(r["att"]), _ptr(r["phase"]), _ptr(r["rs"]), _ptr(r["content"]) if C > 0 else None,
+        _ptr(r["values"]), _ptr(r["lse"]))
+    return r
+
+
+def wave_bwd(x, w, d_out, precision: str = "f32", phase_in=None):
+    """wave_attention_backward_full on one sequence.  Returns a dict with d_x,
+    d_hraw, d_proj_w, d_proj_b, d_v_w, d_v_b, d_out_w, d_out_b."""
+    dt = _dt(precision)
+    x, d_out = _c(x, dt), _c(d_out, dt)
+    ww = {k: _c(w[k], dt) for k in _WAVE_KEYS}
+    H, C, E = wave_dims(ww)
+    T = x.shape[0]
+    hd = E // H
+    ph_in = _c(phase_in, dt) if phase_in is not None else None
+    g = dict(d_x=np.empty((T, E), dt), d_hraw=np.empty(H, dt), d_proj_w=np.empty((H, 2 + C, E), dt),
+             d_proj_b=np.empty((H, 2 + C), dt), d_v_w=np.empty((H, hd, hd), dt), d_v_b=np.empty((H, hd), dt),
+             d_out_w=np.empty((E, E), dt), d_out_b=np.empty(E, dt))
+    _wave_fn("wao_wave_bwd", precision)(
+        _ptr(x), T, E, H, C, *(_ptr(ww[k]) for k in _WAVE_KEYS), _ptr(ph_in), _ptr(d_out),
+        *(_ptr(g[k]) for k in ("d_x", "d_hraw", "d_proj_w", "d_proj_b", "d_v_w", "d_v_b", "d_out_w", "d_out_b")))
+    return g
+
+
+def out_proj_backward(d_attn_out, merged, W, precision: str = "f32"):
+    """out_proj_backward (attn_backward.rs:17-50): (d_out, d_w, d_b)."""
+    dt = _dt(precision)
+    d_attn_out, merged, W = (_c(a, dt) for a in (d_attn_out, merged, W))
+    T, E = d_attn_out.shape
+    d_out, d_w, d_b = np.empty((T, E), dt), np.empty((E, E), dt), np.empty(E, dt)
+    _wave_fn("wao_out_proj_backward", precision)(_ptr(d_attn_out), _ptr(merged), _ptr(W), T, E, _ptr(d_out),
+                                                 _ptr(d_w), _ptr(d_b))
+    return d_out, d_w, d_b
+
+
+def value_aggregation_backward(d_head, att, v, precision: str = "f32"):
+    """value_aggregation_backward (attn_backward.rs:72-103): (d_att, d_v)."""
+    dt = _dt(precision)
+    d_head, att, v = (_c(a, dt) for a in (d_head, att, v))
+    T, hd = d_head.shape
+    d_att, d_v = np.empty((T, T), dt), np.empty((T, hd), dt)
+    _wave_fn("wao_value_aggregation_backward", precision)(_ptr(d_head), _ptr(att), _ptr(v), T, hd, _ptr(d_att),
+                                                          _ptr(d_v))
+    return d_att, d_v
+
+
+def wave_softmax_backward(d_att, att, precision: str = "f32"):
+    """softmax_backward (attn_backward.rs:109-122) on [T][T]."""
+    dt = _dt(precision)
+    d_att, att = _c(d_att, dt), _c(att, dt)
+    T = att.shape[0]
+    out = np.empty((T, T), dt)
+    _wave_fn("wao_wave_softmax_backward", precision)(_ptr(d_att), _ptr(att), T, _ptr(out))
+    return out
+
+
+def score_backward(d_scores, phases, n, att, cv=None, cs=0.0, precision: str = "f32"):
+    """score_backward (attn_backward.rs:128-163): (d_delta, d_content or None, d_n)."""
+    dt = _dt(precision)
+    real = ctypes.c_float if precision == "f32" else ctypes.c_double
+    d_scores, phases, att = (_c(a, dt) for a in (d_scores, phases, att))
+    T = phases.shape[0]
+    cvv = _c(cv, dt) if cv is not None else None
+    C = cvv.shape[1] if cvv is not None else 0
+    d_delta = np.empty((T, T), dt)
+    d_c = np.empty((T, max(C, 1)), dt)
+    f = _wave_fn("wao_score_backward", precision, real)
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, real, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, real,
+                  ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    d_n = f(_ptr(d_scores), _ptr(phases), n, _ptr(att), _ptr(cvv), C, cs, T, _ptr(d_delta), _ptr(d_c))
+    return d_delta, (d_c[:, :C] if cvv is not None else None), float(d_n)
+
+
+def phase_subtraction_backward(d_delta, att, precision: str = "f32"):
+    dt = _dt(precision)
+    d_delta, att = _c(d_delta, dt), _c(att, dt)
+    T = att.shape[0]
+    out = np.empty(T, dt)
+    _wave_fn("wao_phase_subtraction_backward", precision)(_ptr(d_delta), _ptr(att), T, _ptr(out))
+    return out
+
+
+def phase_projection_backward(d_phases, x, pw, pb, precision: str = "f32"):
+    """phase_projection_backward (attn_backward.rs:190-231): (d_x, d_w, d_b)."""
+    dt = _dt(precision)
+    d_phases, x, pw, pb = (_c(a, dt) for a in (d_phases, x, pw, pb))
+    T, E = x.shape
+    d_x, d_w, d_b = np.empty((T, E), dt), np.empty((2, E), dt), np.empty(2, dt)
+    _wave_fn("wao_phase_projection_backward", precision)(_ptr(d_phases), _ptr(x), _ptr(pw), _ptr(pb), T, E,
+                                                         _ptr(d_x), _ptr(d_w), _ptr(d_b))
+    return d_x, d_w, d_b
+
+
+def value_projection_backward(d_v, x, offset, vw, precision: str = "f32"):
+    """value_projection_backward (attn_backward.rs:237-263): (d_x, d_w, d_b)."""
+    dt = _dt(precision)
+    d_v, x, vw = (_c(a, dt) for a in (d_v, x, vw))
+    T, E = x.shape
+    hd = d_v.shape[1]
+    d_x, d_w, d_b = np.empty((T, E), dt), np.empty((hd, hd), dt), np.empty(hd, dt)
+    _wave_fn("wao_value_projection_backward", precision)(_ptr(d_v), _ptr(x), offset, hd, E, _ptr(vw), T,
+                                                         _ptr(d_x), _ptr(d_w), _ptr(d_b))
+    return d_x, d_w, d_b
+
+
+def content_projection_backward(d_cv, x, cw, precision: str = "f32"):
+    """content_projection_backward (attn_backward.rs:269-294): (d_x, d_w, d_b)."""
+    dt = _dt(precision)
+    d_cv, x, cw = (_c(a, dt) for a in (d_cv, x, cw))
+    T, E = x.shape
+    C = cw.shape[0]
+    d_x, d_w, d_b = np.empty((T, E), dt), np.empty((C, E), dt), np.empty(C, dt)
+    _wave_fn("wao_content_projection_backward", precision)(_ptr(d_cv), _ptr(x), _ptr(cw), T, E, C, _ptr(d_x),
+                                                           _ptr(d_w), _ptr(d_b))
+    return d_x, d_w, d_b
+
+
+def combine_d_normed(d_phase, d_v, d_content=None, precision: str = "f32"):
+    """combine_d_normed (attn_backward.rs:299-323): inputs [H][T][E]."""
+    dt = _dt(precision)
+    d_phase, d_v = _c(d_phase, dt), _c(d_v, dt)
+    H, T, E = d_phase.shape
+    dc = _c(d_content, dt) if d_content is not None and len(d_content) else None
+    out = np.empty((T, E), dt)
+    _wave_fn("wao_combine_d_normed", precision)(_ptr(d_phase), _ptr(d_v), _ptr(dc), H, T, E, _ptr(out))
+    return out

@@ -16,6 +16,9 @@
  *   src/cpu/backward.rs:313-363     attention_backward_single
  *   src/common/math/attn_backward.rs:109-122  softmax_backward (same algebra)
  *   src/common/rng.rs:24-34         xorshift64 next_u64 / next_f32
+ *   src/common/attn.rs:72-430       wave (harmonic coherence) attention forward
+ *                                   and full backward (wave_core.inc)
+ *   src/common/math/attn_backward.rs:13-323  its backward primitives
  * The Box-Muller normal draw is this build's own definition (the reference
  * has no normal sampler, src/common/rng.rs:5-45).
  */
@@ -32,7 +35,20 @@
 #define LOGF logf
 #define SQRTF sqrtf
 #define MAXF fmaxf
+#define FABSF fabsf
+#define ATAN2F atan2f
+#define COSF cosf
+#define SINF sinf
+#define FMODF fmodf
+#define WAVE_TAU 6.2831853071795864769f /* std::f32::consts::TAU */
 #include "oracle_core.inc"
+#include "wave_core.inc"
+#undef FABSF
+#undef ATAN2F
+#undef COSF
+#undef SINF
+#undef FMODF
+#undef WAVE_TAU
 #undef REAL
 #undef FN
 #undef EXPF
@@ -47,7 +63,20 @@
 #define LOGF log
 #define SQRTF sqrt
 #define MAXF fmax
+#define FABSF fabs
+#define ATAN2F atan2
+#define COSF cos
+#define SINF sin
+#define FMODF fmod
+#define WAVE_TAU 6.2831853071795864769
 #include "oracle_core.inc"
+#include "wave_core.inc"
+#undef FABSF
+#undef ATAN2F
+#undef COSF
+#undef SINF
+#undef FMODF
+#undef WAVE_TAU
 #undef REAL
 #undef FN
 #undef EXPF

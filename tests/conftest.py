@@ -41,3 +41,21 @@ def assert_parity(name, got, want, max_abs=MAX_ABS, rel_l2=REL_L2):
     assert np.isfinite(ma) and ma <= max_abs and rl <= rel_l2, \
         f"{name}: max_abs={ma:.3e} (<= {max_abs:g}) rel_l2={rl:.3e} (<= {rel_l2:g})"
     return ma, rl
+
+
+def make_wave_weights(H, C, E, seed, dtype=np.float32):
+    """Wave-attention weights in the packed layout (harmonic_raw, proj_w
+    [H][2+C][E], proj_b, v_w [H][hd][hd], v_b, out_w [E][E], out_b), scaled so
+    that projections of a unit-variance input are O(1)."""
+    rng = np.random.default_rng(seed)
+    hd = E // H
+    w = dict(
+        hraw=rng.normal(0.5, 1.0, size=H),
+        proj_w=rng.normal(0, 1.0 / np.sqrt(E), size=(H, 2 + C, E)),
+        proj_b=rng.normal(0, 0.1, size=(H, 2 + C)),
+        v_w=rng.normal(0, 1.0 / np.sqrt(hd), size=(H, hd, hd)),
+        v_b=rng.normal(0, 0.1, size=(H, hd)),
+        out_w=rng.normal(0, 1.0 / np.sqrt(E), size=(E, E)),
+        out_b=rng.normal(0, 0.1, size=E),
+    )
+    return {k: v.astype(dtype) for k, v in w.items()}

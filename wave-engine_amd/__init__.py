@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "wha_attn_fwd", "wha_attn_bwd_workspace_size", "wha_attn_bwd",
     "wha_attn_bwd_from_probs_workspace_size", "wha_attn_bwd_from_probs",
     "wha_decode_workspace_size", "wha_decode_fwd", "wha_attn_probs_rows",
+    "wha_wave_fwd", "wha_wave_bwd_workspace_size", "wha_wave_bwd", "wha_wave_probs_rows",
     "wha_linear_fwd", "wha_linear_bwd_dx", "wha_linear_bwd_dw_workspace_size", "wha_linear_bwd_dw",
     "wha_host_attention_core_fwd", "wha_host_attention_backward", "wha_host_attention",
     "wha_synth_normal",
@@ -58,6 +59,25 @@ class WaveLayout(ctypes.Structure):
     def __repr__(self):
         return (f"WaveLayout(B={self.B}, H={self.H}, T={self.T}, D={self.D}, "
                 f"strides=({self.stride_b}, {self.stride_h}, {self.stride_t}))")
+
+
+class WaveShape(ctypes.Structure):
+    """wha_wave_shape."""
+    _fields_ = [("B", ctypes.c_int32), ("T", ctypes.c_int32), ("n_embd", ctypes.c_int32),
+                ("n_head", ctypes.c_int32), ("content_dim", ctypes.c_int32)]
+
+
+class _WaveWeightsC(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("harmonic_raw", "proj_w", "proj_b", "v_w", "v_b", "out_w", "out_b")]
+
+
+class _WaveCacheC(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("proj", "values", "feat", "phase", "bucket", "merged", "lse")]
+
+
+class _WaveGradsC(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("d_x", "d_harmonic_raw", "d_proj_w", "d_proj_b", "d_v_w", "d_v_b",
+                                                "d_out_w", "d_out_b")]
 
 
 def layout_bhtd(B, H, T, D) -> WaveLayout:
@@ -119,6 +139,13 @@ def lib():
         L.wha_host_attention_core_fwd.argtypes = [f32p, f32p, f32p, i32, i32, i32, f32p]
         L.wha_host_attention_backward.argtypes = [f32p] * 5 + [i32, i32, i32] + [f32p] * 3
         L.wha_attn_probs_rows.argtypes = [vp, vp, vp, ctypes.POINTER(ctypes.c_int32), i32, vp, lp, ctypes.c_float, vp]
+        wsp, wwp = ctypes.POINTER(WaveShape), ctypes.POINTER(_WaveWeightsC)
+        wcp, wgp = ctypes.POINTER(_WaveCacheC), ctypes.POINTER(_WaveGradsC)
+        L.wha_wave_fwd.argtypes = [vp, wwp, wsp, vp, wcp, vp]
+        L.wha_wave_bwd_workspace_size.argtypes = [wsp]
+        L.wha_wave_bwd_workspace_size.restype = sz
+        L.wha_wave_bwd.argtypes = [vp, vp, wwp, wsp, wcp, wgp, vp, sz, vp]
+        L.wha_wave_probs_rows.argtypes = [wcp, wsp, ctypes.POINTER(ctypes.c_int32), i32, vp, vp]
         L.wha_synth_normal.argtypes = [ctypes.POINTER(ctypes.c_uint64), f32p, sz, ctypes.c_double, ctypes.c_int]
         L.wha_synth_normal.restype = ctypes.c_int
         L.wha_timing_enable.argtypes = [ctypes.c_int]
@@ -481,6 +508,199 @@ class HipBackend:
 
 
 # ------------------------------------------------------------------ synthetic inputs
+
+# ------------------------------------------------------------------ wave attention
+# Mirror of the harmonic coherence attention interface (src/common/attn.rs:17-511):
+# the same names, weights and results, on device tensors, batched over B
+# sequences.  Weight layout: include/wave_hip_attn.h (wha_wave_weights).
+
+class WaveAttnWeights:
+    """WaveAttnWeights (src/common/attn.rs:39-46) for all heads, as device
+    float32 tensors: harmonic_raw [H], proj_w [H][2+C][E] (phase rows r, s then
+    content rows), proj_b [H][2+C], v_w [H][hd][hd], v_b [H][hd], out_w [E][E],
+    out_b [E]."""
+
+    _NAMES = ("harmonic_raw", "proj_w", "proj_b", "v_w", "v_b", "out_w", "out_b")
+
+    def __init__(self, harmonic_raw, proj_w, proj_b, v_w, v_b, out_w, out_b):
+        torch = _torch()
+        vals = (harmonic_raw, proj_w, proj_b, v_w, v_b, out_w, out_b)
+        for name, t in zip(self._NAMES, vals):
+            if not (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
+                raise ValueError(f"{name} must be a contiguous float32 device tensor")
+            setattr(self, name, t)
+        H, P, E = proj_w.shape
+        hd = E // H if H else 0
+        want = {"harmonic_raw": (H,), "proj_b": (H, P), "v_w": (H, hd, hd), "v_b": (H, hd), "out_w": (E, E),
+                "out_b": (E,)}
+        for name, shp in want.items():
+            if tuple(getattr(self, name).shape) != shp:
+                raise ValueError(f"{name}: expected shape {shp}, got {tuple(getattr(self, name).shape)}")
+        if H == 0 or E % H:
+            raise ValueError(f"n_embd {E} is not divisible by n_head {H}")
+        self.n_head, self.content_dim, self.n_embd = H, P - 2, E
+
+    @classmethod
+    def from_heads(cls, heads, out_proj_w, out_proj_b, device="cuda"):
+        """From the reference's per-head fields (WaveAttnHeadWeights,
+        attn.rs:17-37): each head a mapping with harmonic_raw, phase_proj_w [2][E],
+        phase_proj_b [2], v_proj_w [hd][hd], v_proj_b [hd], content_proj_w [C][E]
+        (empty: no content projection) and content_proj_b [C]."""
+        torch = _torch()
+        f = lambda a: np.asarray(a, dtype=np.float32)
+        cdims = {len(h.get("content_proj_w", [])) for h in heads}
+        if len(cdims) != 1:
+            raise ValueError("every head must have the same content_dim")
+        rows_w, rows_b = [], []
+        for h in heads:
+            cw = f(h.get("content_proj_w", [])).reshape(-1, f(h["phase_proj_w"]).shape[1])
+            rows_w.append(np.concatenate([f(h["phase_proj_w"]), cw], axis=0))
+            rows_b.append(np.concatenate([f(h["phase_proj_b"]), f(h.get("content_proj_b", []))]))
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(device)
+        return cls(t([h["harmonic_raw"] for h in heads]), t(np.stack(rows_w)), t(np.stack(rows_b)),
+                   t(np.stack([f(h["v_proj_w"]) for h in heads])), t(np.stack([f(h["v_proj_b"]) for h in heads])),
+                   t(out_proj_w), t(out_proj_b))
+
+    def _c(self):
+        return _WaveWeightsC(*(t.data_ptr() for t in (getattr(self, n) for n in self._NAMES)))
+
+
+class WaveAttnCache:
+    """Forward intermediates (the role of WaveAttnCache, attn.rs:48-70) on the
+    device; ``normed`` is the input the forward read, as in the reference."""
+
+    def __init__(self, shape: WaveShape, device):
+        torch = _torch()
+        B, T, E, H, C = shape.B, shape.T, shape.n_embd, shape.n_head, shape.content_dim
+        e = lambda *s, dt=torch.float32: torch.empty(*s, dtype=dt, device=device)
+        self.shape = shape
+        self.proj = e(B, T, H, 2 + C)
+        self.values = e(B, T, E)
+        self.feat = e(B, H, T, 32)
+        self.phase = e(B, H, T)
+        self.bucket = e(B, H, T, dt=torch.int32)
+        self.merged = e(B, T, E)
+        self.lse = e(B, H, T)
+        self.normed = None
+
+    def _c(self):
+        return _WaveCacheC(*(t.data_ptr() for t in (self.proj, self.values, self.feat, self.phase, self.bucket,
+                                                     self.merged, self.lse)))
+
+
+class WaveAttnGrads:
+    """WaveAttnGrads (attn.rs:328-336): per-head weight gradients in the packed
+    layout of WaveAttnWeights (summed over the batch), out_proj gradients and
+    d_normed."""
+
+    def __init__(self, d_normed, d_harmonic_raw, d_proj_w, d_proj_b, d_v_w, d_v_b, out_proj_w, out_proj_b):
+        self.d_normed, self.d_harmonic_raw = d_normed, d_harmonic_raw
+        self.d_proj_w, self.d_proj_b, self.d_v_w, self.d_v_b = d_proj_w, d_proj_b, d_v_w, d_v_b
+        self.out_proj_w, self.out_proj_b = out_proj_w, out_proj_b
+
+
+class WaveAttnRows:
+    """Lazy view of att_weights_all: rows are recomputed on the device from the
+    cache (the forward never materialises [H][T][T])."""
+
+    def __init__(self, cache: WaveAttnCache):
+        self.cache = cache
+
+    def rows(self, rows):
+        return wave_probs_rows(self.cache, rows)
+
+    def last_rows(self):
+        """[B][H][T]: the row attn_monitor reads (src/monitors/attn_monitor.rs:26-80)."""
+        return self.rows([self.cache.shape.T - 1])[:, :, 0, :]
+
+
+def _wave_x(x, weights: WaveAttnWeights):
+    torch = _torch()
+    if x.dim() == 2:
+        x = x.unsqueeze(0)
+    if x.dim() != 3 or x.shape[2] != weights.n_embd:
+        raise ValueError(f"x must be [B][T][{weights.n_embd}] (or [T][{weights.n_embd}]), got {tuple(x.shape)}")
+    if not (x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()):
+        raise ValueError("x must be a contiguous float32 device tensor")
+    return x
+
+
+def wave_attention_forward(weights: WaveAttnWeights, x, n_bands=None, return_pathway_cache=True, out=None):
+    """wave_attention_forward (src/common/attn.rs:90-305) on x [B][T][n_embd]
+    (or one sequence [T][n_embd]).  Returns (out, att_weights, cache): att_weights
+    is a WaveAttnRows view; cache is None unless return_pathway_cache."""
+    torch = _torch()
+    x = _wave_x(x, weights)
+    if n_bands is not None and 2 * n_bands != weights.n_embd:
+        raise ValueError(f"n_bands {n_bands} does not match n_embd {weights.n_embd}")
+    B, T, E = x.shape
+    shape = WaveShape(B, T, E, weights.n_head, weights.content_dim)
+    cache = WaveAttnCache(shape, x.device)
+    cache.normed = x
+    if out is None:
+        out = torch.empty_like(x)
+    _check("wha_wave_fwd", lib().wha_wave_fwd(_ptr(x), ctypes.byref(weights._c()), ctypes.byref(shape), _ptr(out),
+                                               ctypes.byref(cache._c()), _stream_ptr(x)))
+    return out, WaveAttnRows(cache), (cache if return_pathway_cache else None)
+
+
+def wave_bwd_workspace_bytes(shape: WaveShape) -> int:
+    return int(lib().wha_wave_bwd_workspace_size(ctypes.byref(shape)))
+
+
+def _wave_bwd(weights, cache, d_attn_out, full, workspace=None):
+    torch = _torch()
+    if cache is None or cache.normed is None:
+        raise ValueError("the backward needs the forward's pathway cache")
+    x = cache.normed
+    d = d_attn_out.unsqueeze(0) if d_attn_out.dim() == 2 else d_attn_out
+    if tuple(d.shape) != tuple(x.shape) or not d.is_contiguous() or d.dtype != torch.float32:
+        raise ValueError(f"d_attn_out must be a contiguous float32 tensor of shape {tuple(x.shape)}")
+    H, C, E = weights.n_head, weights.content_dim, weights.n_embd
+    hd = E // H
+    dev = x.device
+    z = lambda *s: torch.empty(*s, dtype=torch.float32, device=dev)
+    d_x = torch.empty_like(x)
+    g = dict(d_harmonic_raw=z(H), d_proj_w=z(H, 2 + C, E), d_proj_b=z(H, 2 + C), d_v_w=z(H, hd, hd),
+             d_v_b=z(H, hd), d_out_w=z(E, E), d_out_b=z(E)) if full else {}
+    gc = _WaveGradsC(d_x.data_ptr(), *((g[k].data_ptr() if full else None) for k in
+                                      ("d_harmonic_raw", "d_proj_w", "d_proj_b", "d_v_w", "d_v_b", "d_out_w",
+                                       "d_out_b")))
+    shape = cache.shape
+    ws = workspace
+    if ws is None:
+        ws = torch.empty(wave_bwd_workspace_bytes(shape) // 4 + 64, dtype=torch.float32, device=dev)
+    _check("wha_wave_bwd", lib().wha_wave_bwd(_ptr(x), _ptr(d), ctypes.byref(weights._c()), ctypes.byref(shape),
+                                               ctypes.byref(cache._c()), ctypes.byref(gc), _ptr(ws),
+                                               ws.numel() * 4, _stream_ptr(x)))
+    if not full:
+        return d_x
+    return WaveAttnGrads(d_x, g["d_harmonic_raw"], g["d_proj_w"], g["d_proj_b"], g["d_v_w"], g["d_v_b"],
+                         g["d_out_w"], g["d_out_b"])
+
+
+def wave_attention_backward_full(weights: WaveAttnWeights, cache: WaveAttnCache, d_attn_out, workspace=None):
+    """wave_attention_backward_full (attn.rs:346-430): WaveAttnGrads."""
+    return _wave_bwd(weights, cache, d_attn_out, True, workspace)
+
+
+def wave_attention_backward_pathway(weights: WaveAttnWeights, cache: WaveAttnCache, d_attn_out, workspace=None):
+    """wave_attention_backward_pathway (attn.rs:432-511): d_normed only."""
+    return _wave_bwd(weights, cache, d_attn_out, False, workspace)
+
+
+def wave_probs_rows(cache: WaveAttnCache, rows):
+    """Rows of att_weights_all from the cache: [B][H][len(rows)][T] (0 where
+    the bucket mask excludes a key, -inf after the diagonal)."""
+    torch = _torch()
+    rows = [int(r) for r in rows]
+    arr = (ctypes.c_int32 * len(rows))(*rows)
+    sh = cache.shape
+    out = torch.empty(sh.B, sh.n_head, len(rows), sh.T, dtype=torch.float32, device=cache.lse.device)
+    _check("wha_wave_probs_rows", lib().wha_wave_probs_rows(ctypes.byref(cache._c()), ctypes.byref(sh), arr,
+                                                             len(rows), _ptr(out), _stream_ptr(out)))
+    return out
+
 
 class SynthStream:
     """Seeded normal draws from the library's generator: xorshift64 exactly as

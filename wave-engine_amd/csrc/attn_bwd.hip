@@ -38,12 +38,6 @@ namespace wha {
 
 enum DqMode { kFused = 0, kProbs = 1, kDeltaFromProbs = 2 };
 
-// First row of dS column block kt: sum_{j<kt} (T - 64 j).
-__host__ __device__ __forceinline__ int64_t ds_block_row(int kt, int T) {
-  return (int64_t)kt * T - (int64_t)32 * kt * (kt - 1);
-}
-// Rows of dS per (b,h).
-__host__ __device__ __forceinline__ int64_t ds_rows(int T) { return ds_block_row((T + 63) / 64, T); }
 
 // Delta_t = sum_d dO[t][d] * O[t][d]; 16 lanes per row, 16 rows per block.
 __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const float* __restrict__ O,
@@ -545,6 +539,27 @@ hipError_t bwd_probs_t(const float* d_o, const float* q, const float* k, const f
 }  // namespace
 
 size_t bwd_ds_floats(const View& L) { return (size_t)L.B * L.H * (size_t)ds_rows(L.T) * 64; }
+
+hipError_t launch_attn_bwd_delta(const float* o, const float* d_o, float* delta, const View& L, const char* name,
+                                 hipStream_t stream) {
+  const int64_t rows = (int64_t)L.B * L.H * L.T;
+  TimingScope ts(name, stream);
+  hipLaunchKernelGGL(attn_bwd_delta_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, stream, o, d_o,
+                     delta, L);
+  return hipGetLastError();
+}
+
+hipError_t launch_dq_from_ds(const float* k, const float* ds, float* dq, const View& L, float scale,
+                             const char* name, hipStream_t stream) {
+  // instantiated for the 32-wide wave-attention features (16-byte aligned rows)
+  if (L.D != kWaveFeatures) return hipErrorInvalidValue;
+  constexpr int NWD = WHA_DQ_NW;
+  const int n_qt = (L.T + NWD * 16 - 1) / (NWD * 16);
+  TimingScope ts(name, stream);
+  hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<kWaveFeatures, NWD, true>), dim3((unsigned)(n_qt * L.B * L.H)),
+                     dim3(NWD * 64), 0, stream, k, ds, dq, L, scale);
+  return hipGetLastError();
+}
 
 hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const float* o,
                            const float* d_o, const float* lse, float* dq, float* dk, float* dv,

@@ -36,7 +36,11 @@ struct GemmArgs {
   const float* bias;   // [N] or nullptr
   int M, N, K;
   int k_chunk;         // k range per split (multiple of 16)
-  bool c_vec;          // c and ldc allow 128-bit stores
+  bool c_vec;          // c, ldc and c_sb allow 128-bit stores
+  bool accumulate;     // C += result instead of C = result
+  int batch = 1;       // independent GEMMs, operands offset by the strides below
+  int splits = 1;      // blockIdx.z = batch index * splits + split index
+  int64_t a_sb = 0, b_sb = 0, c_sb = 0, bias_sb = 0;
 };
 
 // Staging of one 128 x 16 operand tile (rows r = m or n, k contiguous in LDS);
@@ -111,7 +115,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   const int lq = lane & 15, gq = lane >> 4;
   const int wn = wave & 1, wm = wave >> 1;
   const int n0 = blockIdx.x * kGBN, m0 = blockIdx.y * kGBM;
-  const int k_begin = blockIdx.z * g.k_chunk;
+  const int bt = (int)blockIdx.z / g.splits;
+  const int k_begin = ((int)blockIdx.z % g.splits) * g.k_chunk;
+  const float* __restrict__ A = g.a + bt * g.a_sb;
+  const float* __restrict__ Bm = g.b + bt * g.b_sb;
   const int k_end = min(g.K, k_begin + g.k_chunk);
 
   floatx4 acc[4][4];
@@ -123,8 +130,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   GemmStage<A_KC> sa;
   GemmStage<B_KC> sb;
   if (k_begin < k_end) {
-    sa.load(g.a, g.a_sm, g.a_sk, m0, g.M, k_begin, k_end, tid);
-    sb.load(g.b, g.b_sn, g.b_sk, n0, g.N, k_begin, k_end, tid);
+    sa.load(A, g.a_sm, g.a_sk, m0, g.M, k_begin, k_end, tid);
+    sb.load(Bm, g.b_sn, g.b_sk, n0, g.N, k_begin, k_end, tid);
   }
   for (int kk = k_begin; kk < k_end; kk += kGKT) {
     __syncthreads();
@@ -132,8 +139,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     sb.store(Bs, tid);
     __syncthreads();
     if (kk + kGKT < k_end) {
-      sa.load(g.a, g.a_sm, g.a_sk, m0, g.M, kk + kGKT, k_end, tid);
-      sb.load(g.b, g.b_sn, g.b_sk, n0, g.N, kk + kGKT, k_end, tid);
+      sa.load(A, g.a_sm, g.a_sk, m0, g.M, kk + kGKT, k_end, tid);
+      sb.load(Bm, g.b_sn, g.b_sk, n0, g.N, kk + kGKT, k_end, tid);
     }
     float4 bv[4], av[4];
 #pragma unroll
@@ -166,18 +173,33 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
       if (n >= g.N) continue;
       float4 r = make_float4(acc[nt][mt][0], acc[nt][mt][1], acc[nt][mt][2], acc[nt][mt][3]);
       float* dst;
+      const bool vec = PARTIAL ? (g.N % 4 == 0) : g.c_vec;
       if (PARTIAL) {
         dst = g.c + ((int64_t)blockIdx.z * g.M + m) * g.N + n;
       } else {
-        dst = g.c + (int64_t)m * g.ldc + n;
+        dst = g.c + bt * g.c_sb + (int64_t)m * g.ldc + n;
         if (g.bias != nullptr) {
-          r.x = (n + 0 < g.N ? g.bias[n + 0] : 0.f) + r.x;
-          r.y = (n + 1 < g.N ? g.bias[n + 1] : 0.f) + r.y;
-          r.z = (n + 2 < g.N ? g.bias[n + 2] : 0.f) + r.z;
-          r.w = (n + 3 < g.N ? g.bias[n + 3] : 0.f) + r.w;
+          const float* bias = g.bias + bt * g.bias_sb;
+          r.x = (n + 0 < g.N ? bias[n + 0] : 0.f) + r.x;
+          r.y = (n + 1 < g.N ? bias[n + 1] : 0.f) + r.y;
+          r.z = (n + 2 < g.N ? bias[n + 2] : 0.f) + r.z;
+          r.w = (n + 3 < g.N ? bias[n + 3] : 0.f) + r.w;
+        }
+        if (g.accumulate) {
+          if (vec && n + 3 < g.N) {
+            const float4 o = *reinterpret_cast<const float4*>(dst);
+            r.x += o.x;
+            r.y += o.y;
+            r.z += o.z;
+            r.w += o.w;
+          } else {
+            r.x += dst[0];
+            if (n + 1 < g.N) r.y += dst[1];
+            if (n + 2 < g.N) r.z += dst[2];
+            if (n + 3 < g.N) r.w += dst[3];
+          }
         }
       }
-      const bool vec = PARTIAL ? (g.N % 4 == 0) : g.c_vec;
       if (vec && n + 3 < g.N) {
         *reinterpret_cast<float4*>(dst) = r;
       } else {
@@ -190,17 +212,19 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   }
 }
 
-// C[m][n] = bias[n] + sum_z part[z][m][n], z in increasing order.
-__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part, int splits,
-                                                                 const float* __restrict__ bias,
-                                                                 float* __restrict__ c, int64_t ldc, int M,
-                                                                 int N) {
+// C[bt][m][n] (+)= bias[bt][n] + sum_s part[bt*splits + s][m][n], s in increasing order.
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part, GemmArgs g) {
+  const int64_t MN = (int64_t)g.M * g.N;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)M * N) return;
-  const int m = (int)(i / N), n = (int)(i % N);
+  if (i >= MN * g.batch) return;
+  const int bt = (int)(i / MN);
+  const int64_t e = i - bt * MN;
+  const int m = (int)(e / g.N), n = (int)(e % g.N);
   float s = 0.f;
-  for (int z = 0; z < splits; ++z) s += part[(int64_t)z * M * N + i];
-  c[(int64_t)m * ldc + n] = (bias != nullptr ? bias[n] : 0.f) + s;
+  for (int z = 0; z < g.splits; ++z) s += part[((int64_t)bt * g.splits + z) * MN + e];
+  float* dst = g.c + bt * g.c_sb + (int64_t)m * g.ldc + n;
+  const float r = (g.bias != nullptr ? g.bias[bt * g.bias_sb + n] : 0.f) + s;
+  *dst = g.accumulate ? *dst + r : r;
 }
 
 // out[n] = sum_m y[m][n] (column sums, for the bias gradient): rows split over
@@ -226,8 +250,8 @@ __global__ __launch_bounds__(256) void colsum_final_kernel(const float* __restri
 
 namespace {
 
-int gemm_splits(int M, int N, int K) {
-  const int tiles = ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
+int gemm_splits(int M, int N, int K, int batch) {
+  const int tiles = ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN) * batch;
   int splits = 1;
   // aim for >= 512 blocks while keeping >= 256 k per split
   while (tiles * splits < 512 && (K / (splits * 2)) >= 256) splits *= 2;
@@ -238,8 +262,9 @@ int colsum_chunks(int M) { return M >= 4096 ? 64 : (M >= 256 ? 16 : 1); }
 
 template <bool A_KC, bool B_KC>
 hipError_t gemm_t(GemmArgs g, float* ws, const char* name, hipStream_t stream) {
-  const int splits = ws ? gemm_splits(g.M, g.N, g.K) : 1;
-  const dim3 grid((g.N + kGBN - 1) / kGBN, (g.M + kGBM - 1) / kGBM, splits);
+  const int splits = ws ? gemm_splits(g.M, g.N, g.K, g.batch) : 1;
+  g.splits = splits;
+  const dim3 grid((g.N + kGBN - 1) / kGBN, (g.M + kGBM - 1) / kGBM, splits * g.batch);
   TimingScope ts(name, stream);
   if (splits == 1) {
     g.k_chunk = ((g.K + kGKT - 1) / kGKT) * kGKT;
@@ -254,9 +279,9 @@ hipError_t gemm_t(GemmArgs g, float* ws, const char* name, hipStream_t stream) {
   hipLaunchKernelGGL((gemm_kernel<A_KC, B_KC, true>), grid, dim3(256), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int64_t total = (int64_t)g.M * g.N;
+  const int64_t total = (int64_t)g.M * g.N * g.batch;
   hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
-                     (const float*)ws, splits, g.bias, g.c, g.ldc, g.M, g.N);
+                     (const float*)ws, g);
   return hipGetLastError();
 }
 
@@ -264,46 +289,90 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 }  // namespace
 
-size_t linear_dw_workspace_floats(int N, int K, int64_t M) {
-  // split-K partials of the [N][K] weight gradient plus column-sum partials
-  const int splits = gemm_splits(N, K, (int)(M > 0x7fffffff ? 0x7fffffff : M));
-  const size_t part = splits > 1 ? (size_t)splits * N * K : 0;
-  return part + (size_t)colsum_chunks((int)M) * N + 64;
+size_t linear_dw_workspace_floats(int N, int K, int64_t M, int batch) {
+  // split-K partials of the [batch][N][K] weight gradient plus column-sum partials
+  const int splits = gemm_splits(N, K, (int)(M > 0x7fffffff ? 0x7fffffff : M), batch);
+  const size_t part = splits > 1 ? (size_t)splits * batch * N * K : 0;
+  return part + (size_t)colsum_chunks((int)M) * N * batch + 64;
 }
+
+// y[bt] = x[bt] w[bt]^T + b[bt]:  x [M][K] (row stride ldx), w [N][K], y [M][N] (row stride ldy)
+hipError_t launch_linear_fwd_batched(const float* x, int64_t ldx, int64_t x_sb, const float* w, int64_t w_sb,
+                                     const float* b, int64_t b_sb, float* y, int64_t ldy, int64_t y_sb, int M,
+                                     int N, int K, int batch, hipStream_t stream) {
+  GemmArgs g{x, ldx, 1, w, (int64_t)K, 1, y, ldy, b, M, N, K, 0,
+             aligned16(y) && ldy % 4 == 0 && y_sb % 4 == 0, false};
+  g.batch = batch;
+  g.a_sb = x_sb;
+  g.b_sb = w_sb;
+  g.c_sb = y_sb;
+  g.bias_sb = b_sb;
+  return gemm_t<true, true>(g, nullptr, "linear_fwd", stream);
+}
+
+// dx[bt] (+)= dy[bt] w[bt]:  dy [M][N], w [N][K], dx [M][K]
+hipError_t launch_linear_bwd_dx_batched(const float* dy, int64_t lddy, int64_t dy_sb, const float* w,
+                                        int64_t w_sb, float* dx, int64_t lddx, int64_t dx_sb, int M, int N,
+                                        int K, int batch, bool accumulate, hipStream_t stream) {
+  // dx[m][k] = sum_n dy[m][n] w[n][k]: GEMM with (M, N=K_in, K=N_out)
+  GemmArgs g{dy, lddy, 1, w, 1, (int64_t)K, dx, lddx, nullptr, M, K, N, 0,
+             aligned16(dx) && lddx % 4 == 0 && dx_sb % 4 == 0, accumulate};
+  g.batch = batch;
+  g.a_sb = dy_sb;
+  g.b_sb = w_sb;
+  g.c_sb = dx_sb;
+  return gemm_t<true, false>(g, nullptr, "linear_bwd_dx", stream);
+}
+
+// dw[bt] = dy[bt]^T x[bt] over the M rows:  dy [M][N], x [M][K], dw [N][K];
+// db[bt*N + n] = sum_m dy[bt][m][n] when db != nullptr.  ws: linear_dw_workspace_floats.
+hipError_t launch_linear_bwd_dw_batched(const float* dy, int64_t lddy, int64_t dy_sb, const float* x,
+                                        int64_t ldx, int64_t x_sb, float* dw, int64_t dw_sb, float* db, int M,
+                                        int N, int K, int batch, float* ws, hipStream_t stream) {
+  // dw[n][k] = sum_m dy[m][n] x[m][k]: GEMM with (M=N_out, N=K_in, K=M rows), both operands
+  // contiguous along the output index
+  GemmArgs g{dy, 1, lddy, x, 1, ldx, dw, (int64_t)K, nullptr, N, K, M, 0,
+             aligned16(dw) && K % 4 == 0 && dw_sb % 4 == 0, false};
+  g.batch = batch;
+  g.a_sb = dy_sb;
+  g.b_sb = x_sb;
+  g.c_sb = dw_sb;
+  const int splits = gemm_splits(N, K, M, batch);
+  float* part = splits > 1 ? ws : nullptr;
+  hipError_t e = gemm_t<false, false>(g, part, "linear_bwd_dw", stream);
+  if (e != hipSuccess || db == nullptr) return e;
+  float* cs = ws + (splits > 1 ? (size_t)splits * batch * N * K : 0);
+  const int chunks = colsum_chunks(M);
+  const int rows_per = (M + chunks - 1) / chunks;
+  TimingScope ts("linear_bwd_db", stream);
+  for (int bt = 0; bt < batch; ++bt) {
+    hipLaunchKernelGGL(colsum_partial_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)chunks), dim3(256), 0,
+                       stream, dy + bt * dy_sb, lddy, M, N, rows_per, cs + (size_t)bt * chunks * N);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, stream,
+                       (const float*)(cs + (size_t)bt * chunks * N), chunks, N, db + (size_t)bt * N);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+size_t linear_dw_workspace_floats(int N, int K, int64_t M) { return linear_dw_workspace_floats(N, K, M, 1); }
 
 hipError_t launch_linear_fwd(const float* x, int64_t ldx, const float* w, const float* b, float* y, int64_t ldy,
                              int M, int N, int K, hipStream_t stream) {
-  GemmArgs g{x, ldx, 1, w, (int64_t)K, 1, y, ldy, b, M, N, K, 0, aligned16(y) && ldy % 4 == 0};
-  return gemm_t<true, true>(g, nullptr, "linear_fwd", stream);
+  return launch_linear_fwd_batched(x, ldx, 0, w, 0, b, 0, y, ldy, 0, M, N, K, 1, stream);
 }
 
 hipError_t launch_linear_bwd_dx(const float* dy, int64_t lddy, const float* w, float* dx, int64_t lddx, int M,
                                 int N, int K, hipStream_t stream) {
-  // dx[m][k] = sum_n dy[m][n] w[n][k]: GEMM with (M, N=K_in, K=N_out)
-  GemmArgs g{dy, lddy, 1, w, 1, (int64_t)K, dx, lddx, nullptr, M, K, N, 0, aligned16(dx) && lddx % 4 == 0};
-  return gemm_t<true, false>(g, nullptr, "linear_bwd_dx", stream);
+  return launch_linear_bwd_dx_batched(dy, lddy, 0, w, 0, dx, lddx, 0, M, N, K, 1, false, stream);
 }
 
 hipError_t launch_linear_bwd_dw(const float* dy, int64_t lddy, const float* x, int64_t ldx, float* dw, float* db,
                                 int M, int N, int K, float* ws, hipStream_t stream) {
-  // dw[n][k] = sum_m dy[m][n] x[m][k]: GEMM with (M=N_out, N=K_in, K=M rows), both operands
-  // contiguous along the output index
-  GemmArgs g{dy, 1, lddy, x, 1, ldx, dw, (int64_t)K, nullptr, N, K, M, 0, aligned16(dw) && K % 4 == 0};
-  const int splits = gemm_splits(N, K, M);
-  float* part = splits > 1 ? ws : nullptr;
-  hipError_t e = gemm_t<false, false>(g, part, "linear_bwd_dw", stream);
-  if (e != hipSuccess || db == nullptr) return e;
-  float* cs = ws + (splits > 1 ? (size_t)splits * N * K : 0);
-  const int chunks = colsum_chunks(M);
-  const int rows_per = (M + chunks - 1) / chunks;
-  TimingScope ts("linear_bwd_db", stream);
-  hipLaunchKernelGGL(colsum_partial_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)chunks), dim3(256), 0,
-                     stream, dy, lddy, M, N, rows_per, cs);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, stream,
-                     (const float*)cs, chunks, N, db);
-  return hipGetLastError();
+  return launch_linear_bwd_dw_batched(dy, lddy, 0, x, ldx, 0, dw, 0, db, M, N, K, 1, ws, stream);
 }
 
 }  // namespace wha

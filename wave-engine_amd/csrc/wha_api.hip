@@ -3,6 +3,7 @@
 // Declarations and contracts: include/wave_hip_attn.h.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -398,6 +399,200 @@ int wha_decode_fwd(const float* q, const float* k_cache, const float* v_cache, f
   const bool vec = vec_ok(V, {k_cache, v_cache});
   hipError_t e = wha::launch_decode(q, k_cache, v_cache, o, lse, static_cast<float*>(ws), V, vec, scale, s);
   if (e != hipSuccess) return hip_fail(e, "wha_decode_fwd launch");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+// ---------------------------------------------------------------- wave attention
+
+static int check_wave_shape(const wha_wave_shape* sh, const char* fn) {
+  if (sh == nullptr) return fail(WHA_ERR_INVALID, "%s: shape is NULL", fn);
+  if (sh->B <= 0 || sh->T <= 0 || sh->n_embd <= 0 || sh->n_head <= 0)
+    return fail(WHA_ERR_INVALID, "%s: B, T, n_embd, n_head must be positive (got %d, %d, %d, %d)", fn, sh->B,
+                sh->T, sh->n_embd, sh->n_head);
+  if (sh->n_embd % sh->n_head != 0)
+    return fail(WHA_ERR_INVALID, "%s: n_embd %d is not divisible by n_head %d", fn, sh->n_embd, sh->n_head);
+  if (wha::padded_dim(sh->n_embd / sh->n_head) == 0)
+    return fail(WHA_ERR_UNSUPPORTED, "%s: head_dim %d exceeds the supported maximum of 128", fn,
+                sh->n_embd / sh->n_head);
+  if (sh->content_dim < 0 || sh->content_dim > wha::kWaveFeatures - 2)
+    return fail(WHA_ERR_UNSUPPORTED, "%s: content_dim must be in [0, %d] (got %d)", fn, wha::kWaveFeatures - 2,
+                sh->content_dim);
+  if ((int64_t)sh->B * sh->n_head * sh->T > ((int64_t)1 << 31) || (int64_t)sh->B * sh->T * sh->n_embd > ((int64_t)1 << 40))
+    return fail(WHA_ERR_UNSUPPORTED, "%s: shape too large", fn);
+  return WHA_OK;
+}
+
+static wha::View wave_view(const wha_wave_shape* sh) {
+  const int hd = sh->n_embd / sh->n_head;
+  return wha::View{sh->B, sh->n_head, sh->T, hd, (int64_t)sh->T * sh->n_embd, (int64_t)hd, (int64_t)sh->n_embd};
+}
+
+static float wave_content_scale(int C) { return C > 0 ? 1.0f / sqrtf((float)C) : 0.0f; }
+
+static int check_wave_cache(const wha_wave_cache* c, const char* fn) {
+  if (c == nullptr) return fail(WHA_ERR_INVALID, "%s: cache is NULL", fn);
+  if (!c->proj || !c->values || !c->feat || !c->phase || !c->bucket || !c->merged || !c->lse)
+    return fail(WHA_ERR_INVALID, "%s: every cache buffer must be non-NULL", fn);
+  if (!aligned16(c->feat)) return fail(WHA_ERR_INVALID, "%s: cache->feat must be 16-byte aligned", fn);
+  return WHA_OK;
+}
+
+static int check_wave_weights(const wha_wave_weights* w, const char* fn) {
+  if (w == nullptr) return fail(WHA_ERR_INVALID, "%s: weights is NULL", fn);
+  if (!w->harmonic_raw || !w->proj_w || !w->proj_b || !w->v_w || !w->v_b || !w->out_w || !w->out_b)
+    return fail(WHA_ERR_INVALID, "%s: every weight pointer must be non-NULL", fn);
+  return WHA_OK;
+}
+
+int wha_wave_fwd(const float* x, const wha_wave_weights* w, const wha_wave_shape* shape, float* out,
+                 const wha_wave_cache* cache, void* stream) {
+  static const char* fn = "wha_wave_fwd";
+  int rc;
+  if ((rc = check_wave_shape(shape, fn)) || (rc = check_wave_weights(w, fn)) || (rc = check_wave_cache(cache, fn)))
+    return rc;
+  if (!x || !out) return fail(WHA_ERR_INVALID, "%s: x and out must be non-NULL", fn);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int B = shape->B, T = shape->T, E = shape->n_embd, H = shape->n_head, C = shape->content_dim;
+  const int hd = E / H, HP = H * (2 + C), M = B * T;
+  const wha::View Lv = wave_view(shape);
+  const float cs = wave_content_scale(C);
+  hipError_t e = wha::launch_linear_fwd(x, E, w->proj_w, w->proj_b, cache->proj, HP, M, HP, E, s);
+  if (e == hipSuccess)
+    e = wha::launch_linear_fwd_batched(x, E, hd, w->v_w, (int64_t)hd * hd, w->v_b, hd, cache->values, E, hd, M,
+                                       hd, hd, H, s);
+  if (e == hipSuccess)
+    e = wha::launch_wave_features(cache->proj, w->harmonic_raw, cache->feat, cache->phase, cache->bucket, B, H, T,
+                                  C, s);
+  if (e == hipSuccess)
+    e = wha::launch_wave_fwd(cache->feat, cache->bucket, cache->values, cache->merged, cache->lse, Lv,
+                             vec_ok(Lv, {cache->values, cache->merged}), cs, s);
+  if (e == hipSuccess) e = wha::launch_linear_fwd(cache->merged, E, w->out_w, w->out_b, out, E, M, E, E, s);
+  if (e != hipSuccess) return hip_fail(e, "wha_wave_fwd launch");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+// Workspace of wha_wave_bwd, in floats, each part rounded to 64 floats.
+struct WaveBwdParts {
+  size_t d_merged, delta, ds, dfk, dfq, dv, dproj, hpart, gemm, total;
+};
+
+static WaveBwdParts wave_bwd_parts(const wha_wave_shape* sh) {
+  auto r64 = [](size_t n) { return (n + 63) & ~(size_t)63; };
+  const size_t B = sh->B, T = sh->T, E = sh->n_embd, H = sh->n_head, P = 2 + sh->content_dim;
+  const int64_t M = (int64_t)B * T;
+  const int hd = (int)(E / H);
+  WaveBwdParts p{};
+  p.d_merged = r64(B * T * E);
+  p.delta = r64(B * H * T);
+  p.ds = r64(wha::bwd_ds_floats(wave_view(sh)));
+  p.dfk = r64(B * H * T * wha::kWaveFeatures);
+  p.dfq = p.dfk;
+  p.dv = r64(B * T * E);
+  p.dproj = r64(B * T * H * P);
+  p.hpart = r64(B * H * T);
+  size_t g = wha::linear_dw_workspace_floats((int)E, (int)E, M);
+  g = std::max(g, wha::linear_dw_workspace_floats((int)(H * P), (int)E, M));
+  g = std::max(g, wha::linear_dw_workspace_floats(hd, hd, M, (int)H));
+  p.gemm = r64(g);
+  p.total = p.d_merged + p.delta + p.ds + p.dfk + p.dfq + p.dv + p.dproj + p.hpart + p.gemm;
+  return p;
+}
+
+size_t wha_wave_bwd_workspace_size(const wha_wave_shape* shape) {
+  if (check_wave_shape(shape, "wha_wave_bwd_workspace_size") != WHA_OK) return 0;
+  return wave_bwd_parts(shape).total * sizeof(float);
+}
+
+int wha_wave_bwd(const float* x, const float* d_out, const wha_wave_weights* w, const wha_wave_shape* shape,
+                 const wha_wave_cache* cache, const wha_wave_grads* grads, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  static const char* fn = "wha_wave_bwd";
+  int rc;
+  if ((rc = check_wave_shape(shape, fn)) || (rc = check_wave_weights(w, fn)) || (rc = check_wave_cache(cache, fn)))
+    return rc;
+  if (!x || !d_out || !grads || !grads->d_x)
+    return fail(WHA_ERR_INVALID, "%s: x, d_out, grads and grads->d_x must be non-NULL", fn);
+  const float* wg[7] = {grads->d_harmonic_raw, grads->d_proj_w, grads->d_proj_b, grads->d_v_w,
+                        grads->d_v_b,          grads->d_out_w,  grads->d_out_b};
+  int n_set = 0;
+  for (const float* p : wg) n_set += p != nullptr;
+  if (n_set != 0 && n_set != 7)
+    return fail(WHA_ERR_INVALID, "%s: the weight gradients must be all non-NULL or all NULL", fn);
+  const bool full = n_set == 7;
+  const WaveBwdParts parts = wave_bwd_parts(shape);
+  if (parts.ds * sizeof(float) > kMaxDsBytes)
+    return fail(WHA_ERR_UNSUPPORTED, "%s: B*n_head*T^2 too large for the score-gradient buffer", fn);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* wsv = nullptr;
+  if ((rc = resolve_workspace(workspace, workspace_bytes, parts.total * sizeof(float), s, fn, &wsv))) return rc;
+  float* p = static_cast<float*>(wsv);
+  float* d_merged = p;
+  p += parts.d_merged;
+  float* delta = p;
+  p += parts.delta;
+  float* ds = p;
+  p += parts.ds;
+  float* dfk = p;
+  p += parts.dfk;
+  float* dfq = p;
+  p += parts.dfq;
+  float* dv = p;
+  p += parts.dv;
+  float* dproj = p;
+  p += parts.dproj;
+  float* hpart = p;
+  p += parts.hpart;
+  float* gws = p;
+
+  const int B = shape->B, T = shape->T, E = shape->n_embd, H = shape->n_head, C = shape->content_dim;
+  const int hd = E / H, HP = H * (2 + C), M = B * T;
+  const wha::View Lv = wave_view(shape);
+  const float cs = wave_content_scale(C);
+  const bool vec = vec_ok(Lv, {cache->values, cache->merged, d_merged, dv});
+  hipError_t e = wha::launch_linear_bwd_dx(d_out, E, w->out_w, d_merged, E, M, E, E, s);
+  if (e == hipSuccess && full)
+    e = wha::launch_linear_bwd_dw(d_out, E, cache->merged, E, grads->d_out_w, grads->d_out_b, M, E, E, gws, s);
+  if (e == hipSuccess)
+    e = wha::launch_wave_bwd_core(cache->feat, cache->bucket, cache->values, cache->merged, d_merged, cache->lse,
+                                  delta, dfk, dfq, dv, ds, Lv, vec, cs, s);
+  if (e == hipSuccess)
+    e = wha::launch_wave_feat_bwd(cache->proj, cache->feat, cache->phase, dfq, dfk, w->harmonic_raw, dproj, hpart,
+                                  full ? grads->d_harmonic_raw : nullptr, B, H, T, C, cs, s);
+  if (e == hipSuccess) e = wha::launch_linear_bwd_dx(dproj, HP, w->proj_w, grads->d_x, E, M, HP, E, s);
+  if (e == hipSuccess)
+    e = wha::launch_linear_bwd_dx_batched(dv, E, hd, w->v_w, (int64_t)hd * hd, grads->d_x, E, hd, M, hd, hd, H,
+                                          true, s);
+  if (e == hipSuccess && full)
+    e = wha::launch_linear_bwd_dw(dproj, HP, x, E, grads->d_proj_w, grads->d_proj_b, M, HP, E, gws, s);
+  if (e == hipSuccess && full)
+    e = wha::launch_linear_bwd_dw_batched(dv, E, hd, x, E, hd, grads->d_v_w, (int64_t)hd * hd, grads->d_v_b, M, hd,
+                                          hd, H, gws, s);
+  if (e != hipSuccess) return hip_fail(e, "wha_wave_bwd launch");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+int wha_wave_probs_rows(const wha_wave_cache* cache, const wha_wave_shape* shape, const int32_t* rows,
+                        int32_t n_rows, float* out, void* stream) {
+  static const char* fn = "wha_wave_probs_rows";
+  int rc;
+  if ((rc = check_wave_shape(shape, fn)) || (rc = check_wave_cache(cache, fn))) return rc;
+  if (!rows || !out) return fail(WHA_ERR_INVALID, "%s: rows and out must be non-NULL", fn);
+  if (n_rows < 1 || n_rows > wha::kMaxProbRows)
+    return fail(WHA_ERR_INVALID, "%s: n_rows must be in [1, %d] (got %d)", fn, wha::kMaxProbRows, n_rows);
+  wha::RowList rl;
+  rl.n = n_rows;
+  for (int i = 0; i < n_rows; ++i) {
+    if (rows[i] < 0 || rows[i] >= shape->T)
+      return fail(WHA_ERR_INVALID, "%s: rows[%d] = %d is outside [0, %d)", fn, i, rows[i], shape->T);
+    rl.rows[i] = rows[i];
+  }
+  hipError_t e = wha::launch_wave_probs_rows(cache->feat, cache->bucket, cache->lse, rl, out, shape->B,
+                                             shape->n_head, shape->T, wave_content_scale(shape->content_dim),
+                                             static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "wha_wave_probs_rows launch");
   g_err[0] = 0;
   return WHA_OK;
 }

@@ -214,4 +214,13 @@ __device__ __forceinline__ void store_row_frag(float* __restrict__ base, int row
   }
 }
 
+// dS workspace of the backward, per (b,h): column block kt (keys 64kt..64kt+63)
+// holds rows q = 64kt..T-1, 64 floats each, blocks back to back.
+// First row of column block kt: sum_{j<kt} (T - 64 j).
+__host__ __device__ __forceinline__ int64_t ds_block_row(int kt, int T) {
+  return (int64_t)kt * T - (int64_t)32 * kt * (kt - 1);
+}
+// Rows of dS per (b,h).
+__host__ __device__ __forceinline__ int64_t ds_rows(int T) { return ds_block_row((T + 63) / 64, T); }
+
 }  // namespace wha

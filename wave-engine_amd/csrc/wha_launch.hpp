@@ -11,6 +11,9 @@
 
 namespace wha {
 
+// Feature width of the wave-attention score contraction (cos, sin, content, zero pad).
+constexpr int kWaveFeatures = 32;
+
 // Padded head dimension used by the kernels for a given D (0 = unsupported).
 inline int padded_dim(int D) {
   if (D <= 0) return 0;
@@ -73,7 +76,48 @@ hipError_t launch_linear_bwd_dx(const float* dy, int64_t lddy, const float* w, f
 // dw[n][k] = sum_m dy[m][n] x[m][k]; db[n] = sum_m dy[m][n] (db may be nullptr).
 // ws: linear_dw_workspace_floats(N, K, M) floats.
 size_t linear_dw_workspace_floats(int N, int K, int64_t M);
+size_t linear_dw_workspace_floats(int N, int K, int64_t M, int batch);
 hipError_t launch_linear_bwd_dw(const float* dy, int64_t lddy, const float* x, int64_t ldx, float* dw, float* db,
                                 int M, int N, int K, float* ws, hipStream_t stream);
+// Batched forms: `batch` independent problems, operand bt offset by bt * (its _sb stride).
+hipError_t launch_linear_fwd_batched(const float* x, int64_t ldx, int64_t x_sb, const float* w, int64_t w_sb,
+                                     const float* b, int64_t b_sb, float* y, int64_t ldy, int64_t y_sb, int M,
+                                     int N, int K, int batch, hipStream_t stream);
+hipError_t launch_linear_bwd_dx_batched(const float* dy, int64_t lddy, int64_t dy_sb, const float* w,
+                                        int64_t w_sb, float* dx, int64_t lddx, int64_t dx_sb, int M, int N,
+                                        int K, int batch, bool accumulate, hipStream_t stream);
+// db: [batch][N] or nullptr; ws: linear_dw_workspace_floats(N, K, M, batch) floats.
+hipError_t launch_linear_bwd_dw_batched(const float* dy, int64_t lddy, int64_t dy_sb, const float* x,
+                                        int64_t ldx, int64_t x_sb, float* dw, int64_t dw_sb, float* db, int M,
+                                        int N, int K, int batch, float* ws, hipStream_t stream);
+
+// Backward building blocks shared with the wave-attention path.
+// Delta[b,h,t] = sum_d dO . O over the view's head.
+hipError_t launch_attn_bwd_delta(const float* o, const float* d_o, float* delta, const View& L, const char* name,
+                                 hipStream_t stream);
+// dQ = scale * dS K from the dS workspace (ds_block_row layout); L.D must be kWaveFeatures.
+hipError_t launch_dq_from_ds(const float* k, const float* ds, float* dq, const View& L, float scale,
+                             const char* name, hipStream_t stream);
+
+// ---- wave (harmonic coherence) attention ----
+// proj [B][T][H][2+C] -> feat [B][H][T][kWaveFeatures], phase, bucket [B][H][T].
+hipError_t launch_wave_features(const float* proj, const float* hraw, float* feat, float* phase, int* bucket,
+                                int B, int H, int T, int C, hipStream_t stream);
+// Fused forward over the per-head values (view Lv, D = head_dim): merged
+// head outputs (same view) and natural-log LSE [B][H][T].
+hipError_t launch_wave_fwd(const float* feat, const int* bucket, const float* v, float* merged, float* lse,
+                           const View& Lv, bool vec, float cs, hipStream_t stream);
+// Core backward: Delta, dV, raw feature gradients of the key (dfk) and query
+// (dfq) roles [B][H][T][kWaveFeatures]; ds: bwd_ds_floats(Lv) floats.
+hipError_t launch_wave_bwd_core(const float* feat, const int* bucket, const float* v, const float* merged,
+                                const float* d_merged, const float* lse, float* delta, float* dfk, float* dfq,
+                                float* dv, float* ds, const View& Lv, bool vec, float cs, hipStream_t stream);
+// Rows of the wave attention probabilities: out [B][H][rl.n][T].
+hipError_t launch_wave_probs_rows(const float* feat, const int* bucket, const float* lse, const RowList& rl,
+                                  float* out, int B, int H, int T, float cs, hipStream_t stream);
+// Feature gradients -> dproj [B][T][H][2+C]; hpart [H][B*T] scratch; d_hraw [H] or nullptr.
+hipError_t launch_wave_feat_bwd(const float* proj, const float* feat, const float* phase, const float* dfq,
+                                const float* dfk, const float* hraw, float* dproj, float* hpart, float* d_hraw,
+                                int B, int H, int T, int C, float cs, hipStream_t stream);
 
 }  // namespace wha
