@@ -11,7 +11,10 @@ credited FLOPs (12*B*H*D*P, P = T(T+1)/2), a roofline object for the dominant
 kernel (algorithmic FLOPs per launch / its average HIP-event duration), and the
 CPU baseline (the reference-order f32 oracle, one thread per sequence).
 
-    python bench.py [--steps K] [--warmup W] [--config 768|384|168|4096|decode]
+    python bench.py [--steps K] [--warmup W] [--config 768|384|168|4096|decode|wave]
+
+--config wave measures the wave (harmonic coherence) attention layer the
+reference trains with, forward and full backward with its projections.
 """
 from __future__ import annotations
 
@@ -34,6 +37,8 @@ CONFIGS = {
     "768": dict(name="768-dim production config", B=8, H=12, T=1024, D=64),
     "4096": dict(name="4096-dim preset", B=4, H=32, T=2048, D=128),
     "decode": dict(name="768-dim decode (serve tier)", B=64, H=12, T=8192, D=64),
+    "wave": dict(name="768-dim wave attention (harmonic coherence, content 16), full fwd+bwd", B=8, H=12,
+                 T=1024, D=64, C=16),
 }
 
 METRIC = "causal attn fwd+bwd tokens/s & TFLOP/s (% fp32 MFMA peak), 768-dim seq1024"
@@ -187,6 +192,127 @@ def run_decode(args, cfg, pkg, torch):
                          "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic("decode_split", cfg)}}
 
 
+def wave_credited_flops(B, H, T, D, C):
+    """FLOPs of one wave-attention layer step (wave_attention_forward +
+    wave_attention_backward_full).  Core terms count every causal pair (what the
+    kernels execute; the bucket mask admits about 3/8 of them) with the
+    (2 + C)-wide feature dot product, not its 32-wide zero padding."""
+    E, M, F = H * D, B * T, 2 + C
+    P = B * H * (T * (T + 1) // 2)
+    proj = 2 * M * E * H * F          # phase + content projections
+    vproj = 2 * M * E * D             # per-head value projections
+    outp = 2 * M * E * E
+    return {"wave_fwd": 2 * P * (F + D),
+            "wave_bwd_dkv": 2 * P * (F + 2 * D + F),   # S, dP, dV, dF_k
+            "wave_bwd_dq": 2 * P * F,                  # dF_q = dS F_k
+            "linear_fwd": proj + vproj + outp,
+            "linear_bwd": 2 * (proj + vproj + outp),   # input and weight gradients
+            "total": 2 * P * (F + D) + 2 * P * (3 * F + 2 * D) + 3 * (proj + vproj + outp)}
+
+
+def run_wave(args, cfg, pkg, torch):
+    import numpy as np
+    B, H, T, D, C = cfg["B"], cfg["H"], cfg["T"], cfg["D"], cfg["C"]
+    E = H * D
+    dev = torch.device("cuda:0")
+    g = pkg.SynthStream(42)
+    t = lambda n, sd, *shape: torch.from_numpy(g.normal(n, sd).reshape(*shape)).to(dev)
+    x = t(B * T * E, 1.0, B, T, E)
+    W = pkg.WaveAttnWeights(t(H, 1.0, H), t(H * (2 + C) * E, 1 / np.sqrt(E), H, 2 + C, E),
+                            t(H * (2 + C), 0.1, H, 2 + C), t(H * D * D, 1 / np.sqrt(D), H, D, D), t(H * D, 0.1, H, D),
+                            t(E * E, 1 / np.sqrt(E), E, E), t(E, 0.1, E))
+    dy = t(B * T * E, 1.0 / np.sqrt(B * T), B, T, E)
+    shape = pkg.WaveShape(B, T, E, H, C)
+    ws = torch.empty(pkg.wave_bwd_workspace_bytes(shape) // 4 + 64, dtype=torch.float32, device=dev)
+    out = torch.empty_like(x)
+
+    def step():
+        _, _, cache = pkg.wave_attention_forward(W, x, out=out)
+        pkg.wave_attention_backward_full(W, cache, dy, workspace=ws)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    names = ("wave_feat", "wave_fwd", "wave_bwd_delta", "wave_bwd_dkv", "wave_bwd_dq", "wave_feat_bwd",
+             "wave_harmonic", "linear_fwd", "linear_bwd_dx", "linear_bwd_dw", "linear_bwd_db")
+    pkg.timing_reset()
+    pkg.timing_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    pkg.timing_enable(False)
+    kern = {}
+    for name in names:
+        ms, n = pkg.timing_read(name)
+        kern[name] = {"total_ms": ms / args.steps, "avg_ms": ms / max(n, 1), "launches": n}
+    pkg.timing_reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) / args.steps * 1e3
+    fl = wave_credited_flops(B, H, T, D, C)
+    dom = max(("wave_fwd", "wave_bwd_dkv", "wave_bwd_dq"), key=lambda n: kern[n]["avg_ms"])
+    achieved = fl[dom] / (kern[dom]["avg_ms"] * 1e-3) / 1e12
+    return {
+        "metric": "wave attention layer fwd+bwd tokens/s & TFLOP/s, 768-dim seq1024",
+        "value": B * T / (ms_per_step * 1e-3), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded xorshift64 + Box-Muller, seed 42), random-init weights",
+        "config": {"workload": cfg["name"], "batch": B, "heads": H, "seq_len": T, "head_dim": D,
+                   "content_dim": C, "parallelism": "none (1 GPU)"},
+        "tflops": fl["total"] / (ms_per_step * 1e-3) / 1e12,
+        "kernel_ms_per_step": {n: round(kern[n]["total_ms"], 5) for n in names},
+        "ms_per_step_with_events": wall / args.steps * 1e3,
+        "roofline": {"kernel": dom, "bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS,
+                     "traffic": load_traffic(dom, cfg), "algorithmic_flops_per_launch": fl[dom],
+                     "avg_launch_ms": kern[dom]["avg_ms"]},
+    }
+
+
+def wave_cpu_baseline(cfg, seed=42, max_threads=None, min_seconds=10.0):
+    """Reference-order f32 oracle of wave_attention_forward + backward_full, one
+    thread per sequence on a bounded sample, repeated to at least min_seconds."""
+    import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
+    import oracle
+    B, H, T, D, C = cfg["B"], cfg["H"], cfg["T"], cfg["D"], cfg["C"]
+    E = H * D
+    ncpu = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    nthreads = min(B, ncpu, max_threads or 16)
+    rng = oracle.Xorshift64(seed)
+    x = rng.normal(nthreads * T * E, 1.0).reshape(nthreads, T, E)
+    w = dict(hraw=rng.normal(H, 1.0), proj_w=rng.normal(H * (2 + C) * E, 1 / np.sqrt(E)).reshape(H, 2 + C, E),
+             proj_b=rng.normal(H * (2 + C), 0.1).reshape(H, 2 + C),
+             v_w=rng.normal(H * D * D, 1 / np.sqrt(D)).reshape(H, D, D), v_b=rng.normal(H * D, 0.1).reshape(H, D),
+             out_w=rng.normal(E * E, 1 / np.sqrt(E)).reshape(E, E), out_b=rng.normal(E, 0.1))
+    dy = rng.normal(nthreads * T * E, 1.0 / np.sqrt(B * T)).reshape(nthreads, T, E)
+
+    def one(i):
+        oracle.wave_fwd(x[i], w, "f32")
+        oracle.wave_bwd(x[i], w, dy[i], "f32")
+
+    reps = 0
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(nthreads) as ex:
+        while True:
+            list(ex.map(one, range(nthreads)))
+            reps += 1
+            if time.perf_counter() - t0 >= min_seconds:
+                break
+    dt = (time.perf_counter() - t0) / reps
+    return {"value": nthreads * T / dt, "unit": "tokens/s", "cores": nthreads, "kind": "port",
+            "sample": f"{nthreads} of the {B} sequences ({nthreads}x{T} tokens), wave_attention_forward + "
+                      f"wave_attention_backward_full, one thread per sequence, repeated {reps}x",
+            "seconds_per_rep": dt}
+
+
 def load_traffic(kernel, cfg):
     """HBM bytes per launch of `kernel` on this workload, from the rocprofv3 --pmc
     FETCH_SIZE / WRITE_SIZE summary committed under profiles/ (null if absent)."""
@@ -233,12 +359,14 @@ def main():
         del x, y
     if args.config == "decode":
         res = run_decode(args, cfg, pkg, torch)
+    elif args.config == "wave":
+        res = run_wave(args, cfg, pkg, torch)
     else:
         res = run_attention(args, cfg, pkg, torch)
-    if not args.no_cpu_baseline and args.config != "decode":
-        res["cpu_baseline"] = cpu_baseline(cfg)
-    elif args.config == "decode":
+    if args.config == "decode":
         res["cpu_baseline"] = None
+    elif not args.no_cpu_baseline:
+        res["cpu_baseline"] = wave_cpu_baseline(cfg) if args.config == "wave" else cpu_baseline(cfg)
     print(json.dumps(res), flush=True)
 
 

@@ -273,6 +273,50 @@ int wha_wave_bwd(const float* x, const float* d_out, const wha_wave_weights* w, 
 int wha_wave_probs_rows(const wha_wave_cache* cache, const wha_wave_shape* shape, const int32_t* rows,
                         int32_t n_rows, float* out, void* stream);
 
+/* ---------------------------------------------------------------- wave KV cache
+ * Serving (src/common/kv_cache.rs:93-356, driven by
+ * src/serve_tier/inference.rs:29-106): the attention half of prefill and
+ * forward_one for B concurrent sequences.  Like the reference's cache path,
+ * these score phases only (no content bias, kv_cache.rs:150-162, :285-298)
+ * even when the weights carry a content projection.
+ *
+ * Cache of one layer (HeadCache, kv_cache.rs:35-41), caller-allocated device
+ * buffers with room for `capacity` positions per (sequence, head):
+ *   cs     [B][n_head][capacity][2]         cos(n phi), sin(n phi)
+ *   bucket [B][n_head][capacity]            phase_to_bucket(phi)
+ *   phase  [B][n_head][capacity]            phi
+ *   values [B][n_head][capacity][head_dim]  value rows (16-byte aligned) */
+typedef struct wha_wave_kv_cache {
+  float* cs;
+  int32_t* bucket;
+  float* phase;
+  float* values;
+  int32_t capacity;
+} wha_wave_kv_cache;
+
+/* Workspace bytes of wha_wave_kv_prefill for prompts of shape->T positions. */
+size_t wha_wave_kv_prefill_workspace_size(const wha_wave_shape* shape);
+
+/* prefill's attention (kv_cache.rs:121-193) over prompts x [B][T][n_embd]
+ * (shape->T <= capacity): out [B][T][n_embd] after out_proj, and cache entries
+ * for positions 0 .. T-1 of every sequence. */
+int wha_wave_kv_prefill(const float* x, const wha_wave_weights* w, const wha_wave_shape* shape,
+                        const wha_wave_kv_cache* kv, float* out, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* Workspace bytes of wha_wave_kv_decode for shape->B sequences and caches of
+ * up to `capacity` positions. */
+size_t wha_wave_kv_decode_workspace_size(const wha_wave_shape* shape, int32_t capacity);
+
+/* forward_one's attention (kv_cache.rs:263-335) for one new token per
+ * sequence: x [B][n_embd] (shape->T must be 1), lengths = host array of the B
+ * cached lengths (each in [0, capacity - 1]; B <= 256).  Writes out [B][n_embd]
+ * after out_proj and appends each new position at index lengths[b]; the
+ * caller then advances its lengths (cache.n_cached += 1, :358). */
+int wha_wave_kv_decode(const float* x, const wha_wave_weights* w, const wha_wave_shape* shape,
+                       const wha_wave_kv_cache* kv, const int32_t* lengths, float* out, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------- inputs
  * Seeded synthetic inputs (host): continues the xorshift64 stream in *state
  * (the reference's Rng::next_u64/next_f32, src/common/rng.rs:24-34) with

@@ -503,3 +503,41 @@ def combine_d_normed(d_phase, d_v, d_content=None, precision: str = "f32"):
     out = np.empty((T, E), dt)
     _wave_fn("wao_combine_d_normed", precision)(_ptr(d_phase), _ptr(d_v), _ptr(dc), H, T, E, _ptr(out))
     return out
+
+
+def wave_kv_prefill(x, w, precision: str = "f32", phase_in=None):
+    """kv_cache::prefill's attention (src/common/kv_cache.rs:121-193) on one
+    prompt x [T][E]: no content bias.  Returns out, phase [H][T], values
+    [H][T][hd], merged."""
+    dt = _dt(precision)
+    x = _c(x, dt)
+    ww = {k: _c(w[k], dt) for k in _WAVE_KEYS}
+    H, C, E = wave_dims(ww)
+    T = x.shape[0]
+    hd = E // H
+    ph_in = _c(phase_in, dt) if phase_in is not None else None
+    r = dict(out=np.empty((T, E), dt), phase=np.empty((H, T), dt), values=np.empty((H, T, hd), dt),
+             merged=np.empty((T, E), dt))
+    _wave_fn("wao_wave_kv_prefill", precision)(
+        _ptr(x), T, E, H, C, *(_ptr(ww[k]) for k in _WAVE_KEYS), _ptr(ph_in), _ptr(r["out"]), _ptr(r["phase"]),
+        _ptr(r["values"]), _ptr(r["merged"]))
+    return r
+
+
+def wave_kv_step(x, w, phases, values, n_cached: int, precision: str = "f32", phase_new_in=None):
+    """kv_cache::forward_one's attention (src/common/kv_cache.rs:263-335) for one
+    sequence: x [E] against cached phases [H][cap] and values [H][cap][hd]
+    (entries 0..n_cached-1).  Returns out [E], phase_new [H], v_new [H][hd], merged [E]."""
+    dt = _dt(precision)
+    x = _c(x, dt)
+    ww = {k: _c(w[k], dt) for k in _WAVE_KEYS}
+    H, C, E = wave_dims(ww)
+    hd = E // H
+    phases, values = _c(phases, dt), _c(values, dt)
+    cap = phases.shape[1]
+    ph_in = _c(phase_new_in, dt) if phase_new_in is not None else None
+    r = dict(out=np.empty(E, dt), phase_new=np.empty(H, dt), v_new=np.empty((H, hd), dt), merged=np.empty(E, dt))
+    _wave_fn("wao_wave_kv_step", precision)(
+        _ptr(x), E, H, C, *(_ptr(ww[k]) for k in _WAVE_KEYS), _ptr(phases), _ptr(values), cap, int(n_cached),
+        _ptr(ph_in), _ptr(r["out"]), _ptr(r["phase_new"]), _ptr(r["v_new"]), _ptr(r["merged"]))
+    return r

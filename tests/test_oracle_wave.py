@@ -224,3 +224,42 @@ def test_backward_matches_finite_differences(C):
             assert abs(fd - grad[idx]) <= 1e-6 * max(1.0, abs(fd)), (name, idx, fd, grad[idx])
             checked += 1
     assert checked >= 40
+
+
+# ------------------------------------------------------------ KV-cache serving
+
+@pytest.mark.parametrize("precision", ["f32", "f64"])
+def test_kv_prefill_is_the_forward_without_content(precision):
+    """kv_cache::prefill scores phases only (kv_cache.rs:150-162): the forward
+    with the content rows removed gives the same result."""
+    T, E, H, C = 30, 24, 3, 4
+    w = make_weights(H, C, E, seed=4)
+    x = np.random.default_rng(1).normal(size=(T, E)).astype(np.float32)
+    p = oracle.wave_kv_prefill(x, w, precision)
+    w0 = dict(w, proj_w=w["proj_w"][:, :2].copy(), proj_b=w["proj_b"][:, :2].copy())
+    f = oracle.wave_fwd(x, w0, precision)
+    np.testing.assert_array_equal(p["out"], f["out"])
+    np.testing.assert_array_equal(p["phase"], f["phase"])
+    np.testing.assert_array_equal(p["values"], f["values"])
+
+
+@pytest.mark.parametrize("precision", ["f32", "f64"])
+def test_kv_step_equals_the_last_prefill_row(precision):
+    """forward_one after prefilling t positions reproduces row t of a prefill
+    over t+1 positions bit for bit (self score 1 = cos 0, the same mask and the
+    same summation order), for every t."""
+    T, E, H, C = 21, 16, 2, 3
+    w = make_weights(H, C, E, seed=6)
+    x = np.random.default_rng(2).normal(size=(T, E)).astype(np.float32)
+    full = oracle.wave_kv_prefill(x, w, precision)
+    cap = T + 3
+    hd = E // H
+    dt = np.float32 if precision == "f32" else np.float64
+    phases = np.zeros((H, cap), dt)
+    values = np.zeros((H, cap, hd), dt)
+    for t in range(T):
+        st = oracle.wave_kv_step(x[t], w, phases, values, t, precision)
+        np.testing.assert_array_equal(st["out"], full["out"][t])
+        np.testing.assert_array_equal(st["phase_new"], full["phase"][:, t])
+        phases[:, t] = st["phase_new"]
+        values[:, t] = st["v_new"]

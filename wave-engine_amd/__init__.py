@@ -41,6 +41,8 @@ EXPORTED_SYMBOLS = (
     "wha_attn_bwd_from_probs_workspace_size", "wha_attn_bwd_from_probs",
     "wha_decode_workspace_size", "wha_decode_fwd", "wha_attn_probs_rows",
     "wha_wave_fwd", "wha_wave_bwd_workspace_size", "wha_wave_bwd", "wha_wave_probs_rows",
+    "wha_wave_kv_prefill_workspace_size", "wha_wave_kv_prefill", "wha_wave_kv_decode_workspace_size",
+    "wha_wave_kv_decode",
     "wha_linear_fwd", "wha_linear_bwd_dx", "wha_linear_bwd_dw_workspace_size", "wha_linear_bwd_dw",
     "wha_host_attention_core_fwd", "wha_host_attention_backward", "wha_host_attention",
     "wha_synth_normal",
@@ -78,6 +80,11 @@ class _WaveCacheC(ctypes.Structure):
 class _WaveGradsC(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in ("d_x", "d_harmonic_raw", "d_proj_w", "d_proj_b", "d_v_w", "d_v_b",
                                                 "d_out_w", "d_out_b")]
+
+
+class _WaveKvC(ctypes.Structure):
+    _fields_ = [("cs", ctypes.c_void_p), ("bucket", ctypes.c_void_p), ("phase", ctypes.c_void_p),
+                ("values", ctypes.c_void_p), ("capacity", ctypes.c_int32)]
 
 
 def layout_bhtd(B, H, T, D) -> WaveLayout:
@@ -146,6 +153,13 @@ def lib():
         L.wha_wave_bwd_workspace_size.restype = sz
         L.wha_wave_bwd.argtypes = [vp, vp, wwp, wsp, wcp, wgp, vp, sz, vp]
         L.wha_wave_probs_rows.argtypes = [wcp, wsp, ctypes.POINTER(ctypes.c_int32), i32, vp, vp]
+        kvp = ctypes.POINTER(_WaveKvC)
+        L.wha_wave_kv_prefill_workspace_size.argtypes = [wsp]
+        L.wha_wave_kv_prefill_workspace_size.restype = sz
+        L.wha_wave_kv_prefill.argtypes = [vp, wwp, wsp, kvp, vp, vp, sz, vp]
+        L.wha_wave_kv_decode_workspace_size.argtypes = [wsp, i32]
+        L.wha_wave_kv_decode_workspace_size.restype = sz
+        L.wha_wave_kv_decode.argtypes = [vp, wwp, wsp, kvp, ctypes.POINTER(ctypes.c_int32), vp, vp, sz, vp]
         L.wha_synth_normal.argtypes = [ctypes.POINTER(ctypes.c_uint64), f32p, sz, ctypes.c_double, ctypes.c_int]
         L.wha_synth_normal.restype = ctypes.c_int
         L.wha_timing_enable.argtypes = [ctypes.c_int]
@@ -699,6 +713,76 @@ def wave_probs_rows(cache: WaveAttnCache, rows):
     out = torch.empty(sh.B, sh.n_head, len(rows), sh.T, dtype=torch.float32, device=cache.lse.device)
     _check("wha_wave_probs_rows", lib().wha_wave_probs_rows(ctypes.byref(cache._c()), ctypes.byref(sh), arr,
                                                              len(rows), _ptr(out), _stream_ptr(out)))
+    return out
+
+
+# ------------------------------------------------------------------ wave KV cache (serving)
+
+class WaveKvCache:
+    """One layer's KV cache for B concurrent sequences (the per-layer part of
+    KvCache, src/common/kv_cache.rs:35-89): per (sequence, head) cos/sin of
+    n*phase, bucket, phase and value rows for up to `capacity` positions, plus
+    the host-side count of cached positions per sequence (n_cached)."""
+
+    def __init__(self, B: int, n_head: int, head_dim: int, capacity: int, device="cuda"):
+        torch = _torch()
+        self.B, self.n_head, self.head_dim, self.capacity = B, n_head, head_dim, capacity
+        z = lambda *sh, dt=torch.float32: torch.zeros(*sh, dtype=dt, device=device)
+        self.cs = z(B, n_head, capacity, 2)
+        self.bucket = z(B, n_head, capacity, dt=torch.int32)
+        self.phase = z(B, n_head, capacity)
+        self.values = z(B, n_head, capacity, head_dim)
+        self.lengths = [0] * B
+
+    def _c(self, b0=0):
+        """C view of sequences b0.. (pointer offsets into the batch)."""
+        return _WaveKvC(self.cs[b0:].data_ptr(), self.bucket[b0:].data_ptr(), self.phase[b0:].data_ptr(),
+                        self.values[b0:].data_ptr(), self.capacity)
+
+
+def prefill_attention(weights: WaveAttnWeights, x, cache: WaveKvCache, first_seq: int = 0, workspace=None):
+    """prefill's attention (kv_cache.rs:121-193) for prompts x [b][T][n_embd] of
+    sequences first_seq .. first_seq+b-1 of the cache: returns out (after
+    out_proj) and sets those sequences' cached positions to T."""
+    torch = _torch()
+    x = _wave_x(x, weights)
+    nb, T, E = x.shape
+    if first_seq < 0 or first_seq + nb > cache.B:
+        raise ValueError("sequence range outside the cache")
+    shape = WaveShape(nb, T, E, weights.n_head, weights.content_dim)
+    ws = workspace
+    if ws is None:
+        ws = torch.empty(int(lib().wha_wave_kv_prefill_workspace_size(ctypes.byref(shape))) // 4 + 64,
+                         dtype=torch.float32, device=x.device)
+    out = torch.empty_like(x)
+    _check("wha_wave_kv_prefill", lib().wha_wave_kv_prefill(
+        _ptr(x), ctypes.byref(weights._c()), ctypes.byref(shape), ctypes.byref(cache._c(first_seq)), _ptr(out),
+        _ptr(ws), ws.numel() * 4, _stream_ptr(x)))
+    for b in range(first_seq, first_seq + nb):
+        cache.lengths[b] = T
+    return out
+
+
+def forward_one_attention(weights: WaveAttnWeights, x, cache: WaveKvCache, workspace=None):
+    """forward_one's attention (kv_cache.rs:263-335) for one new token of every
+    sequence: x [B][n_embd] -> out [B][n_embd]; appends the tokens and advances
+    the cached counts (kv_cache.rs:358)."""
+    torch = _torch()
+    if x.dim() != 2 or x.shape[0] != cache.B or x.shape[1] != weights.n_embd:
+        raise ValueError(f"x must be [{cache.B}][{weights.n_embd}]")
+    if not (x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()):
+        raise ValueError("x must be a contiguous float32 device tensor")
+    shape = WaveShape(cache.B, 1, weights.n_embd, weights.n_head, weights.content_dim)
+    ws = workspace
+    if ws is None:
+        ws = torch.empty(int(lib().wha_wave_kv_decode_workspace_size(ctypes.byref(shape), cache.capacity)) // 4
+                         + 64, dtype=torch.float32, device=x.device)
+    lens = (ctypes.c_int32 * cache.B)(*cache.lengths)
+    out = torch.empty_like(x)
+    _check("wha_wave_kv_decode", lib().wha_wave_kv_decode(
+        _ptr(x), ctypes.byref(weights._c()), ctypes.byref(shape), ctypes.byref(cache._c()), lens, _ptr(out),
+        _ptr(ws), ws.numel() * 4, _stream_ptr(x)))
+    cache.lengths = [n + 1 for n in cache.lengths]
     return out
 
 

@@ -227,25 +227,29 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
   *dst = g.accumulate ? *dst + r : r;
 }
 
-// out[n] = sum_m y[m][n] (column sums, for the bias gradient): rows split over
-// blockIdx.y into fixed chunks whose partials are then added in order.
-__global__ __launch_bounds__(256) void colsum_partial_kernel(const float* __restrict__ y, int64_t ldy, int M,
-                                                             int N, int rows_per, float* __restrict__ part) {
+// out[bt][n] = sum_m y[bt][m][n] (column sums, for the bias gradient): rows
+// split over blockIdx.y into fixed chunks whose partials are then added in
+// order; blockIdx.z = batch index (operand offset bt * y_sb).
+__global__ __launch_bounds__(256) void colsum_partial_kernel(const float* __restrict__ y, int64_t ldy,
+                                                             int64_t y_sb, int M, int N, int rows_per,
+                                                             float* __restrict__ part) {
   const int n = blockIdx.x * 256 + threadIdx.x;
   if (n >= N) return;
+  const float* yb = y + (int64_t)blockIdx.z * y_sb;
   const int r0 = blockIdx.y * rows_per, r1 = min(M, r0 + rows_per);
   float s = 0.f;
-  for (int m = r0; m < r1; ++m) s += y[(int64_t)m * ldy + n];
-  part[(int64_t)blockIdx.y * N + n] = s;
+  for (int m = r0; m < r1; ++m) s += yb[(int64_t)m * ldy + n];
+  part[((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * N + n] = s;
 }
 
 __global__ __launch_bounds__(256) void colsum_final_kernel(const float* __restrict__ part, int chunks, int N,
                                                            float* __restrict__ out) {
   const int n = blockIdx.x * 256 + threadIdx.x;
   if (n >= N) return;
+  const float* pb = part + (int64_t)blockIdx.z * chunks * N;
   float s = 0.f;
-  for (int z = 0; z < chunks; ++z) s += part[(int64_t)z * N + n];
-  out[n] = s;
+  for (int z = 0; z < chunks; ++z) s += pb[(int64_t)z * N + n];
+  out[(int64_t)blockIdx.z * N + n] = s;
 }
 
 namespace {
@@ -345,17 +349,13 @@ hipError_t launch_linear_bwd_dw_batched(const float* dy, int64_t lddy, int64_t d
   const int chunks = colsum_chunks(M);
   const int rows_per = (M + chunks - 1) / chunks;
   TimingScope ts("linear_bwd_db", stream);
-  for (int bt = 0; bt < batch; ++bt) {
-    hipLaunchKernelGGL(colsum_partial_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)chunks), dim3(256), 0,
-                       stream, dy + bt * dy_sb, lddy, M, N, rows_per, cs + (size_t)bt * chunks * N);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, stream,
-                       (const float*)(cs + (size_t)bt * chunks * N), chunks, N, db + (size_t)bt * N);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
-  return hipSuccess;
+  hipLaunchKernelGGL(colsum_partial_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)chunks, (unsigned)batch),
+                     dim3(256), 0, stream, dy, lddy, dy_sb, M, N, rows_per, cs);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((N + 255) / 256), 1, (unsigned)batch), dim3(256), 0,
+                     stream, (const float*)cs, chunks, N, db);
+  return hipGetLastError();
 }
 
 size_t linear_dw_workspace_floats(int N, int K, int64_t M) { return linear_dw_workspace_floats(N, K, M, 1); }

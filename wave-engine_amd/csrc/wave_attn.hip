@@ -56,7 +56,7 @@ __device__ __forceinline__ bool bucket_near(int kb, int qb) { return ((kb - qb +
 __global__ __launch_bounds__(256) void wave_feat_kernel(const float* __restrict__ proj,
                                                         const float* __restrict__ hraw, float* __restrict__ feat,
                                                         float* __restrict__ phase, int* __restrict__ bucket, int B,
-                                                        int H, int T, int C) {
+                                                        int H, int T, int C, int C_used) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)B * H * T) return;
   const int t = (int)(i % T);
@@ -73,7 +73,7 @@ __global__ __launch_bounds__(256) void wave_feat_kernel(const float* __restrict_
   for (int j = 0; j < kFP; ++j) f[j] = 0.f;
   f[0] = cn;
   f[1] = sn;
-  for (int j = 0; j < C; ++j) f[2 + j] = pr[2 + j];
+  for (int j = 0; j < C_used; ++j) f[2 + j] = pr[2 + j];
   float4* dst = reinterpret_cast<float4*>(feat + i * kFP);
 #pragma unroll
   for (int j = 0; j < kFP / 4; ++j) dst[j] = make_float4(f[4 * j], f[4 * j + 1], f[4 * j + 2], f[4 * j + 3]);
@@ -521,11 +521,11 @@ __global__ __launch_bounds__(256) void wave_probs_rows_kernel(const float* __res
 // ------------------------------------------------------------------ launchers
 
 hipError_t launch_wave_features(const float* proj, const float* hraw, float* feat, float* phase, int* bucket,
-                                int B, int H, int T, int C, hipStream_t stream) {
+                                int B, int H, int T, int C, int C_used, hipStream_t stream) {
   const int64_t n = (int64_t)B * H * T;
   TimingScope ts("wave_feat", stream);
   hipLaunchKernelGGL(wave_feat_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, proj, hraw, feat,
-                     phase, bucket, B, H, T, C);
+                     phase, bucket, B, H, T, C, C_used);
   return hipGetLastError();
 }
 

@@ -463,7 +463,7 @@ int wha_wave_fwd(const float* x, const wha_wave_weights* w, const wha_wave_shape
                                        hd, hd, H, s);
   if (e == hipSuccess)
     e = wha::launch_wave_features(cache->proj, w->harmonic_raw, cache->feat, cache->phase, cache->bucket, B, H, T,
-                                  C, s);
+                                  C, C, s);
   if (e == hipSuccess)
     e = wha::launch_wave_fwd(cache->feat, cache->bucket, cache->values, cache->merged, cache->lse, Lv,
                              vec_ok(Lv, {cache->values, cache->merged}), cs, s);
@@ -593,6 +593,161 @@ int wha_wave_probs_rows(const wha_wave_cache* cache, const wha_wave_shape* shape
                                              shape->n_head, shape->T, wave_content_scale(shape->content_dim),
                                              static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "wha_wave_probs_rows launch");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+// ---------------------------------------------------------------- wave KV cache
+
+static int check_kv(const wha_wave_kv_cache* kv, const char* fn) {
+  if (kv == nullptr) return fail(WHA_ERR_INVALID, "%s: kv cache is NULL", fn);
+  if (!kv->cs || !kv->bucket || !kv->phase || !kv->values)
+    return fail(WHA_ERR_INVALID, "%s: every kv cache buffer must be non-NULL", fn);
+  if (kv->capacity <= 0) return fail(WHA_ERR_INVALID, "%s: capacity must be positive (got %d)", fn, kv->capacity);
+  if (!aligned16(kv->values) || (reinterpret_cast<uintptr_t>(kv->cs) & 7u))
+    return fail(WHA_ERR_INVALID, "%s: kv->values must be 16-byte and kv->cs 8-byte aligned", fn);
+  return WHA_OK;
+}
+
+struct KvPrefillParts {
+  size_t proj, values, feat, phase, bucket, merged, lse, total;
+};
+
+static KvPrefillParts kv_prefill_parts(const wha_wave_shape* sh) {
+  auto r64 = [](size_t n) { return (n + 63) & ~(size_t)63; };
+  const size_t B = sh->B, T = sh->T, E = sh->n_embd, H = sh->n_head, P = 2 + sh->content_dim;
+  KvPrefillParts p{};
+  p.proj = r64(B * T * H * P);
+  p.values = r64(B * T * E);
+  p.feat = r64(B * H * T * wha::kWaveFeatures);
+  p.phase = r64(B * H * T);
+  p.bucket = r64(B * H * T);
+  p.merged = r64(B * T * E);
+  p.lse = r64(B * H * T);
+  p.total = p.proj + p.values + p.feat + p.phase + p.bucket + p.merged + p.lse;
+  return p;
+}
+
+size_t wha_wave_kv_prefill_workspace_size(const wha_wave_shape* shape) {
+  if (check_wave_shape(shape, "wha_wave_kv_prefill_workspace_size") != WHA_OK) return 0;
+  return kv_prefill_parts(shape).total * sizeof(float);
+}
+
+int wha_wave_kv_prefill(const float* x, const wha_wave_weights* w, const wha_wave_shape* shape,
+                        const wha_wave_kv_cache* kv, float* out, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  static const char* fn = "wha_wave_kv_prefill";
+  int rc;
+  if ((rc = check_wave_shape(shape, fn)) || (rc = check_wave_weights(w, fn)) || (rc = check_kv(kv, fn))) return rc;
+  if (!x || !out) return fail(WHA_ERR_INVALID, "%s: x and out must be non-NULL", fn);
+  if (shape->T > kv->capacity)
+    return fail(WHA_ERR_INVALID, "%s: prompt length %d exceeds the cache capacity %d", fn, shape->T, kv->capacity);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const KvPrefillParts parts = kv_prefill_parts(shape);
+  void* wsv = nullptr;
+  if ((rc = resolve_workspace(workspace, workspace_bytes, parts.total * sizeof(float), s, fn, &wsv))) return rc;
+  float* p = static_cast<float*>(wsv);
+  float* proj = p;
+  p += parts.proj;
+  float* values = p;
+  p += parts.values;
+  float* feat = p;
+  p += parts.feat;
+  float* phase = p;
+  p += parts.phase;
+  int* bucket = reinterpret_cast<int*>(p);
+  p += parts.bucket;
+  float* merged = p;
+  p += parts.merged;
+  float* lse = p;
+
+  const int B = shape->B, T = shape->T, E = shape->n_embd, H = shape->n_head, C = shape->content_dim;
+  const int hd = E / H, HP = H * (2 + C), M = B * T;
+  const wha::View Lv = wave_view(shape);
+  hipError_t e = wha::launch_linear_fwd(x, E, w->proj_w, w->proj_b, proj, HP, M, HP, E, s);
+  if (e == hipSuccess)
+    e = wha::launch_linear_fwd_batched(x, E, hd, w->v_w, (int64_t)hd * hd, w->v_b, hd, values, E, hd, M, hd, hd, H,
+                                       s);
+  if (e == hipSuccess) e = wha::launch_wave_features(proj, w->harmonic_raw, feat, phase, bucket, B, H, T, C, 0, s);
+  if (e == hipSuccess)
+    e = wha::launch_wave_fwd(feat, bucket, values, merged, lse, Lv, vec_ok(Lv, {values, merged}), 0.f, s);
+  if (e == hipSuccess) e = wha::launch_linear_fwd(merged, E, w->out_w, w->out_b, out, E, M, E, E, s);
+  if (e == hipSuccess)
+    e = wha::launch_wave_kv_write(feat, bucket, phase, values, kv->cs, kv->bucket, kv->phase, kv->values, B, H, T,
+                                  hd, E, kv->capacity, s);
+  if (e != hipSuccess) return hip_fail(e, "wha_wave_kv_prefill launch");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+struct KvDecodeParts {
+  size_t proj, vnew, qinfo, merged, part, total;
+};
+
+static KvDecodeParts kv_decode_parts(const wha_wave_shape* sh, int capacity) {
+  auto r64 = [](size_t n) { return (n + 63) & ~(size_t)63; };
+  const size_t B = sh->B, E = sh->n_embd, H = sh->n_head, P = 2 + sh->content_dim;
+  KvDecodeParts p{};
+  p.proj = r64(B * H * P);
+  p.vnew = r64(B * E);
+  p.qinfo = r64(B * H * 4);
+  p.merged = r64(B * E);
+  p.part = r64(wha::wave_kv_decode_part_floats((int)(B * H), (int)(E / H), capacity));
+  p.total = p.proj + p.vnew + p.qinfo + p.merged + p.part;
+  return p;
+}
+
+size_t wha_wave_kv_decode_workspace_size(const wha_wave_shape* shape, int32_t capacity) {
+  if (check_wave_shape(shape, "wha_wave_kv_decode_workspace_size") != WHA_OK || capacity <= 0) return 0;
+  return kv_decode_parts(shape, capacity).total * sizeof(float);
+}
+
+int wha_wave_kv_decode(const float* x, const wha_wave_weights* w, const wha_wave_shape* shape,
+                       const wha_wave_kv_cache* kv, const int32_t* lengths, float* out, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  static const char* fn = "wha_wave_kv_decode";
+  int rc;
+  if ((rc = check_wave_shape(shape, fn)) || (rc = check_wave_weights(w, fn)) || (rc = check_kv(kv, fn))) return rc;
+  if (!x || !out || !lengths) return fail(WHA_ERR_INVALID, "%s: x, out and lengths must be non-NULL", fn);
+  if (shape->T != 1) return fail(WHA_ERR_INVALID, "%s: shape->T must be 1 (one new token per sequence)", fn);
+  if (shape->B > wha::kMaxKvBatch)
+    return fail(WHA_ERR_UNSUPPORTED, "%s: at most %d sequences per call (got %d)", fn, wha::kMaxKvBatch, shape->B);
+  wha::KvLens ll;
+  ll.n = shape->B;
+  int max_len = 0;
+  for (int b = 0; b < shape->B; ++b) {
+    if (lengths[b] < 0 || lengths[b] >= kv->capacity)
+      return fail(WHA_ERR_INVALID, "%s: lengths[%d] = %d must be in [0, %d) (room to append)", fn, b, lengths[b],
+                  kv->capacity);
+    ll.len[b] = lengths[b];
+    max_len = std::max(max_len, (int)lengths[b]);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const KvDecodeParts parts = kv_decode_parts(shape, kv->capacity);
+  void* wsv = nullptr;
+  if ((rc = resolve_workspace(workspace, workspace_bytes, parts.total * sizeof(float), s, fn, &wsv))) return rc;
+  float* p = static_cast<float*>(wsv);
+  float* proj = p;
+  p += parts.proj;
+  float* vnew = p;
+  p += parts.vnew;
+  float* qinfo = p;
+  p += parts.qinfo;
+  float* merged = p;
+  p += parts.merged;
+  float* part = p;
+
+  const int B = shape->B, E = shape->n_embd, H = shape->n_head, C = shape->content_dim;
+  const int hd = E / H, P = 2 + C, HP = H * P;
+  const bool vec = hd % 4 == 0 && aligned16(kv->values);
+  hipError_t e = wha::launch_linear_fwd(x, E, w->proj_w, w->proj_b, proj, HP, B, HP, E, s);
+  if (e == hipSuccess)
+    e = wha::launch_linear_fwd_batched(x, E, hd, w->v_w, (int64_t)hd * hd, w->v_b, hd, vnew, E, hd, B, hd, hd, H, s);
+  if (e == hipSuccess)
+    e = wha::launch_wave_kv_decode(proj, w->harmonic_raw, vnew, merged, kv->cs, kv->bucket, kv->phase, kv->values,
+                                   qinfo, part, ll, B, H, P, hd, E, kv->capacity, max_len, vec, s);
+  if (e == hipSuccess) e = wha::launch_linear_fwd(merged, E, w->out_w, w->out_b, out, E, B, E, E, s);
+  if (e != hipSuccess) return hip_fail(e, "wha_wave_kv_decode launch");
   g_err[0] = 0;
   return WHA_OK;
 }

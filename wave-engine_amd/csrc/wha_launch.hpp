@@ -100,9 +100,10 @@ hipError_t launch_dq_from_ds(const float* k, const float* ds, float* dq, const V
                              const char* name, hipStream_t stream);
 
 // ---- wave (harmonic coherence) attention ----
-// proj [B][T][H][2+C] -> feat [B][H][T][kWaveFeatures], phase, bucket [B][H][T].
+// proj [B][T][H][2+C] -> feat [B][H][T][kWaveFeatures], phase, bucket [B][H][T];
+// the first C_used content columns become features (0: the phase-only score).
 hipError_t launch_wave_features(const float* proj, const float* hraw, float* feat, float* phase, int* bucket,
-                                int B, int H, int T, int C, hipStream_t stream);
+                                int B, int H, int T, int C, int C_used, hipStream_t stream);
 // Fused forward over the per-head values (view Lv, D = head_dim): merged
 // head outputs (same view) and natural-log LSE [B][H][T].
 hipError_t launch_wave_fwd(const float* feat, const int* bucket, const float* v, float* merged, float* lse,
@@ -119,5 +120,23 @@ hipError_t launch_wave_probs_rows(const float* feat, const int* bucket, const fl
 hipError_t launch_wave_feat_bwd(const float* proj, const float* feat, const float* phase, const float* dfq,
                                 const float* dfk, const float* hraw, float* dproj, float* hpart, float* d_hraw,
                                 int B, int H, int T, int C, float cs, hipStream_t stream);
+
+// ---- wave attention KV cache (serving) ----
+constexpr int kMaxKvBatch = 256;
+struct KvLens {  // cached positions per sequence (kernel argument by value)
+  int n;
+  int len[kMaxKvBatch];
+};
+int wave_kv_chunk(int max_len);
+size_t wave_kv_decode_part_floats(int BH, int hd, int max_len);
+// Cache entries of positions [0, T) from a prompt's forward intermediates.
+hipError_t launch_wave_kv_write(const float* feat, const int* bucket, const float* phase, const float* values,
+                                float* cs, int* bk, float* ph, float* vc, int B, int H, int T, int hd, int E,
+                                int cap, hipStream_t stream);
+// One decode step: proj [B][H][2+C], vnew [B][E] -> merged [B][E]; appends at lengths[b].
+// qinfo: [B*H*4] scratch, part: wave_kv_decode_part_floats(B*H, hd, max_len) scratch.
+hipError_t launch_wave_kv_decode(const float* proj, const float* hraw, const float* vnew, float* merged, float* cs,
+                                 int* bk, float* ph, float* vc, float* qinfo, float* part, const KvLens& ll, int B,
+                                 int H, int P, int hd, int E, int cap, int max_len, bool vec, hipStream_t stream);
 
 }  // namespace wha
