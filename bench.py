@@ -11,7 +11,7 @@ credited FLOPs (12*B*H*D*P, P = T(T+1)/2), a roofline object for the dominant
 kernel (algorithmic FLOPs per launch / its average HIP-event duration), and the
 CPU baseline (the reference-order f32 oracle, one thread per sequence).
 
-    python bench.py [--steps K] [--warmup W] [--config 768|384|168|4096|decode|wave]
+    python bench.py [--steps K] [--warmup W] [--config 768|384|168|4096|decode|wave|wavedecode]
 
 --config wave measures the wave (harmonic coherence) attention layer the
 reference trains with, forward and full backward with its projections.
@@ -39,6 +39,8 @@ CONFIGS = {
     "decode": dict(name="768-dim decode (serve tier)", B=64, H=12, T=8192, D=64),
     "wave": dict(name="768-dim wave attention (harmonic coherence, content 16), full fwd+bwd", B=8, H=12,
                  T=1024, D=64, C=16),
+    "wavedecode": dict(name="768-dim wave-attention KV-cache decode (serve tier), 64 sequences x 8192 cached",
+                       B=64, H=12, T=8192, D=64, C=16),
 }
 
 METRIC = "causal attn fwd+bwd tokens/s & TFLOP/s (% fp32 MFMA peak), 768-dim seq1024"
@@ -276,6 +278,76 @@ def run_wave(args, cfg, pkg, torch):
     }
 
 
+def run_wave_decode(args, cfg, pkg, torch):
+    """One forward_one attention step (projections, split-K decode over the
+    cache, merge + append, out_proj) for B sequences with L cached positions
+    each; the counts are reset before every step, so each step redoes the same
+    work at length L (the append rewrites position L)."""
+    import numpy as np
+    B, H, L, D, C = cfg["B"], cfg["H"], cfg["T"], cfg["D"], cfg["C"]
+    E = H * D
+    dev = torch.device("cuda:0")
+    g = pkg.SynthStream(42)
+    t = lambda n, sd, *shape: torch.from_numpy(g.normal(n, sd).reshape(*shape)).to(dev)
+    W = pkg.WaveAttnWeights(t(H, 1.0, H), t(H * (2 + C) * E, 1 / np.sqrt(E), H, 2 + C, E),
+                            t(H * (2 + C), 0.1, H, 2 + C), t(H * D * D, 1 / np.sqrt(D), H, D, D), t(H * D, 0.1, H, D),
+                            t(E * E, 1 / np.sqrt(E), E, E), t(E, 0.1, E))
+    cache = pkg.WaveKvCache(B, H, D, L + 1, dev)
+    for b0 in range(0, B, 16):  # prefill the prompts in groups of 16 sequences
+        pkg.prefill_attention(W, t(16 * L * E, 1.0, 16, L, E), cache, first_seq=b0)
+    torch.cuda.synchronize()
+    xn = t(B * E, 1.0, B, E)
+    shape = pkg.WaveShape(B, 1, E, H, C)
+    ws = torch.empty(pkg.wave_kv_decode_workspace_bytes(shape, cache.capacity) // 4 + 64, dtype=torch.float32,
+                     device=dev)
+
+    def step():
+        cache.lengths = [L] * B
+        return pkg.forward_one_attention(W, xn, cache, workspace=ws)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    pkg.timing_reset()
+    pkg.timing_enable(True)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    pkg.timing_enable(False)
+    kern = {}
+    for name in ("linear_fwd", "wave_kv_query", "wave_kv_split", "wave_kv_merge"):
+        ms, n = pkg.timing_read(name)
+        kern[name] = {"total_ms": ms / args.steps, "avg_ms": ms / max(n, 1)}
+    pkg.timing_reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    # algorithmic bytes of the split kernel: cos/sin and bucket of every cached
+    # position, plus the value rows of the positions the mask admits
+    bk = cache.bucket[:, :, :L]
+    qb = cache.bucket[:, :, L:L + 1]
+    near = ((bk - qb + 1) & 7) <= 2
+    near[:, :, L - 1] = True
+    n_valid = int(near.sum().item())
+    alg_bytes = B * H * L * 12 + n_valid * D * 4
+    achieved = alg_bytes / (kern["wave_kv_split"]["avg_ms"] * 1e-3) / 1e9
+    return {"metric": "wave-attention KV-cache decode tokens/s (one new token per sequence), 768-dim, 8192 cached",
+            "value": B / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic prompts (seeded), random-init weights",
+            "config": {"workload": cfg["name"], "batch": B, "heads": H, "cached": L, "head_dim": D,
+                       "content_dim": C},
+            "kernel_ms_per_step": {n: round(kern[n]["total_ms"], 5) for n in kern},
+            "mask_fraction": n_valid / (B * H * L),
+            "roofline": {"kernel": "wave_kv_split", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                         "traffic": load_traffic("wave_kv_split", cfg), "algorithmic_bytes_per_launch": alg_bytes,
+                         "avg_launch_ms": kern["wave_kv_split"]["avg_ms"]}}
+
+
 def wave_cpu_baseline(cfg, seed=42, max_threads=None, min_seconds=10.0):
     """Reference-order f32 oracle of wave_attention_forward + backward_full, one
     thread per sequence on a bounded sample, repeated to at least min_seconds."""
@@ -361,9 +433,11 @@ def main():
         res = run_decode(args, cfg, pkg, torch)
     elif args.config == "wave":
         res = run_wave(args, cfg, pkg, torch)
+    elif args.config == "wavedecode":
+        res = run_wave_decode(args, cfg, pkg, torch)
     else:
         res = run_attention(args, cfg, pkg, torch)
-    if args.config == "decode":
+    if args.config in ("decode", "wavedecode"):
         res["cpu_baseline"] = None
     elif not args.no_cpu_baseline:
         res["cpu_baseline"] = wave_cpu_baseline(cfg) if args.config == "wave" else cpu_baseline(cfg)

@@ -763,6 +763,10 @@ def prefill_attention(weights: WaveAttnWeights, x, cache: WaveKvCache, first_seq
     return out
 
 
+def wave_kv_decode_workspace_bytes(shape: WaveShape, capacity: int) -> int:
+    return int(lib().wha_wave_kv_decode_workspace_size(ctypes.byref(shape), capacity))
+
+
 def forward_one_attention(weights: WaveAttnWeights, x, cache: WaveKvCache, workspace=None):
     """forward_one's attention (kv_cache.rs:263-335) for one new token of every
     sequence: x [B][n_embd] -> out [B][n_embd]; appends the tokens and advances
@@ -775,8 +779,8 @@ def forward_one_attention(weights: WaveAttnWeights, x, cache: WaveKvCache, works
     shape = WaveShape(cache.B, 1, weights.n_embd, weights.n_head, weights.content_dim)
     ws = workspace
     if ws is None:
-        ws = torch.empty(int(lib().wha_wave_kv_decode_workspace_size(ctypes.byref(shape), cache.capacity)) // 4
-                         + 64, dtype=torch.float32, device=x.device)
+        ws = torch.empty(wave_kv_decode_workspace_bytes(shape, cache.capacity) // 4 + 64, dtype=torch.float32,
+                         device=x.device)
     lens = (ctypes.c_int32 * cache.B)(*cache.lengths)
     out = torch.empty_like(x)
     _check("wha_wave_kv_decode", lib().wha_wave_kv_decode(

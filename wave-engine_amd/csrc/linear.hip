@@ -254,19 +254,19 @@ __global__ __launch_bounds__(256) void colsum_final_kernel(const float* __restri
 
 namespace {
 
-int gemm_splits(int M, int N, int K, int batch) {
+// Split-K factor: aim for >= 512 blocks while keeping >= min_k k per split.
+int gemm_splits(int M, int N, int K, int batch, int min_k = 256) {
   const int tiles = ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN) * batch;
   int splits = 1;
-  // aim for >= 512 blocks while keeping >= 256 k per split
-  while (tiles * splits < 512 && (K / (splits * 2)) >= 256) splits *= 2;
+  while (tiles * splits < 512 && (K / (splits * 2)) >= min_k) splits *= 2;
   return splits;
 }
 
 int colsum_chunks(int M) { return M >= 4096 ? 64 : (M >= 256 ? 16 : 1); }
 
 template <bool A_KC, bool B_KC>
-hipError_t gemm_t(GemmArgs g, float* ws, const char* name, hipStream_t stream) {
-  const int splits = ws ? gemm_splits(g.M, g.N, g.K, g.batch) : 1;
+hipError_t gemm_t(GemmArgs g, float* ws, const char* name, hipStream_t stream, int min_k = 256) {
+  const int splits = ws ? gemm_splits(g.M, g.N, g.K, g.batch, min_k) : 1;
   g.splits = splits;
   const dim3 grid((g.N + kGBN - 1) / kGBN, (g.M + kGBM - 1) / kGBM, splits * g.batch);
   TimingScope ts(name, stream);
@@ -300,10 +300,19 @@ size_t linear_dw_workspace_floats(int N, int K, int64_t M, int batch) {
   return part + (size_t)colsum_chunks((int)M) * N * batch + 64;
 }
 
-// y[bt] = x[bt] w[bt]^T + b[bt]:  x [M][K] (row stride ldx), w [N][K], y [M][N] (row stride ldy)
+// Few output tiles (decode-sized M): split K down to 64 per split.
+constexpr int kFwdMinK = 64;
+
+size_t linear_fwd_workspace_floats(int M, int N, int K, int batch) {
+  const int splits = gemm_splits(M, N, K, batch, kFwdMinK);
+  return splits > 1 ? (size_t)splits * batch * M * N : 0;
+}
+
+// y[bt] = x[bt] w[bt]^T + b[bt]:  x [M][K] (row stride ldx), w [N][K], y [M][N] (row stride ldy);
+// ws (linear_fwd_workspace_floats, or nullptr for no split-K) lets few-tile shapes split K.
 hipError_t launch_linear_fwd_batched(const float* x, int64_t ldx, int64_t x_sb, const float* w, int64_t w_sb,
                                      const float* b, int64_t b_sb, float* y, int64_t ldy, int64_t y_sb, int M,
-                                     int N, int K, int batch, hipStream_t stream) {
+                                     int N, int K, int batch, hipStream_t stream, float* ws) {
   GemmArgs g{x, ldx, 1, w, (int64_t)K, 1, y, ldy, b, M, N, K, 0,
              aligned16(y) && ldy % 4 == 0 && y_sb % 4 == 0, false};
   g.batch = batch;
@@ -311,7 +320,7 @@ hipError_t launch_linear_fwd_batched(const float* x, int64_t ldx, int64_t x_sb, 
   g.b_sb = w_sb;
   g.c_sb = y_sb;
   g.bias_sb = b_sb;
-  return gemm_t<true, true>(g, nullptr, "linear_fwd", stream);
+  return gemm_t<true, true>(g, ws, "linear_fwd", stream, kFwdMinK);
 }
 
 // dx[bt] (+)= dy[bt] w[bt]:  dy [M][N], w [N][K], dx [M][K]

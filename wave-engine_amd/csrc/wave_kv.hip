@@ -10,11 +10,12 @@
 // path -- then appends its entry at index lengths[b].
 //
 // The decode is a stream over the cache, HBM-bound, so it follows the split-K
-// design of the dot-product decode: 16 lanes per key, each 16-lane group keeps
-// its own online-softmax state, a block covers one chunk of one (b,h), and a
+// design of the dot-product decode: a block covers one chunk of one (b,h), a
 // merge kernel combines the chunks with the self term and writes the appended
-// entry.  The bucket test runs before the value row is loaded, so the rows of
-// masked positions (about 5/8 of the cache) are never read.
+// entry.  Within a block the bucket test runs first for the whole chunk and
+// only the admitted positions are listed, so the value rows of masked
+// positions (about 5/8 of the cache) are never read; 16 lanes then share each
+// listed row, each 16-lane group keeping its own online-softmax state.
 #include "wha_launch.hpp"
 
 namespace wha {
@@ -23,6 +24,7 @@ namespace {
 constexpr int kKvThreads = 256;
 constexpr int kKvGroups = kKvThreads / 16;
 constexpr int kKvUnroll = 4;
+constexpr int kKvMaxChunk = 1024;  // keys per block (wave_kv_chunk never exceeds it)
 
 __device__ __forceinline__ int phase_bucket_kv(float phi) {
   const float tau = 6.28318548f;  // std::f32::consts::TAU
@@ -57,7 +59,12 @@ __global__ __launch_bounds__(256) void wave_kv_query_kernel(const float* __restr
   qinfo[i] = make_float4(cn, sn, phi, __int_as_float(phase_bucket_kv(phi)));
 }
 
-// One chunk of one (b,h): partial (max, sum, o[DP]) in the log2 domain.
+// One chunk (<= 1024 keys) of one (b,h): partial (max, sum, o[DP]) in the log2
+// domain.  Pass 1: every thread tests up to four keys (coalesced bucket and
+// cos/sin loads), and the admitted keys with their scores are compacted into
+// an LDS list in key order (wave ballots + prefix counts).  Pass 2: 16-lane
+// groups stream the value rows of the listed keys only -- all addresses known
+// up front, so the loads of a group's four keys in flight are independent.
 template <int DP, bool VEC>
 __global__ __launch_bounds__(kKvThreads) void wave_kv_split_kernel(const float4* __restrict__ qinfo,
                                                                    const float2* __restrict__ CS,
@@ -66,6 +73,10 @@ __global__ __launch_bounds__(kKvThreads) void wave_kv_split_kernel(const float4*
                                                                    float* __restrict__ part, KvLens ll, int H,
                                                                    int hd, int cap, int chunk, int n_split) {
   constexpr int NPL = DP / 16;
+  constexpr int KPT = kKvMaxChunk / kKvThreads;  // keys tested per thread
+  __shared__ int list_k[kKvMaxChunk];
+  __shared__ float list_s[kKvMaxChunk];
+  __shared__ int wave_cnt[KPT][kKvThreads / 64];
   __shared__ float sm_m[kKvGroups], sm_l[kKvGroups];
   __shared__ float sm_o[kKvGroups][DP];
 
@@ -74,37 +85,68 @@ __global__ __launch_bounds__(kKvThreads) void wave_kv_split_kernel(const float4*
   const int b = bh / H;
   const int len = ll.len[b];
   const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
   const int grp = tid >> 4, sub = tid & 15;
   const int d0 = sub * NPL;
   const float4 q = qinfo[bh];
   const float cq = q.x * kLog2e, sq = q.y * kLog2e;
   const int qb = __float_as_int(q.w);
   const int64_t hb = (int64_t)bh * cap;
-
   const int k_begin = split * chunk;
   const int k_end = min(len, k_begin + chunk);
+
+  // pass 1: test, score and compact
+  bool valid[KPT];
+  float score[KPT];
+  int pos[KPT];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int key = k_begin + i * kKvThreads + tid;
+    const bool in = key < k_end;
+    const int kb = in ? BK[hb + key] : 0;
+    const float2 c = in ? CS[hb + key] : make_float2(0.f, 0.f);
+    valid[i] = in && (bucket_near_kv(kb, qb) || key == len - 1);
+    score[i] = cq * c.x + sq * c.y;
+    const unsigned long long mask = __ballot(valid[i]);
+    pos[i] = __popcll(mask & ((1ull << lane) - 1ull));
+    if (lane == 0) wave_cnt[i][wave] = __popcll(mask);
+  }
+  __syncthreads();
+  int n_list = 0;
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    int before = n_list;
+    for (int w = 0; w < kKvThreads / 64; ++w) {
+      if (w < wave) before += wave_cnt[i][w];
+      n_list += wave_cnt[i][w];
+    }
+    if (valid[i]) {
+      list_k[before + pos[i]] = k_begin + i * kKvThreads + tid;
+      list_s[before + pos[i]] = score[i];
+    }
+  }
+  __syncthreads();
+
+  // pass 2: value rows of the listed keys, four in flight per group
   float m = -1e30f, l = 0.f;
   float acc[NPL];
 #pragma unroll
   for (int e = 0; e < NPL; ++e) acc[e] = 0.f;
-
-  for (int k0 = k_begin + grp; k0 < k_end; k0 += kKvGroups * kKvUnroll) {
+  for (int j0 = grp; j0 < n_list; j0 += kKvGroups * kKvUnroll) {
     float sc[kKvUnroll];
     float vv[kKvUnroll][NPL];
 #pragma unroll
     for (int u = 0; u < kKvUnroll; ++u) {
-      const int key = k0 + u * kKvGroups;
-      const bool in = key < k_end;
-      const int kb = in ? BK[hb + key] : 0;
-      const float2 c = in ? CS[hb + key] : make_float2(0.f, 0.f);
-      const bool valid = in && (bucket_near_kv(kb, qb) || key == len - 1);
-      sc[u] = valid ? cq * c.x + sq * c.y : -INFINITY;
+      const int j = j0 + u * kKvGroups;
+      const bool in = j < n_list;
+      const int key = in ? list_k[j] : 0;
+      sc[u] = in ? list_s[j] : -INFINITY;
       const float* vp = Vc + (hb + key) * hd + d0;
       if (VEC && NPL % 4 == 0) {
 #pragma unroll
         for (int e4 = 0; e4 < NPL / 4; ++e4) {
           float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-          if (valid && d0 + 4 * e4 < hd) a = *reinterpret_cast<const float4*>(vp + 4 * e4);
+          if (in && d0 + 4 * e4 < hd) a = *reinterpret_cast<const float4*>(vp + 4 * e4);
           vv[u][4 * e4 + 0] = a.x;
           vv[u][4 * e4 + 1] = a.y;
           vv[u][4 * e4 + 2] = a.z;
@@ -112,7 +154,7 @@ __global__ __launch_bounds__(kKvThreads) void wave_kv_split_kernel(const float4*
         }
       } else {
 #pragma unroll
-        for (int e = 0; e < NPL; ++e) vv[u][e] = (valid && d0 + e < hd) ? vp[e] : 0.f;
+        for (int e = 0; e < NPL; ++e) vv[u][e] = (in && d0 + e < hd) ? vp[e] : 0.f;
       }
     }
     float mx = -INFINITY;
@@ -141,7 +183,7 @@ __global__ __launch_bounds__(kKvThreads) void wave_kv_split_kernel(const float4*
   for (int e = 0; e < NPL; ++e) sm_o[grp][d0 + e] = acc[e];
   __syncthreads();
 
-  // groups whose keys were all masked keep the finite floor and l = 0, o = 0
+  // groups that listed no key keep the finite floor and l = 0, o = 0
   float* out = part + ((int64_t)bh * n_split + split) * (DP + 2);
   float M = -1e30f;
 #pragma unroll

@@ -681,7 +681,7 @@ int wha_wave_kv_prefill(const float* x, const wha_wave_weights* w, const wha_wav
 }
 
 struct KvDecodeParts {
-  size_t proj, vnew, qinfo, merged, part, total;
+  size_t proj, vnew, qinfo, merged, part, gemm, total;
 };
 
 static KvDecodeParts kv_decode_parts(const wha_wave_shape* sh, int capacity) {
@@ -693,7 +693,12 @@ static KvDecodeParts kv_decode_parts(const wha_wave_shape* sh, int capacity) {
   p.qinfo = r64(B * H * 4);
   p.merged = r64(B * E);
   p.part = r64(wha::wave_kv_decode_part_floats((int)(B * H), (int)(E / H), capacity));
-  p.total = p.proj + p.vnew + p.qinfo + p.merged + p.part;
+  const int hd = (int)(E / H);
+  size_t g = wha::linear_fwd_workspace_floats((int)B, (int)(H * P), (int)E, 1);
+  g = std::max(g, wha::linear_fwd_workspace_floats((int)B, hd, hd, (int)H));
+  g = std::max(g, wha::linear_fwd_workspace_floats((int)B, (int)E, (int)E, 1));
+  p.gemm = r64(g);
+  p.total = p.proj + p.vnew + p.qinfo + p.merged + p.part + p.gemm;
   return p;
 }
 
@@ -736,17 +741,21 @@ int wha_wave_kv_decode(const float* x, const wha_wave_weights* w, const wha_wave
   float* merged = p;
   p += parts.merged;
   float* part = p;
+  p += parts.part;
+  float* gws = p;
 
   const int B = shape->B, E = shape->n_embd, H = shape->n_head, C = shape->content_dim;
   const int hd = E / H, P = 2 + C, HP = H * P;
   const bool vec = hd % 4 == 0 && aligned16(kv->values);
-  hipError_t e = wha::launch_linear_fwd(x, E, w->proj_w, w->proj_b, proj, HP, B, HP, E, s);
+  hipError_t e = wha::launch_linear_fwd_batched(x, E, 0, w->proj_w, 0, w->proj_b, 0, proj, HP, 0, B, HP, E, 1, s, gws);
   if (e == hipSuccess)
-    e = wha::launch_linear_fwd_batched(x, E, hd, w->v_w, (int64_t)hd * hd, w->v_b, hd, vnew, E, hd, B, hd, hd, H, s);
+    e = wha::launch_linear_fwd_batched(x, E, hd, w->v_w, (int64_t)hd * hd, w->v_b, hd, vnew, E, hd, B, hd, hd, H, s,
+                                       gws);
   if (e == hipSuccess)
     e = wha::launch_wave_kv_decode(proj, w->harmonic_raw, vnew, merged, kv->cs, kv->bucket, kv->phase, kv->values,
                                    qinfo, part, ll, B, H, P, hd, E, kv->capacity, max_len, vec, s);
-  if (e == hipSuccess) e = wha::launch_linear_fwd(merged, E, w->out_w, w->out_b, out, E, B, E, E, s);
+  if (e == hipSuccess)
+    e = wha::launch_linear_fwd_batched(merged, E, 0, w->out_w, 0, w->out_b, 0, out, E, 0, B, E, E, 1, s, gws);
   if (e != hipSuccess) return hip_fail(e, "wha_wave_kv_decode launch");
   g_err[0] = 0;
   return WHA_OK;

@@ -80,9 +80,12 @@ size_t linear_dw_workspace_floats(int N, int K, int64_t M, int batch);
 hipError_t launch_linear_bwd_dw(const float* dy, int64_t lddy, const float* x, int64_t ldx, float* dw, float* db,
                                 int M, int N, int K, float* ws, hipStream_t stream);
 // Batched forms: `batch` independent problems, operand bt offset by bt * (its _sb stride).
+// ws: linear_fwd_workspace_floats floats (split-K for shapes with few output
+// tiles) or nullptr (no split).
+size_t linear_fwd_workspace_floats(int M, int N, int K, int batch);
 hipError_t launch_linear_fwd_batched(const float* x, int64_t ldx, int64_t x_sb, const float* w, int64_t w_sb,
                                      const float* b, int64_t b_sb, float* y, int64_t ldy, int64_t y_sb, int M,
-                                     int N, int K, int batch, hipStream_t stream);
+                                     int N, int K, int batch, hipStream_t stream, float* ws = nullptr);
 hipError_t launch_linear_bwd_dx_batched(const float* dy, int64_t lddy, int64_t dy_sb, const float* w,
                                         int64_t w_sb, float* dx, int64_t lddx, int64_t dx_sb, int M, int N,
                                         int K, int batch, bool accumulate, hipStream_t stream);
