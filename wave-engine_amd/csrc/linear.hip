@@ -20,10 +20,14 @@
 // second kernel sums in a fixed order (deterministic).
 #include "wha_launch.hpp"
 
+#ifndef WHA_GEMM_KT
+#define WHA_GEMM_KT 32
+#endif
+
 namespace wha {
 
 namespace {
-constexpr int kGBM = 128, kGBN = 128, kGKT = 16, kGLD = kGKT + 4;
+constexpr int kGBN = 128;  // output columns per block (2 waves x 64)
 }
 
 struct GemmArgs {
@@ -35,7 +39,7 @@ struct GemmArgs {
   int64_t ldc;         // C(m,n) = c[m*ldc + n]  (or the split-K partial [z][M][N])
   const float* bias;   // [N] or nullptr
   int M, N, K;
-  int k_chunk;         // k range per split (multiple of 16)
+  int k_chunk;         // k range per split (multiple of the stage depth)
   bool c_vec;          // c, ldc and c_sb allow 128-bit stores
   bool accumulate;     // C += result instead of C = result
   int batch = 1;       // independent GEMMs, operands offset by the strides below
@@ -43,21 +47,27 @@ struct GemmArgs {
   int64_t a_sb = 0, b_sb = 0, c_sb = 0, bias_sb = 0;
 };
 
-// Staging of one 128 x 16 operand tile (rows r = m or n, k contiguous in LDS);
-// element (r, k) of the source is p[r*s_r + k*s_k].  KC: s_k == 1 (rows of the
-// tile are source rows); otherwise s_r == 1 and the tile is transposed on the
-// way in.
-template <bool KC>
+// Staging of one ROWS x KT operand tile (rows r = m or n, k contiguous in LDS
+// with pitch KT + 4); element (r, k) of the source is p[r*s_r + k*s_k].  KC:
+// s_k == 1 (rows of the tile are source rows, 128-bit loads); otherwise s_r == 1
+// and each thread gathers four consecutive k of one row with 32-bit loads, so
+// the tile is transposed on the way in and still lands in LDS with one 128-bit
+// store per thread.
+template <int ROWS, int KT, bool KC>
 struct GemmStage {
-  float4 v[2];
+  static constexpr int LD = KT + 4;
+  static constexpr int NF4 = ROWS * KT / 4;
+  static constexpr int PER = NF4 / 256;
+  static_assert(NF4 % 256 == 0, "tile must split evenly over 256 threads");
+  float4 v[PER];
   __device__ __forceinline__ void load(const float* __restrict__ p, int64_t s_r, int64_t s_k, int r0, int R,
                                        int k0, int k_end, int tid) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < PER; ++q) {
       const int idx = tid + 256 * q;
       float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
       if (KC) {
-        const int rr = idx >> 2, c = (idx & 3) * 4;
+        const int rr = idx / (KT / 4), c = (idx % (KT / 4)) * 4;
         const int r = r0 + rr, k = k0 + c;
         if (r < R) {
           const float* src = p + (int64_t)r * s_r + (int64_t)k * s_k;
@@ -71,18 +81,16 @@ struct GemmStage {
           }
         }
       } else {
-        const int kr = idx >> 5, rc = (idx & 31) * 4;
-        const int r = r0 + rc, k = k0 + kr;
-        if (k < k_end) {
+        // one row, four consecutive k: each of the four loads is coalesced
+        // across the wave (consecutive lanes, consecutive rows)
+        const int rr = idx % ROWS, kq = idx / ROWS;
+        const int r = r0 + rr, k = k0 + 4 * kq;
+        if (r < R) {
           const float* src = p + (int64_t)k * s_k + (int64_t)r * s_r;
-          if (r + 3 < R && (((uintptr_t)src) & 15) == 0) {
-            val = *reinterpret_cast<const float4*>(src);
-          } else {
-            if (r + 0 < R) val.x = src[0];
-            if (r + 1 < R) val.y = src[1];
-            if (r + 2 < R) val.z = src[2];
-            if (r + 3 < R) val.w = src[3];
-          }
+          if (k + 0 < k_end) val.x = src[0];
+          if (k + 1 < k_end) val.y = src[s_k];
+          if (k + 2 < k_end) val.z = src[2 * s_k];
+          if (k + 3 < k_end) val.w = src[3 * s_k];
         }
       }
       v[q] = val;
@@ -90,82 +98,87 @@ struct GemmStage {
   }
   __device__ __forceinline__ void store(float* lds, int tid) const {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < PER; ++q) {
       const int idx = tid + 256 * q;
       if (KC) {
-        const int rr = idx >> 2, c = (idx & 3) * 4;
-        *reinterpret_cast<float4*>(lds + rr * kGLD + c) = v[q];
+        const int rr = idx / (KT / 4), c = (idx % (KT / 4)) * 4;
+        *reinterpret_cast<float4*>(lds + rr * LD + c) = v[q];
       } else {
-        const int kr = idx >> 5, rc = (idx & 31) * 4;
-        lds[(rc + 0) * kGLD + kr] = v[q].x;
-        lds[(rc + 1) * kGLD + kr] = v[q].y;
-        lds[(rc + 2) * kGLD + kr] = v[q].z;
-        lds[(rc + 3) * kGLD + kr] = v[q].w;
+        const int rr = idx % ROWS, kq = idx / ROWS;
+        *reinterpret_cast<float4*>(lds + rr * LD + 4 * kq) = v[q];
       }
     }
   }
 };
 
-template <bool A_KC, bool B_KC, bool PARTIAL>
+// BM x 128 output tile per 256-thread block, 2 x 2 waves of (BM/2) x 64,
+// KT-deep k stages.  MFMA rows are output columns n, MFMA columns output rows m.
+template <int BM, int KT, bool A_KC, bool B_KC, bool PARTIAL>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
-  __shared__ __align__(16) float As[kGBM * kGLD];
-  __shared__ __align__(16) float Bs[kGBN * kGLD];
+  constexpr int LD = KT + 4;
+  constexpr int MT = BM / 32;  // 16-row m tiles per wave
+  __shared__ __align__(16) float As[BM * LD];
+  __shared__ __align__(16) float Bs[kGBN * LD];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int lq = lane & 15, gq = lane >> 4;
   const int wn = wave & 1, wm = wave >> 1;
-  const int n0 = blockIdx.x * kGBN, m0 = blockIdx.y * kGBM;
+  const int n0 = blockIdx.x * kGBN, m0 = blockIdx.y * BM;
   const int bt = (int)blockIdx.z / g.splits;
   const int k_begin = ((int)blockIdx.z % g.splits) * g.k_chunk;
   const float* __restrict__ A = g.a + bt * g.a_sb;
   const float* __restrict__ Bm = g.b + bt * g.b_sb;
   const int k_end = min(g.K, k_begin + g.k_chunk);
 
-  floatx4 acc[4][4];
+  floatx4 acc[4][MT];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < MT; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  GemmStage<A_KC> sa;
-  GemmStage<B_KC> sb;
+  GemmStage<BM, KT, A_KC> sa;
+  GemmStage<kGBN, KT, B_KC> sb;
   if (k_begin < k_end) {
     sa.load(A, g.a_sm, g.a_sk, m0, g.M, k_begin, k_end, tid);
     sb.load(Bm, g.b_sn, g.b_sk, n0, g.N, k_begin, k_end, tid);
   }
-  for (int kk = k_begin; kk < k_end; kk += kGKT) {
+  for (int kk = k_begin; kk < k_end; kk += KT) {
     __syncthreads();
     sa.store(As, tid);
     sb.store(Bs, tid);
     __syncthreads();
-    if (kk + kGKT < k_end) {
-      sa.load(A, g.a_sm, g.a_sk, m0, g.M, kk + kGKT, k_end, tid);
-      sb.load(Bm, g.b_sn, g.b_sk, n0, g.N, kk + kGKT, k_end, tid);
-    }
-    float4 bv[4], av[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      bv[t] = *reinterpret_cast<const float4*>(&Bs[(64 * wn + 16 * t + lq) * kGLD + 4 * gq]);
-      av[t] = *reinterpret_cast<const float4*>(&As[(64 * wm + 16 * t + lq) * kGLD + 4 * gq]);
+    if (kk + KT < k_end) {
+      sa.load(A, g.a_sm, g.a_sk, m0, g.M, kk + KT, k_end, tid);
+      sb.load(Bm, g.b_sn, g.b_sk, n0, g.N, kk + KT, k_end, tid);
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int ks = 0; ks < KT; ks += 16) {
+      float4 bv[4], av[MT];
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const float bvals[4] = {bv[nt].x, bv[nt].y, bv[nt].z, bv[nt].w};
+      for (int t = 0; t < 4; ++t)
+        bv[t] = *reinterpret_cast<const float4*>(&Bs[(64 * wn + 16 * t + lq) * LD + ks + 4 * gq]);
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const float avals[4] = {av[mt].x, av[mt].y, av[mt].z, av[mt].w};
-          acc[nt][mt] = mfma4(bvals[e], avals[e], acc[nt][mt]);
+      for (int t = 0; t < MT; ++t)
+        av[t] = *reinterpret_cast<const float4*>(&As[((BM / 2) * wm + 16 * t + lq) * LD + ks + 4 * gq]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          const float bvals[4] = {bv[nt].x, bv[nt].y, bv[nt].z, bv[nt].w};
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const float avals[4] = {av[mt].x, av[mt].y, av[mt].z, av[mt].w};
+            acc[nt][mt] = mfma4(bvals[e], avals[e], acc[nt][mt]);
+          }
         }
       }
     }
   }
 
-  // acc[nt][mt][i] = C[m = m0+64wm+16mt+lq][n = n0+64wn+16nt+4gq+i]
+  // acc[nt][mt][i] = C[m = m0+(BM/2)wm+16mt+lq][n = n0+64wn+16nt+4gq+i]
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    const int m = m0 + 64 * wm + 16 * mt + lq;
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = m0 + (BM / 2) * wm + 16 * mt + lq;
     if (m >= g.M) continue;
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
@@ -254,9 +267,17 @@ __global__ __launch_bounds__(256) void colsum_final_kernel(const float* __restri
 
 namespace {
 
+// Tile height: 128 rows unless that leaves fewer than two blocks per CU.
+constexpr int kCUs = 256;
+int gemm_bm(int M, int N, int batch) {
+  const int tiles128 = ((M + 127) / 128) * ((N + kGBN - 1) / kGBN) * batch;
+  return tiles128 >= 2 * kCUs ? 128 : 64;
+}
+
 // Split-K factor: aim for >= 512 blocks while keeping >= min_k k per split.
 int gemm_splits(int M, int N, int K, int batch, int min_k = 256) {
-  const int tiles = ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN) * batch;
+  const int bm = gemm_bm(M, N, batch);
+  const int tiles = ((M + bm - 1) / bm) * ((N + kGBN - 1) / kGBN) * batch;
   int splits = 1;
   while (tiles * splits < 512 && (K / (splits * 2)) >= min_k) splits *= 2;
   return splits;
@@ -264,29 +285,35 @@ int gemm_splits(int M, int N, int K, int batch, int min_k = 256) {
 
 int colsum_chunks(int M) { return M >= 4096 ? 64 : (M >= 256 ? 16 : 1); }
 
-template <bool A_KC, bool B_KC>
-hipError_t gemm_t(GemmArgs g, float* ws, const char* name, hipStream_t stream, int min_k = 256) {
-  const int splits = ws ? gemm_splits(g.M, g.N, g.K, g.batch, min_k) : 1;
+template <int BM, int KT, bool A_KC, bool B_KC>
+hipError_t gemm_launch(GemmArgs g, float* ws, int splits, const char* name, hipStream_t stream) {
+  const dim3 grid((g.N + kGBN - 1) / kGBN, (g.M + BM - 1) / BM, splits * g.batch);
   g.splits = splits;
-  const dim3 grid((g.N + kGBN - 1) / kGBN, (g.M + kGBM - 1) / kGBM, splits * g.batch);
   TimingScope ts(name, stream);
   if (splits == 1) {
-    g.k_chunk = ((g.K + kGKT - 1) / kGKT) * kGKT;
-    hipLaunchKernelGGL((gemm_kernel<A_KC, B_KC, false>), grid, dim3(256), 0, stream, g);
+    g.k_chunk = ((g.K + KT - 1) / KT) * KT;
+    hipLaunchKernelGGL((gemm_kernel<BM, KT, A_KC, B_KC, false>), grid, dim3(256), 0, stream, g);
     return hipGetLastError();
   }
   const int per = (g.K + splits - 1) / splits;
   GemmArgs p = g;
-  p.k_chunk = ((per + kGKT - 1) / kGKT) * kGKT;
+  p.k_chunk = ((per + KT - 1) / KT) * KT;
   p.c = ws;
   p.bias = nullptr;
-  hipLaunchKernelGGL((gemm_kernel<A_KC, B_KC, true>), grid, dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((gemm_kernel<BM, KT, A_KC, B_KC, true>), grid, dim3(256), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t total = (int64_t)g.M * g.N * g.batch;
   hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
                      (const float*)ws, g);
   return hipGetLastError();
+}
+
+template <bool A_KC, bool B_KC>
+hipError_t gemm_t(GemmArgs g, float* ws, const char* name, hipStream_t stream, int min_k = 256) {
+  const int splits = ws ? gemm_splits(g.M, g.N, g.K, g.batch, min_k) : 1;
+  if (gemm_bm(g.M, g.N, g.batch) == 128) return gemm_launch<128, WHA_GEMM_KT, A_KC, B_KC>(g, ws, splits, name, stream);
+  return gemm_launch<64, WHA_GEMM_KT, A_KC, B_KC>(g, ws, splits, name, stream);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
