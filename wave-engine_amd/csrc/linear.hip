@@ -47,15 +47,17 @@ struct GemmArgs {
   int64_t a_sb = 0, b_sb = 0, c_sb = 0, bias_sb = 0;
 };
 
-// Staging of one ROWS x KT operand tile (rows r = m or n, k contiguous in LDS
-// with pitch KT + 4); element (r, k) of the source is p[r*s_r + k*s_k].  KC:
-// s_k == 1 (rows of the tile are source rows, 128-bit loads); otherwise s_r == 1
-// and each thread gathers four consecutive k of one row with 32-bit loads, so
-// the tile is transposed on the way in and still lands in LDS with one 128-bit
-// store per thread.
+// Staging of one ROWS x KT operand tile; element (r, k) of the source is
+// p[r*s_r + k*s_k].  KC (s_k == 1, rows of the tile are source rows): LDS
+// [ROWS][KT + 4], k contiguous.  Otherwise (s_r == 1, columns of the tile are
+// source rows): LDS [KT][ROWS + 4], rows contiguous.  Either way each thread
+// moves 128-bit pieces along the source's contiguous direction, so global loads
+// are coalesced and LDS stores are 128-bit and conflict-free.
 template <int ROWS, int KT, bool KC>
 struct GemmStage {
-  static constexpr int LD = KT + 4;
+  static constexpr int LDK = KT + 4;
+  static constexpr int LDR = ROWS + 4;
+  static constexpr int ELEMS = KC ? ROWS * LDK : KT * LDR;
   static constexpr int NF4 = ROWS * KT / 4;
   static constexpr int PER = NF4 / 256;
   static_assert(NF4 % 256 == 0, "tile must split evenly over 256 threads");
@@ -81,16 +83,18 @@ struct GemmStage {
           }
         }
       } else {
-        // one row, four consecutive k: each of the four loads is coalesced
-        // across the wave (consecutive lanes, consecutive rows)
-        const int rr = idx % ROWS, kq = idx / ROWS;
-        const int r = r0 + rr, k = k0 + 4 * kq;
-        if (r < R) {
+        const int kr = idx / (ROWS / 4), rc = (idx % (ROWS / 4)) * 4;
+        const int r = r0 + rc, k = k0 + kr;
+        if (k < k_end) {
           const float* src = p + (int64_t)k * s_k + (int64_t)r * s_r;
-          if (k + 0 < k_end) val.x = src[0];
-          if (k + 1 < k_end) val.y = src[s_k];
-          if (k + 2 < k_end) val.z = src[2 * s_k];
-          if (k + 3 < k_end) val.w = src[3 * s_k];
+          if (r + 3 < R && (((uintptr_t)src) & 15) == 0) {
+            val = *reinterpret_cast<const float4*>(src);
+          } else {
+            if (r + 0 < R) val.x = src[0];
+            if (r + 1 < R) val.y = src[1];
+            if (r + 2 < R) val.z = src[2];
+            if (r + 3 < R) val.w = src[3];
+          }
         }
       }
       v[q] = val;
@@ -102,23 +106,60 @@ struct GemmStage {
       const int idx = tid + 256 * q;
       if (KC) {
         const int rr = idx / (KT / 4), c = (idx % (KT / 4)) * 4;
-        *reinterpret_cast<float4*>(lds + rr * LD + c) = v[q];
+        *reinterpret_cast<float4*>(lds + rr * LDK + c) = v[q];
       } else {
-        const int rr = idx % ROWS, kq = idx / ROWS;
-        *reinterpret_cast<float4*>(lds + rr * LD + 4 * kq) = v[q];
+        const int kr = idx / (ROWS / 4), rc = (idx % (ROWS / 4)) * 4;
+        *reinterpret_cast<float4*>(lds + kr * LDR + rc) = v[q];
       }
     }
   }
+  // MFMA operand values of the TPW 16-row tiles a wave owns (rows rowbase ..
+  // rowbase + 16*TPW) for k = ks + 4g + e, e = 0..3: out[t][e].  KC: tile t,
+  // lane lq is row rowbase + 16t + lq (one 128-bit read per tile).  Otherwise
+  // tile t, lane lq is row rowbase + TPW*lq + t (one TPW-wide read per e): the
+  // row permutation the epilogue undoes.
+  template <int TPW>
+  __device__ __forceinline__ static void fetch(const float* lds, int rowbase, int ks, int lq, int g,
+                                               float (&out)[TPW][4]) {
+    if (KC) {
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const float4 x = *reinterpret_cast<const float4*>(&lds[(rowbase + 16 * t + lq) * LDK + ks + 4 * g]);
+        out[t][0] = x.x;
+        out[t][1] = x.y;
+        out[t][2] = x.z;
+        out[t][3] = x.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float* src = &lds[(ks + 4 * g + e) * LDR + rowbase + TPW * lq];
+        if (TPW == 4) {
+          const float4 x = *reinterpret_cast<const float4*>(src);
+          out[0][e] = x.x;
+          out[1 % TPW][e] = x.y;
+          out[2 % TPW][e] = x.z;
+          out[3 % TPW][e] = x.w;
+        } else {
+#pragma unroll
+          for (int t = 0; t < TPW; ++t) out[t][e] = src[t];
+        }
+      }
+    }
+  }
+  // Row (within the wave's rows) of tile t, MFMA row/column index j.
+  __device__ __forceinline__ static int row_of(int t, int j, int tpw) { return KC ? 16 * t + j : tpw * j + t; }
 };
 
 // BM x 128 output tile per 256-thread block, 2 x 2 waves of (BM/2) x 64,
 // KT-deep k stages.  MFMA rows are output columns n, MFMA columns output rows m.
 template <int BM, int KT, bool A_KC, bool B_KC, bool PARTIAL>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
-  constexpr int LD = KT + 4;
+  using SA = GemmStage<BM, KT, A_KC>;
+  using SB = GemmStage<kGBN, KT, B_KC>;
   constexpr int MT = BM / 32;  // 16-row m tiles per wave
-  __shared__ __align__(16) float As[BM * LD];
-  __shared__ __align__(16) float Bs[kGBN * LD];
+  __shared__ __align__(16) float As[SA::ELEMS];
+  __shared__ __align__(16) float Bs[SB::ELEMS];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int lq = lane & 15, gq = lane >> 4;
@@ -136,8 +177,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < MT; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  GemmStage<BM, KT, A_KC> sa;
-  GemmStage<kGBN, KT, B_KC> sb;
+  SA sa;
+  SB sb;
   if (k_begin < k_end) {
     sa.load(A, g.a_sm, g.a_sk, m0, g.M, k_begin, k_end, tid);
     sb.load(Bm, g.b_sn, g.b_sk, n0, g.N, k_begin, k_end, tid);
@@ -153,46 +194,42 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     }
 #pragma unroll
     for (int ks = 0; ks < KT; ks += 16) {
-      float4 bv[4], av[MT];
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        bv[t] = *reinterpret_cast<const float4*>(&Bs[(64 * wn + 16 * t + lq) * LD + ks + 4 * gq]);
-#pragma unroll
-      for (int t = 0; t < MT; ++t)
-        av[t] = *reinterpret_cast<const float4*>(&As[((BM / 2) * wm + 16 * t + lq) * LD + ks + 4 * gq]);
+      float bvals[4][4], avals[MT][4];
+      SB::template fetch<4>(Bs, 64 * wn, ks, lq, gq, bvals);
+      SA::template fetch<MT>(As, (BM / 2) * wm, ks, lq, gq, avals);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
-          const float bvals[4] = {bv[nt].x, bv[nt].y, bv[nt].z, bv[nt].w};
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const float avals[4] = {av[mt].x, av[mt].y, av[mt].z, av[mt].w};
-            acc[nt][mt] = mfma4(bvals[e], avals[e], acc[nt][mt]);
-          }
+          for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = mfma4(bvals[nt][e], avals[mt][e], acc[nt][mt]);
         }
       }
     }
   }
 
-  // acc[nt][mt][i] = C[m = m0+(BM/2)wm+16mt+lq][n = n0+64wn+16nt+4gq+i]
+  // acc[nt][mt][i] = C[m][n] with m = m0 + (BM/2)wm + SA::row_of(mt, lq) and
+  // n = n0 + 64wn + SB::row_of(nt, 4gq + i): four consecutive n over i (B_KC)
+  // or over nt (otherwise) go out as one 128-bit store.
+  const bool vec = PARTIAL ? (g.N % 4 == 0) : g.c_vec;
+  const float* bias = (!PARTIAL && g.bias != nullptr) ? g.bias + bt * g.bias_sb : nullptr;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const int m = m0 + (BM / 2) * wm + 16 * mt + lq;
+    const int m = m0 + (BM / 2) * wm + SA::row_of(mt, lq, MT);
     if (m >= g.M) continue;
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const int n = n0 + 64 * wn + 16 * nt + 4 * gq;
+    for (int u = 0; u < 4; ++u) {
+      // B_KC: u = nt, the vector runs over i; otherwise u = i, the vector runs over nt
+      const int n = B_KC ? n0 + 64 * wn + 16 * u + 4 * gq : n0 + 64 * wn + 4 * (4 * gq + u);
       if (n >= g.N) continue;
-      float4 r = make_float4(acc[nt][mt][0], acc[nt][mt][1], acc[nt][mt][2], acc[nt][mt][3]);
+      float4 r = B_KC ? make_float4(acc[u][mt][0], acc[u][mt][1], acc[u][mt][2], acc[u][mt][3])
+                      : make_float4(acc[0][mt][u], acc[1][mt][u], acc[2][mt][u], acc[3][mt][u]);
       float* dst;
-      const bool vec = PARTIAL ? (g.N % 4 == 0) : g.c_vec;
       if (PARTIAL) {
         dst = g.c + ((int64_t)blockIdx.z * g.M + m) * g.N + n;
       } else {
         dst = g.c + bt * g.c_sb + (int64_t)m * g.ldc + n;
-        if (g.bias != nullptr) {
-          const float* bias = g.bias + bt * g.bias_sb;
+        if (bias != nullptr) {
           r.x = (n + 0 < g.N ? bias[n + 0] : 0.f) + r.x;
           r.y = (n + 1 < g.N ? bias[n + 1] : 0.f) + r.y;
           r.z = (n + 2 < g.N ? bias[n + 2] : 0.f) + r.z;
