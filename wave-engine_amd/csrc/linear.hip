@@ -277,19 +277,55 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
   *dst = g.accumulate ? *dst + r : r;
 }
 
-// out[bt][n] = sum_m y[bt][m][n] (column sums, for the bias gradient): rows
-// split over blockIdx.y into fixed chunks whose partials are then added in
-// order; blockIdx.z = batch index (operand offset bt * y_sb).
+// out[bt][n] = sum_m y[bt][m][n] (column sums, for the bias gradient).  Block =
+// 64 columns x one chunk of rows: 16 lanes cover the 64 columns with 128-bit
+// loads (32-bit where the row is not 16-byte aligned), 16 row lanes stride
+// through the chunk, and the 16 row partials are added in a fixed order in
+// LDS; blockIdx.z = batch index (operand offset bt * y_sb).  The chunk partials
+// are then added in order by colsum_final_kernel.
 __global__ __launch_bounds__(256) void colsum_partial_kernel(const float* __restrict__ y, int64_t ldy,
                                                              int64_t y_sb, int M, int N, int rows_per,
                                                              float* __restrict__ part) {
-  const int n = blockIdx.x * 256 + threadIdx.x;
-  if (n >= N) return;
+  __shared__ float4 red[16][16];
+  const int cq = threadIdx.x & 15, rl = threadIdx.x >> 4;
+  const int n = blockIdx.x * 64 + 4 * cq;
   const float* yb = y + (int64_t)blockIdx.z * y_sb;
   const int r0 = blockIdx.y * rows_per, r1 = min(M, r0 + rows_per);
-  float s = 0.f;
-  for (int m = r0; m < r1; ++m) s += yb[(int64_t)m * ldy + n];
-  part[((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * N + n] = s;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (n < N) {
+    const bool vec = n + 3 < N && ((((uintptr_t)(yb + n)) | ((uintptr_t)ldy * 4)) & 15) == 0;
+    for (int m = r0 + rl; m < r1; m += 16) {
+      const float* src = yb + (int64_t)m * ldy + n;
+      if (vec) {
+        const float4 v = *reinterpret_cast<const float4*>(src);
+        s.x += v.x;
+        s.y += v.y;
+        s.z += v.z;
+        s.w += v.w;
+      } else {
+        s.x += src[0];
+        if (n + 1 < N) s.y += src[1];
+        if (n + 2 < N) s.z += src[2];
+        if (n + 3 < N) s.w += src[3];
+      }
+    }
+  }
+  red[rl][cq] = s;
+  __syncthreads();
+  if (rl == 0 && n < N) {
+    float4 t = red[0][cq];
+    for (int j = 1; j < 16; ++j) {
+      t.x += red[j][cq].x;
+      t.y += red[j][cq].y;
+      t.z += red[j][cq].z;
+      t.w += red[j][cq].w;
+    }
+    float* dst = part + ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * N + n;
+    dst[0] = t.x;
+    if (n + 1 < N) dst[1] = t.y;
+    if (n + 2 < N) dst[2] = t.z;
+    if (n + 3 < N) dst[3] = t.w;
+  }
 }
 
 __global__ __launch_bounds__(256) void colsum_final_kernel(const float* __restrict__ part, int chunks, int N,
@@ -320,7 +356,7 @@ int gemm_splits(int M, int N, int K, int batch, int min_k = 256) {
   return splits;
 }
 
-int colsum_chunks(int M) { return M >= 4096 ? 64 : (M >= 256 ? 16 : 1); }
+int colsum_chunks(int M) { return M >= 4096 ? 16 : (M >= 256 ? 4 : 1); }
 
 template <int BM, int KT, bool A_KC, bool B_KC>
 hipError_t gemm_launch(GemmArgs g, float* ws, int splits, const char* name, hipStream_t stream) {
@@ -422,7 +458,7 @@ hipError_t launch_linear_bwd_dw_batched(const float* dy, int64_t lddy, int64_t d
   const int chunks = colsum_chunks(M);
   const int rows_per = (M + chunks - 1) / chunks;
   TimingScope ts("linear_bwd_db", stream);
-  hipLaunchKernelGGL(colsum_partial_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)chunks, (unsigned)batch),
+  hipLaunchKernelGGL(colsum_partial_kernel, dim3((unsigned)((N + 63) / 64), (unsigned)chunks, (unsigned)batch),
                      dim3(256), 0, stream, dy, lddy, dy_sb, M, N, rows_per, cs);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
