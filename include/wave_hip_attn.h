@@ -273,6 +273,23 @@ int wha_wave_bwd(const float* x, const float* d_out, const wha_wave_weights* w, 
 int wha_wave_probs_rows(const wha_wave_cache* cache, const wha_wave_shape* shape, const int32_t* rows,
                         int32_t n_rows, float* out, void* stream);
 
+/* Host forms (one sequence, host arrays, synchronous), for callers that keep
+ * activations on the host as the reference does.  `w` holds HOST pointers in
+ * the wha_wave_weights layout; x, out, d_attn_out, d_x are [T][n_embd].
+ *
+ * wave_attention_forward (attn.rs:90-305): out, and optionally the per-head
+ * phases phase_out [n_head][T] (WaveAttnCache.phases). */
+int wha_host_wave_attention_forward(const float* x, const wha_wave_weights* w, int32_t T, int32_t n_embd,
+                                    int32_t n_head, int32_t content_dim, float* out, float* phase_out);
+
+/* wave_attention_backward_full (attn.rs:346-430), or _pathway (:432-511) when
+ * every weight-gradient pointer of `g` is NULL.  The forward intermediates are
+ * recomputed on the device from x and w (the reference passes its cache).
+ * `g` holds HOST pointers in the wha_wave_grads layout. */
+int wha_host_wave_attention_backward(const float* x, const float* d_attn_out, const wha_wave_weights* w,
+                                     int32_t T, int32_t n_embd, int32_t n_head, int32_t content_dim,
+                                     const wha_wave_grads* g);
+
 /* ---------------------------------------------------------------- wave KV cache
  * Serving (src/common/kv_cache.rs:93-356, driven by
  * src/serve_tier/inference.rs:29-106): the attention half of prefill and

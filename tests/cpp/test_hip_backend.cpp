@@ -22,6 +22,14 @@ void wao_attention_full_f32(const float* x, const float* wa, const float* ba, co
                             int T, int E, int H, float* out);
 void wao_attention_backward_f32(const float* d_pre_proj, const float* q, const float* k, const float* v,
                                 const float* att, int T, int E, int H, float* dq, float* dk, float* dv);
+void wao_wave_fwd_f32(const float* x, int T, int E, int H, int C, const float* hraw, const float* proj_w,
+                      const float* proj_b, const float* v_w, const float* v_b, const float* out_w, const float* out_b,
+                      const float* phase_in, float* out, float* merged_out, float* att_out, float* phase_out,
+                      float* rs_out, float* content_out, float* values_out, float* lse_out);
+void wao_wave_bwd_f32(const float* x, int T, int E, int H, int C, const float* hraw, const float* proj_w,
+                      const float* proj_b, const float* v_w, const float* v_b, const float* out_w, const float* out_b,
+                      const float* phase_in, const float* d_attn_out, float* d_x, float* d_hraw, float* d_proj_w,
+                      float* d_proj_b, float* d_v_w, float* d_v_b, float* d_out_w, float* d_out_b);
 }
 
 using wave_hip::Rows;
@@ -227,6 +235,72 @@ void test_concurrent_callers() {
     if (solo[i] != conc[i]) throw std::runtime_error("concurrent result differs for sequence " + std::to_string(i));
 }
 
+// Wave attention through the C++ mirror (attn.rs:90-511) against the oracle,
+// which replays the mirror's phases so both form the same bucket mask.
+void wave_vs_cpu(size_t T, size_t E, size_t H, size_t C, uint64_t seed) {
+  const size_t hd = E / H;
+  uint64_t st = seed;
+  auto normal = [&](size_t n, double sd) {
+    std::vector<float> v(n);
+    wao_fill_normal(&st, v.data(), n, sd);
+    return v;
+  };
+  wave_hip::WaveAttnWeights w;
+  for (size_t h = 0; h < H; ++h) {
+    wave_hip::WaveAttnHeadWeights hw;
+    hw.harmonic_raw = normal(1, 1.0)[0] + 0.5f;
+    hw.phase_proj_w = rows_of(normal(2 * E, 1.0 / std::sqrt((double)E)), 2, E);
+    hw.phase_proj_b = normal(2, 0.1);
+    hw.v_proj_w = rows_of(normal(hd * hd, 1.0 / std::sqrt((double)hd)), hd, hd);
+    hw.v_proj_b = normal(hd, 0.1);
+    if (C) {
+      hw.content_proj_w = rows_of(normal(C * E, 1.0 / std::sqrt((double)E)), C, E);
+      hw.content_proj_b = normal(C, 0.1);
+    }
+    w.heads.push_back(hw);
+  }
+  w.out_proj_w = rows_of(normal(E * E, 1.0 / std::sqrt((double)E)), E, E);
+  w.out_proj_b = normal(E, 0.1);
+  const auto x = normal(T * E, 1.0);
+  const auto dy = normal(T * E, 1.0 / std::sqrt((double)T));
+  wave_hip::HipBackend be;
+  Rows phases;
+  const Rows out = be.wave_attention_forward(w, rows_of(x, T, E), E / 2, &phases);
+  const auto ph = flat_of(phases);
+  // oracle inputs in the packed layout
+  const auto p = wave_hip::detail::pack_wave(w, E);
+  std::vector<float> ref(T * E);
+  wao_wave_fwd_f32(x.data(), (int)T, (int)E, (int)H, (int)C, p.hraw.data(), p.proj_w.data(), p.proj_b.data(),
+                   p.v_w.data(), p.v_b.data(), p.out_w.data(), p.out_b.data(), ph.data(), ref.data(), nullptr,
+                   nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
+  assert_parity(flat_of(out), ref, "wave out");
+  const auto g = be.wave_attention_backward_full(w, rows_of(x, T, E), rows_of(dy, T, E));
+  const size_t P = 2 + C;
+  std::vector<float> d_x(T * E), d_hraw(H), d_pw(H * P * E), d_pb(H * P), d_vw(H * hd * hd), d_vb(H * hd),
+      d_ow(E * E), d_ob(E);
+  wao_wave_bwd_f32(x.data(), (int)T, (int)E, (int)H, (int)C, p.hraw.data(), p.proj_w.data(), p.proj_b.data(),
+                   p.v_w.data(), p.v_b.data(), p.out_w.data(), p.out_b.data(), ph.data(), dy.data(), d_x.data(),
+                   d_hraw.data(), d_pw.data(), d_pb.data(), d_vw.data(), d_vb.data(), d_ow.data(), d_ob.data());
+  assert_parity(flat_of(g.d_normed), d_x, "wave d_normed");
+  assert_parity(flat_of(g.out_proj_w), d_ow, "wave d_out_proj_w");
+  for (size_t h = 0; h < H; ++h) {
+    assert_close(g.heads[h].d_harmonic_raw, d_hraw[h], 1e-4f, "d_harmonic_raw");
+    std::vector<float> want_ph(d_pw.begin() + h * P * E, d_pw.begin() + h * P * E + 2 * E);
+    assert_parity(flat_of(g.heads[h].phase_proj_w), want_ph, "d_phase_proj_w");
+    std::vector<float> want_v(d_vw.begin() + h * hd * hd, d_vw.begin() + (h + 1) * hd * hd);
+    assert_parity(flat_of(g.heads[h].v_proj_w), want_v, "d_v_proj_w");
+    if (C) {
+      std::vector<float> want_c(d_pw.begin() + h * P * E + 2 * E, d_pw.begin() + (h + 1) * P * E);
+      assert_parity(flat_of(g.heads[h].content_proj_w), want_c, "d_content_proj_w");
+    }
+  }
+  const Rows path = be.wave_attention_backward_pathway(w, rows_of(x, T, E), rows_of(dy, T, E));
+  if (flat_of(path) != flat_of(g.d_normed)) throw std::runtime_error("pathway d_normed differs from the full backward");
+}
+
+void test_wave_attention_content() { wave_vs_cpu(130, 96, 4, 16, 77); }
+void test_wave_attention_no_content() { wave_vs_cpu(65, 168, 4, 0, 78); }   // head_dim 42
+
 }  // namespace
 
 int main() {
@@ -240,6 +314,8 @@ int main() {
   run("attention_with_projections", test_attention_with_projections);
   run("bad_head_count_panics", test_bad_head_count_panics);
   run("concurrent_callers", test_concurrent_callers);
+  run("wave_attention_content", test_wave_attention_content);
+  run("wave_attention_no_content", test_wave_attention_no_content);
   std::printf("test result: %s. %d failed\n", g_failures ? "FAILED" : "ok", g_failures);
   return g_failures ? 1 : 0;
 }

@@ -39,3 +39,23 @@ def test_python_host_mirror(pkg, T, E, H):
     assert_parity("d_q", dq, rq)
     assert_parity("d_k", dk, rk)
     assert_parity("d_v", dv, rv)
+
+
+@pytest.mark.parametrize("T,E,H,C", [(90, 64, 4, 16), (33, 168, 4, 0)])
+def test_python_host_wave_mirror(pkg, T, E, H, C):
+    """HipBackend's host-array wave attention (attn.rs:90-511) against the oracle
+    replaying the device phases."""
+    from conftest import make_wave_weights
+    w = make_wave_weights(H, C, E, seed=T)
+    rng = np.random.default_rng(T + 1)
+    x = rng.normal(size=(T, E)).astype(np.float32)
+    dy = (rng.normal(size=(T, E)) / np.sqrt(T)).astype(np.float32)
+    be = pkg.HipBackend()
+    out, ph = be.wave_attention_forward(w, x, n_bands=E // 2, want_phases=True)
+    ref = oracle.wave_fwd(x, w, "f32", phase_in=ph)
+    assert_parity("wave out", out, ref["out"])
+    g = be.wave_attention_backward(w, x, dy)
+    rg = oracle.wave_bwd(x, w, dy, "f32", phase_in=ph)
+    for k in ("d_x", "d_hraw", "d_proj_w", "d_proj_b", "d_v_w", "d_v_b", "d_out_w", "d_out_b"):
+        assert_parity(k, g[k], rg[k])
+    np.testing.assert_array_equal(be.wave_attention_backward(w, x, dy, full=False), g["d_x"])

@@ -42,7 +42,7 @@ EXPORTED_SYMBOLS = (
     "wha_decode_workspace_size", "wha_decode_fwd", "wha_attn_probs_rows",
     "wha_wave_fwd", "wha_wave_bwd_workspace_size", "wha_wave_bwd", "wha_wave_probs_rows",
     "wha_wave_kv_prefill_workspace_size", "wha_wave_kv_prefill", "wha_wave_kv_decode_workspace_size",
-    "wha_wave_kv_decode",
+    "wha_wave_kv_decode", "wha_host_wave_attention_forward", "wha_host_wave_attention_backward",
     "wha_linear_fwd", "wha_linear_bwd_dx", "wha_linear_bwd_dw_workspace_size", "wha_linear_bwd_dw",
     "wha_host_attention_core_fwd", "wha_host_attention_backward", "wha_host_attention",
     "wha_synth_normal",
@@ -153,6 +153,8 @@ def lib():
         L.wha_wave_bwd_workspace_size.restype = sz
         L.wha_wave_bwd.argtypes = [vp, vp, wwp, wsp, wcp, wgp, vp, sz, vp]
         L.wha_wave_probs_rows.argtypes = [wcp, wsp, ctypes.POINTER(ctypes.c_int32), i32, vp, vp]
+        L.wha_host_wave_attention_forward.argtypes = [f32p, wwp, i32, i32, i32, i32, f32p, vp]
+        L.wha_host_wave_attention_backward.argtypes = [f32p, f32p, wwp, i32, i32, i32, i32, wgp]
         kvp = ctypes.POINTER(_WaveKvC)
         L.wha_wave_kv_prefill_workspace_size.argtypes = [wsp]
         L.wha_wave_kv_prefill_workspace_size.restype = sz
@@ -519,6 +521,50 @@ class HipBackend:
                lib().wha_host_attention_backward(_fp(d), _fp(q), _fp(k), _fp(v), _fp(att), T, E,
                                                  int(n_head), _fp(dq), _fp(dk), _fp(dv)))
         return dq, dk, dv
+
+    # ---- wave attention on host arrays (src/common/attn.rs:90-511)
+
+    @staticmethod
+    def _wave_host_weights(w):
+        arrs = {k: np.ascontiguousarray(np.asarray(w[k], dtype=np.float32))
+                for k in ("hraw", "proj_w", "proj_b", "v_w", "v_b", "out_w", "out_b")}
+        H, P, E = arrs["proj_w"].shape
+        c = _WaveWeightsC(*(a.ctypes.data for a in arrs.values()))
+        return arrs, c, H, P - 2, E
+
+    def wave_attention_forward(self, weights, x, n_bands=None, want_phases=False):
+        """wave_attention_forward (attn.rs:90-305) on one sequence x [T][n_embd];
+        weights: mapping of packed host arrays (hraw, proj_w [H][2+C][E], proj_b,
+        v_w, v_b, out_w, out_b).  Returns out (and phases [H][T])."""
+        arrs, c, H, C, E = self._wave_host_weights(weights)
+        xs = _as_2d_f32(x, "x")
+        T = xs.shape[0]
+        if xs.shape[1] != E or (n_bands is not None and 2 * n_bands != E):
+            raise ValueError("x must be [T][n_embd] with n_embd = 2 * n_bands")
+        out = np.empty((T, E), dtype=np.float32)
+        ph = np.empty((H, T), dtype=np.float32)
+        _check("wha_host_wave_attention_forward", lib().wha_host_wave_attention_forward(
+            _fp(xs), ctypes.byref(c), T, E, H, C, _fp(out), ctypes.c_void_p(ph.ctypes.data)))
+        return (out, ph) if want_phases else out
+
+    def wave_attention_backward(self, weights, x, d_attn_out, full=True):
+        """wave_attention_backward_full (attn.rs:346-430), or _pathway (:432-511)
+        when full is False (d_normed only).  The forward is recomputed from x."""
+        arrs, c, H, C, E = self._wave_host_weights(weights)
+        xs, d = _as_2d_f32(x, "x"), _as_2d_f32(d_attn_out, "d_attn_out")
+        T = xs.shape[0]
+        hd = E // H
+        g = dict(d_x=np.empty((T, E), np.float32))
+        if full:
+            g.update(d_hraw=np.empty(H, np.float32), d_proj_w=np.empty((H, 2 + C, E), np.float32),
+                     d_proj_b=np.empty((H, 2 + C), np.float32), d_v_w=np.empty((H, hd, hd), np.float32),
+                     d_v_b=np.empty((H, hd), np.float32), d_out_w=np.empty((E, E), np.float32),
+                     d_out_b=np.empty(E, np.float32))
+        keys = ("d_x", "d_hraw", "d_proj_w", "d_proj_b", "d_v_w", "d_v_b", "d_out_w", "d_out_b")
+        gc = _WaveGradsC(*((g[k].ctypes.data if k in g else None) for k in keys))
+        _check("wha_host_wave_attention_backward", lib().wha_host_wave_attention_backward(
+            _fp(xs), _fp(d), ctypes.byref(c), T, E, H, C, ctypes.byref(gc)))
+        return g if full else g["d_x"]
 
 
 # ------------------------------------------------------------------ synthetic inputs

@@ -597,6 +597,152 @@ int wha_wave_probs_rows(const wha_wave_cache* cache, const wha_wave_shape* shape
   return WHA_OK;
 }
 
+// ---------------------------------------------------------------- wave attention, host forms
+
+namespace {
+
+// Carves 256-byte aligned float segments out of one staging buffer.
+struct Carve {
+  float* base;
+  size_t used;
+  float* take(size_t n) {
+    float* p = base + used;
+    used += round256(n * sizeof(float)) / sizeof(float);
+    return p;
+  }
+};
+
+size_t seg(size_t n) { return round256(n * sizeof(float)); }
+
+struct WaveHostSizes {
+  size_t hraw, pw, pb, vw, vb, ow, ob, te, proj, feat, ht;
+};
+
+WaveHostSizes wave_host_sizes(int T, int E, int H, int C) {
+  const size_t P = 2 + (size_t)C, hd = (size_t)E / H;
+  return WaveHostSizes{(size_t)H, (size_t)H * P * E, (size_t)H * P, (size_t)H * hd * hd, (size_t)H * hd,
+                       (size_t)E * E, (size_t)E, (size_t)T * E, (size_t)T * H * P,
+                       (size_t)H * T * wha::kWaveFeatures, (size_t)H * T};
+}
+
+size_t wave_host_weight_bytes(const WaveHostSizes& z) {
+  return seg(z.hraw) + seg(z.pw) + seg(z.pb) + seg(z.vw) + seg(z.vb) + seg(z.ow) + seg(z.ob);
+}
+
+size_t wave_host_cache_bytes(const WaveHostSizes& z) {
+  // proj, values, feat, phase, bucket, merged, lse
+  return seg(z.proj) + seg(z.te) + seg(z.feat) + 3 * seg(z.ht) + seg(z.te);
+}
+
+// Device copies of the host weights (same layout), enqueued on s.
+hipError_t stage_wave_weights(Carve& cv, const wha_wave_weights* w, const WaveHostSizes& z, hipStream_t s,
+                              wha_wave_weights* dw) {
+  float* d[7] = {cv.take(z.hraw), cv.take(z.pw), cv.take(z.pb), cv.take(z.vw),
+                 cv.take(z.vb),   cv.take(z.ow), cv.take(z.ob)};
+  const float* h[7] = {w->harmonic_raw, w->proj_w, w->proj_b, w->v_w, w->v_b, w->out_w, w->out_b};
+  const size_t n[7] = {z.hraw, z.pw, z.pb, z.vw, z.vb, z.ow, z.ob};
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < 7 && e == hipSuccess; ++i)
+    e = hipMemcpyAsync(d[i], h[i], n[i] * sizeof(float), hipMemcpyHostToDevice, s);
+  *dw = wha_wave_weights{d[0], d[1], d[2], d[3], d[4], d[5], d[6]};
+  return e;
+}
+
+wha_wave_cache carve_wave_cache(Carve& cv, const WaveHostSizes& z) {
+  wha_wave_cache c;
+  c.proj = cv.take(z.proj);
+  c.values = cv.take(z.te);
+  c.feat = cv.take(z.feat);
+  c.phase = cv.take(z.ht);
+  c.bucket = reinterpret_cast<int32_t*>(cv.take(z.ht));
+  c.merged = cv.take(z.te);
+  c.lse = cv.take(z.ht);
+  return c;
+}
+
+}  // namespace
+
+int wha_host_wave_attention_forward(const float* x, const wha_wave_weights* w, int32_t T, int32_t E, int32_t H,
+                                    int32_t C, float* out, float* phase_out) {
+  static const char* fn = "wha_host_wave_attention_forward";
+  const wha_wave_shape sh{1, T, E, H, C};
+  int rc;
+  if ((rc = check_wave_shape(&sh, fn)) || (rc = check_wave_weights(w, fn))) return rc;
+  if (!x || !out) return fail(WHA_ERR_INVALID, "%s: x and out must be non-NULL", fn);
+  const WaveHostSizes z = wave_host_sizes(T, E, H, C);
+  float* base = nullptr;
+  hipStream_t s = nullptr;
+  if ((rc = host_stage(wave_host_weight_bytes(z) + wave_host_cache_bytes(z) + 2 * seg(z.te), &base, &s)))
+    return rc;
+  Carve cv{base, 0};
+  wha_wave_weights dw;
+  hipError_t e = stage_wave_weights(cv, w, z, s, &dw);
+  float* dx = cv.take(z.te);
+  float* dout = cv.take(z.te);
+  const wha_wave_cache dc = carve_wave_cache(cv, z);
+  if (e == hipSuccess) e = hipMemcpyAsync(dx, x, z.te * sizeof(float), hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync H2D");
+  if ((rc = wha_wave_fwd(dx, &dw, &sh, dout, &dc, s))) return rc;
+  e = hipMemcpyAsync(out, dout, z.te * sizeof(float), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess && phase_out)
+    e = hipMemcpyAsync(phase_out, dc.phase, z.ht * sizeof(float), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync D2H");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+int wha_host_wave_attention_backward(const float* x, const float* d_attn_out, const wha_wave_weights* w,
+                                     int32_t T, int32_t E, int32_t H, int32_t C, const wha_wave_grads* g) {
+  static const char* fn = "wha_host_wave_attention_backward";
+  const wha_wave_shape sh{1, T, E, H, C};
+  int rc;
+  if ((rc = check_wave_shape(&sh, fn)) || (rc = check_wave_weights(w, fn))) return rc;
+  if (!x || !d_attn_out || !g || !g->d_x)
+    return fail(WHA_ERR_INVALID, "%s: x, d_attn_out, g and g->d_x must be non-NULL", fn);
+  float* const hg[7] = {g->d_harmonic_raw, g->d_proj_w, g->d_proj_b, g->d_v_w, g->d_v_b, g->d_out_w, g->d_out_b};
+  int n_set = 0;
+  for (float* p : hg) n_set += p != nullptr;
+  if (n_set != 0 && n_set != 7)
+    return fail(WHA_ERR_INVALID, "%s: the weight gradients must be all non-NULL or all NULL", fn);
+  const bool full = n_set == 7;
+  const WaveHostSizes z = wave_host_sizes(T, E, H, C);
+  const size_t ws_bytes = wha_wave_bwd_workspace_size(&sh);
+  const size_t grad_bytes = full ? wave_host_weight_bytes(z) : 0;
+  float* base = nullptr;
+  hipStream_t s = nullptr;
+  if ((rc = host_stage(wave_host_weight_bytes(z) + wave_host_cache_bytes(z) + 4 * seg(z.te) + grad_bytes + ws_bytes,
+                       &base, &s)))
+    return rc;
+  Carve cv{base, 0};
+  wha_wave_weights dw;
+  hipError_t e = stage_wave_weights(cv, w, z, s, &dw);
+  float* dx_in = cv.take(z.te);
+  float* dout_in = cv.take(z.te);
+  float* fwd_out = cv.take(z.te);
+  float* d_x = cv.take(z.te);
+  const wha_wave_cache dc = carve_wave_cache(cv, z);
+  const size_t n[7] = {z.hraw, z.pw, z.pb, z.vw, z.vb, z.ow, z.ob};
+  float* dg[7] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  if (full)
+    for (int i = 0; i < 7; ++i) dg[i] = cv.take(n[i]);
+  void* ws = cv.take(ws_bytes / sizeof(float));
+  if (e == hipSuccess) e = hipMemcpyAsync(dx_in, x, z.te * sizeof(float), hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(dout_in, d_attn_out, z.te * sizeof(float), hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync H2D");
+  if ((rc = wha_wave_fwd(dx_in, &dw, &sh, fwd_out, &dc, s))) return rc;
+  const wha_wave_grads dgr{d_x, dg[0], dg[1], dg[2], dg[3], dg[4], dg[5], dg[6]};
+  if ((rc = wha_wave_bwd(dx_in, dout_in, &dw, &sh, &dc, &dgr, ws, ws_bytes, s))) return rc;
+  e = hipMemcpyAsync(g->d_x, d_x, z.te * sizeof(float), hipMemcpyDeviceToHost, s);
+  if (full)
+    for (int i = 0; i < 7 && e == hipSuccess; ++i)
+      e = hipMemcpyAsync(hg[i], dg[i], n[i] * sizeof(float), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync D2H");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
 // ---------------------------------------------------------------- wave KV cache
 
 static int check_kv(const wha_wave_kv_cache* kv, const char* fn) {
