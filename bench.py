@@ -77,10 +77,15 @@ def cpu_baseline(cfg, seed=42, max_threads=None, min_seconds=10.0):
             break
     dt = (time.perf_counter() - t0) / reps
     flops = credited_flops(nseq, H, T, D)["total"]
+    # one sequence on one thread (attention_cpu itself is single-threaded)
+    t1 = time.perf_counter()
+    oracle.batch_fwd_bwd_f32_threaded(qs[:1], ks[:1], vs[:1], dos[:1], H, nthreads=1)
+    one = time.perf_counter() - t1
     return {"value": nseq * T / dt, "unit": "tokens/s", "cores": nthreads, "kind": "port",
             "sample": f"{nseq} of the {B} sequences ({nseq}x{T} tokens, {H} heads, D={D}), fwd+bwd, "
                       f"one thread per sequence, repeated {reps}x; host has {ncpu} cores",
-            "seconds_per_rep": dt, "tflops": flops / dt / 1e12}
+            "seconds_per_rep": dt, "tflops": flops / dt / 1e12, "nproc": ncpu,
+            "one_thread_seconds_per_sequence": one}
 
 
 def run_attention(args, cfg, pkg, torch):
@@ -129,6 +134,21 @@ def run_attention(args, cfg, pkg, torch):
     torch.cuda.synchronize()
     wall_plain = time.perf_counter() - t0
 
+    # fwd and bwd separately, per step (events on the launch stream), medians
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+            torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for e0, e1, e2 in evs:
+        e0.record(stream)
+        plan.fwd()
+        e1.record(stream)
+        plan.bwd()
+        e2.record(stream)
+    torch.cuda.synchronize()
+    fwd_each = sorted(e0.elapsed_time(e1) for e0, e1, _ in evs)
+    bwd_each = sorted(e1.elapsed_time(e2) for _, e1, e2 in evs)
+    median = lambda xs: xs[len(xs) // 2] if len(xs) % 2 else 0.5 * (xs[len(xs) // 2 - 1] + xs[len(xs) // 2])
+
     ms_per_step = wall_plain / args.steps * 1e3
     flops = credited_flops(B, H, T, D)
     tokens = B * T
@@ -151,6 +171,7 @@ def run_attention(args, cfg, pkg, torch):
         "pct_fp32_mfma_peak": 100.0 * flops["total"] / (ms_per_step * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
         "kernel_ms": {n: round(kern[n]["avg_ms"], 5) for n in kern},
         "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "ms_per_step_with_events": wall / args.steps * 1e3,
+        "fwd_ms_median": median(fwd_each), "bwd_ms_median": median(bwd_each),
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS, "traffic": traffic,
                      "algorithmic_flops_per_launch": flops[dom],

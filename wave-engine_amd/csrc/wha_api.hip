@@ -146,7 +146,18 @@ struct TimingState {
   bool on = false;
   std::vector<TimingRec> pending;
   std::map<std::string, std::pair<double, int64_t>> totals;
+  std::vector<hipEvent_t> free_events;  // reused, so a timed launch costs no event creation
 };
+
+// An event from the pool (device-scope: the timed kernels share the stream).
+hipError_t pooled_event(TimingState& st, hipEvent_t* ev) {
+  if (!st.free_events.empty()) {
+    *ev = st.free_events.back();
+    st.free_events.pop_back();
+    return hipSuccess;
+  }
+  return hipEventCreateWithFlags(ev, hipEventDisableSystemFence);
+}
 TimingState& timing() {
   static TimingState* s = new TimingState();  // never destroyed: usable during exit
   return *s;
@@ -165,8 +176,8 @@ int drain_timing_locked(TimingState& st) {
       t.first += ms;
       t.second += 1;
     }
-    (void)hipEventDestroy(r.start);
-    (void)hipEventDestroy(r.stop);
+    st.free_events.push_back(r.start);
+    st.free_events.push_back(r.stop);
   }
   st.pending.clear();
   return rc;
@@ -235,8 +246,18 @@ TimingScope::TimingScope(const char* name, hipStream_t s) : token(nullptr), stre
   if (!st.on) return;
   TimingRec* r = new TimingRec();
   r->name = name;
-  if (hipEventCreate(&r->start) != hipSuccess || hipEventCreate(&r->stop) != hipSuccess ||
-      hipEventRecord(r->start, s) != hipSuccess) {
+  if (pooled_event(st, &r->start) != hipSuccess) {
+    delete r;
+    return;
+  }
+  if (pooled_event(st, &r->stop) != hipSuccess) {
+    st.free_events.push_back(r->start);
+    delete r;
+    return;
+  }
+  if (hipEventRecord(r->start, s) != hipSuccess) {
+    st.free_events.push_back(r->start);
+    st.free_events.push_back(r->stop);
     delete r;
     return;
   }
@@ -251,8 +272,8 @@ TimingScope::~TimingScope() {
   if (hipEventRecord(r->stop, stream) == hipSuccess) {
     st.pending.push_back(*r);
   } else {
-    (void)hipEventDestroy(r->start);
-    (void)hipEventDestroy(r->stop);
+    st.free_events.push_back(r->start);
+    st.free_events.push_back(r->stop);
   }
   delete r;
 }
