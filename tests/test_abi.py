@@ -139,3 +139,56 @@ def test_head_stats_follow_the_monitor_definitions(pkg):
     np.testing.assert_array_equal(st["top_position"], [2, 3, 0])   # first maximum wins ties
     np.testing.assert_allclose(st["max_weight"], [0.5, 1.0, 0.4])
     np.testing.assert_allclose(st["self_attn_frac"], [0.0, 1.0, 0.0])
+
+
+def _wave_structs(pkg, B=1, T=8, E=64, H=2, C=16):
+    p = 1 << 20
+    w = pkg._WaveWeightsC(*([p] * 7))
+    cache = pkg._WaveCacheC(*([p] * 7))
+    return pkg.WaveShape(B, T, E, H, C), w, cache
+
+
+def test_wave_entry_points_validate_before_device_use(pkg):
+    L = pkg.lib()
+    p = ctypes.c_void_p(1 << 20)
+    sh, w, cache = _wave_structs(pkg)
+    for bad, msg in ((dict(E=63), b"divisible"), (dict(C=31), b"content_dim"), (dict(E=258, H=1), b"128"),
+                     (dict(T=0), b"positive")):
+        s2, _, _ = _wave_structs(pkg, **bad)
+        rc = L.wha_wave_fwd(p, ctypes.byref(w), ctypes.byref(s2), p, ctypes.byref(cache), None)
+        assert rc in (WHA_ERR_INVALID, WHA_ERR_UNSUPPORTED) and msg in L.wha_last_error(), L.wha_last_error()
+    nw = pkg._WaveWeightsC(*([1 << 20] * 6 + [None]))
+    assert L.wha_wave_fwd(p, ctypes.byref(nw), ctypes.byref(sh), p, ctypes.byref(cache), None) == WHA_ERR_INVALID
+    nc = pkg._WaveCacheC(*([1 << 20] * 6 + [None]))
+    assert L.wha_wave_fwd(p, ctypes.byref(w), ctypes.byref(sh), p, ctypes.byref(nc), None) == WHA_ERR_INVALID
+    some = pkg._WaveGradsC(1 << 20, 1 << 20, None, None, None, None, None, None)  # neither all nor none
+    rc = L.wha_wave_bwd(p, p, ctypes.byref(w), ctypes.byref(sh), ctypes.byref(cache), ctypes.byref(some), None, 0,
+                        None)
+    assert rc == WHA_ERR_INVALID and b"all non-NULL or all NULL" in L.wha_last_error()
+    rows = (ctypes.c_int32 * 1)(8)
+    assert L.wha_wave_probs_rows(ctypes.byref(cache), ctypes.byref(sh), rows, 1, p, None) == WHA_ERR_INVALID
+
+
+def test_wave_kv_entry_points_validate(pkg):
+    L = pkg.lib()
+    p = ctypes.c_void_p(1 << 20)
+    sh, w, _ = _wave_structs(pkg, B=2, T=1)
+    kv = pkg._WaveKvC(1 << 20, 1 << 20, 1 << 20, 1 << 20, 16)
+    lens = (ctypes.c_int32 * 2)(3, 16)  # 16 leaves no room to append
+    assert L.wha_wave_kv_decode(p, ctypes.byref(w), ctypes.byref(sh), ctypes.byref(kv), lens, p, None, 0,
+                                None) == WHA_ERR_INVALID
+    assert b"lengths[1]" in L.wha_last_error()
+    sh2, _, _ = _wave_structs(pkg, B=2, T=4)
+    lens = (ctypes.c_int32 * 2)(3, 4)
+    assert L.wha_wave_kv_decode(p, ctypes.byref(w), ctypes.byref(sh2), ctypes.byref(kv), lens, p, None, 0,
+                                None) == WHA_ERR_INVALID
+    assert b"T must be 1" in L.wha_last_error()
+    big, _, _ = _wave_structs(pkg, B=300, T=1)
+    lens = (ctypes.c_int32 * 300)()
+    assert L.wha_wave_kv_decode(p, ctypes.byref(w), ctypes.byref(big), ctypes.byref(kv), lens, p, None, 0,
+                                None) == WHA_ERR_UNSUPPORTED
+    long_prompt, _, _ = _wave_structs(pkg, B=1, T=17)
+    assert L.wha_wave_kv_prefill(p, ctypes.byref(w), ctypes.byref(long_prompt), ctypes.byref(kv), p, None, 0,
+                                 None) == WHA_ERR_INVALID
+    assert b"capacity" in L.wha_last_error()
+    assert L.wha_wave_kv_decode_workspace_size(ctypes.byref(sh), 0) == 0

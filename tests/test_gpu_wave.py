@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 # (B, T, n_embd, n_head, content_dim): head_dim 12 (padded 48), 42, 64, 128, and the
 # 768-dim model shape
 CONFIGS = [(2, 100, 48, 4, 16), (1, 77, 168, 4, 0), (2, 200, 128, 2, 16), (2, 130, 256, 2, 5),
-           (2, 1024, 768, 12, 16)]
+           (2, 1024, 768, 12, 16), (3, 1, 64, 2, 30), (1, 64, 64, 1, 3)]
 
 
 @pytest.fixture(scope="module")
@@ -64,7 +64,7 @@ def test_wave_forward_matches_oracle(pkg, torch_dev, B, T, E, H, C):
         assert_parity(f"lse b{b}", g["lse"][b], ref["lse"])
         assert_parity(f"out b{b}", out[b].cpu().numpy(), ref["out"])
         # rows of att_weights_all on demand
-        rows = sorted({0, 1, T // 2, T - 1})
+        rows = sorted({r for r in (0, 1, T // 2, T - 1) if r < T})
         got_rows = att_rows.rows(rows)[b].cpu().numpy()
         want_rows = ref["att"][:, rows, :]
         assert np.array_equal(np.isneginf(got_rows), np.isneginf(want_rows))
@@ -92,9 +92,14 @@ def test_wave_backward_matches_oracle(pkg, torch_dev, B, T, E, H, C):
         assert_parity(f"d_x b{b}", got_dx[b], refs[b]["d_x"])
     np.testing.assert_array_equal(d_path.cpu().numpy(), got_dx)  # pathway = full backward's d_normed
     s = lambda k: np.sum([r[k] for r in refs], axis=0, dtype=np.float64)
-    assert_parity("d_harmonic_raw", grads.d_harmonic_raw.cpu().numpy(), s("d_hraw"))
-    assert_parity("d_proj_w", grads.d_proj_w.cpu().numpy(), s("d_proj_w"))
-    assert_parity("d_proj_b", grads.d_proj_b.cpu().numpy(), s("d_proj_b"))
+    # with T = 1 every softmax row has one entry, so the score gradient is exactly
+    # zero in the reference (d_att - sum att*d_att = 0) and the phase/content
+    # gradients vanish; the device's dP - Delta carries rounding noise instead, so
+    # only the absolute bound applies (relative L2 is undefined for a zero reference)
+    score_kw = dict(rel_l2=np.inf) if T == 1 else {}
+    assert_parity("d_harmonic_raw", grads.d_harmonic_raw.cpu().numpy(), s("d_hraw"), **score_kw)
+    assert_parity("d_proj_w", grads.d_proj_w.cpu().numpy(), s("d_proj_w"), **score_kw)
+    assert_parity("d_proj_b", grads.d_proj_b.cpu().numpy(), s("d_proj_b"), **score_kw)
     assert_parity("d_v_w", grads.d_v_w.cpu().numpy(), s("d_v_w"))
     assert_parity("d_v_b", grads.d_v_b.cpu().numpy(), s("d_v_b"))
     assert_parity("d_out_w", grads.out_proj_w.cpu().numpy(), s("d_out_w"))
