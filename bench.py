@@ -11,10 +11,12 @@ credited FLOPs (12*B*H*D*P, P = T(T+1)/2), a roofline object for the dominant
 kernel (algorithmic FLOPs per launch / its average HIP-event duration), and the
 CPU baseline (the reference-order f32 oracle, one thread per sequence).
 
-    python bench.py [--steps K] [--warmup W] [--config 768|384|168|4096|decode|wave|wavedecode]
+    python bench.py [--steps K] [--warmup W] [--config 768|384|168|4096|decode|wave|wavedecode|layer]
 
 --config wave measures the wave (harmonic coherence) attention layer the
-reference trains with, forward and full backward with its projections.
+reference trains with, forward and full backward with its projections;
+--config layer the dot-product attention layer with its c_attn / c_proj
+projections (ComputeBackend::attention) forward and backward.
 """
 from __future__ import annotations
 
@@ -41,6 +43,8 @@ CONFIGS = {
                  T=1024, D=64, C=16),
     "wavedecode": dict(name="768-dim wave-attention KV-cache decode (serve tier), 64 sequences x 8192 cached",
                        B=64, H=12, T=8192, D=64, C=16),
+    "layer": dict(name="768-dim ComputeBackend::attention layer (c_attn, causal core, c_proj), fwd+bwd",
+                  B=8, H=12, T=1024, D=64),
 }
 
 METRIC = "causal attn fwd+bwd tokens/s & TFLOP/s (% fp32 MFMA peak), 768-dim seq1024"
@@ -369,6 +373,137 @@ def run_wave_decode(args, cfg, pkg, torch):
                          "avg_launch_ms": kern["wave_kv_split"]["avg_ms"]}}
 
 
+def layer_flops(B, H, T, D):
+    """ComputeBackend::attention forward + backward: c_attn [3E][E] and c_proj [E][E]
+    GEMMs over the B*T rows (forward, input gradient, weight gradient), plus the
+    core's credited 12*B*H*D*P."""
+    E, M = H * D, B * T
+    return {"linear_fwd": 2 * M * E * 4 * E, "linear_bwd_dx": 2 * M * E * 4 * E, "linear_bwd_dw": 2 * M * E * 4 * E,
+            "core": credited_flops(B, H, T, D)["total"],
+            "total": 3 * 2 * M * E * 4 * E + credited_flops(B, H, T, D)["total"]}
+
+
+def run_layer(args, cfg, pkg, torch):
+    """One step = attention_cpu's layer (compute.rs:357-414) forward and its backward
+    for the whole batch: qkv = c_attn(x), the fused core on strided views of qkv,
+    out = c_proj(o); then d_o = c_proj^T dy, dW/db of c_proj, the core backward into
+    a [B*T][3E] gradient, dx = c_attn^T d_qkv and dW/db of c_attn."""
+    import numpy as np
+    B, H, T, D = cfg["B"], cfg["H"], cfg["T"], cfg["D"]
+    E, M = H * D, B * T
+    dev = torch.device("cuda:0")
+    g = pkg.SynthStream(42)
+    t = lambda n, sd, *shape: torch.from_numpy(g.normal(n, sd).reshape(*shape)).to(dev)
+    x = t(M * E, 1.0, M, E)
+    wa, ba = t(3 * E * E, 1 / np.sqrt(E), 3 * E, E), t(3 * E, 0.1, 3 * E)
+    wp, bp = t(E * E, 1 / np.sqrt(E), E, E), t(E, 0.1, E)
+    dy = t(M * E, 1 / np.sqrt(M), M, E)
+    qkv = torch.empty(M, 3 * E, device=dev)
+    obuf = torch.empty(M, 3 * E, device=dev)   # o and d_o share q's [B][T][3E] strides
+    dobuf = torch.empty(M, 3 * E, device=dev)
+    d_qkv = torch.empty(M, 3 * E, device=dev)
+    out = torch.empty(M, E, device=dev)
+    dx = torch.empty(M, E, device=dev)
+    lse = torch.empty(B, H, T, device=dev)
+    heads = lambda buf, c: buf.view(B, T, 3 * E)[:, :, c * E:(c + 1) * E].view(B, T, H, D).permute(0, 2, 1, 3)
+    q, k, v = heads(qkv, 0), heads(qkv, 1), heads(qkv, 2)
+    o4, do4 = heads(obuf, 0), heads(dobuf, 0)
+    dq4, dk4, dv4 = heads(d_qkv, 0), heads(d_qkv, 1), heads(d_qkv, 2)
+    L = pkg.layout_of(q)
+    wsa = torch.empty(pkg.attn_bwd_workspace_bytes(L) // 4 + 64, device=dev)
+    wsl = torch.empty(max(int(pkg.lib().wha_linear_bwd_dw_workspace_size(M, n, E)) for n in (E, 3 * E)) // 4 + 64,
+                      device=dev)
+
+    def step():
+        pkg.linear_fwd(x, wa, ba, out=qkv)
+        pkg.attn_fwd(q, k, v, out=o4, lse=lse)
+        pkg.linear_fwd(obuf[:, :E], wp, bp, out=out)
+        pkg.linear_bwd_dx(dy, wp, out=dobuf[:, :E])
+        pkg.linear_bwd_dw(dy, obuf[:, :E], workspace=wsl)
+        pkg.attn_bwd(q, k, v, o4, do4, lse, workspace=wsa, dq=dq4, dk=dk4, dv=dv4)
+        pkg.linear_bwd_dx(d_qkv, wa, out=dx)
+        pkg.linear_bwd_dw(d_qkv, x, workspace=wsl)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    names = ("linear_fwd", "linear_bwd_dx", "linear_bwd_dw", "linear_bwd_db", "attn_fwd", "attn_bwd_delta",
+             "attn_bwd_dkv", "attn_bwd_dq")
+    pkg.timing_reset()
+    pkg.timing_enable(True)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    pkg.timing_enable(False)
+    kern = {}
+    for name in names:
+        ms, n = pkg.timing_read(name)
+        kern[name] = {"total_ms": ms / args.steps, "avg_ms": ms / max(n, 1), "launches": n}
+    pkg.timing_reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) / args.steps * 1e3
+    fl = layer_flops(B, H, T, D)
+    # dominant kernel family by time; its credited FLOPs per step over its time per step
+    dom = max(("linear_fwd", "linear_bwd_dx", "linear_bwd_dw"), key=lambda n: kern[n]["total_ms"])
+    achieved = fl[dom] / (kern[dom]["total_ms"] * 1e-3) / 1e12
+    return {
+        "metric": "attention layer (c_attn + causal core + c_proj) fwd+bwd tokens/s & TFLOP/s, 768-dim seq1024",
+        "value": M / (ms_per_step * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded xorshift64 + Box-Muller, seed 42)",
+        "config": {"workload": cfg["name"], "batch": B, "heads": H, "seq_len": T, "head_dim": D,
+                   "parallelism": "none (1 GPU)"},
+        "tflops": fl["total"] / (ms_per_step * 1e-3) / 1e12,
+        "pct_fp32_mfma_peak": 100.0 * fl["total"] / (ms_per_step * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
+        "kernel_ms_per_step": {n: round(kern[n]["total_ms"], 5) for n in names},
+        "roofline": {"kernel": dom, "bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS, "traffic": None,
+                     "algorithmic_flops_per_step": fl[dom], "ms_per_step": kern[dom]["total_ms"],
+                     "launches_per_step": kern[dom]["launches"] / args.steps},
+    }
+
+
+def layer_cpu_baseline(cfg, seed=42, max_threads=None):
+    """Reference-order f32 oracle of the same layer step, one thread per sequence
+    (the reference's B concurrent callers), on a bounded sample of sequences."""
+    import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
+    import oracle
+    B, H, T, D = cfg["B"], cfg["H"], cfg["T"], cfg["D"]
+    E = H * D
+    ncpu = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    nthreads = min(B, ncpu, max_threads or 16)
+    rng = oracle.Xorshift64(seed)
+    x = rng.normal(nthreads * T * E, 1.0).reshape(nthreads, T, E)
+    wa, ba = rng.normal(3 * E * E, 1 / np.sqrt(E)).reshape(3 * E, E), rng.normal(3 * E, 0.1)
+    wp, bp = rng.normal(E * E, 1 / np.sqrt(E)).reshape(E, E), rng.normal(E, 0.1)
+    dy = rng.normal(nthreads * T * E, 1 / np.sqrt(B * T)).reshape(nthreads, T, E)
+
+    def one(i):
+        qkv = oracle.linear(x[i], wa, ba)
+        q, k, v = qkv[:, :E], qkv[:, E:2 * E], qkv[:, 2 * E:]
+        o, att = oracle.core_fwd(q, k, v, H, "f32", want_att=True)
+        oracle.linear(o, wp, bp)
+        d_o = oracle.linear_backward_dx(dy[i], wp)
+        oracle.outer_product_accum(dy[i], o, True)
+        dq, dk, dv = oracle.attention_backward(d_o, q, k, v, att, H, "f32")
+        d_qkv = np.concatenate([dq, dk, dv], axis=1)
+        oracle.linear_backward_dx(d_qkv, wa)
+        oracle.outer_product_accum(d_qkv, x[i], True)
+
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(nthreads) as ex:
+        list(ex.map(one, range(nthreads)))
+    dt = time.perf_counter() - t0
+    return {"value": nthreads * T / dt, "unit": "tokens/s", "cores": nthreads, "kind": "port",
+            "sample": f"{nthreads} of the {B} sequences ({nthreads}x{T} tokens): c_attn, core, c_proj forward and "
+                      f"their backward, one thread per sequence, run once", "seconds": dt, "nproc": ncpu}
+
+
 def wave_cpu_baseline(cfg, seed=42, max_threads=None, min_seconds=10.0):
     """Reference-order f32 oracle of wave_attention_forward + backward_full, one
     thread per sequence on a bounded sample, repeated to at least min_seconds."""
@@ -456,12 +591,15 @@ def main():
         res = run_wave(args, cfg, pkg, torch)
     elif args.config == "wavedecode":
         res = run_wave_decode(args, cfg, pkg, torch)
+    elif args.config == "layer":
+        res = run_layer(args, cfg, pkg, torch)
     else:
         res = run_attention(args, cfg, pkg, torch)
     if args.config in ("decode", "wavedecode"):
         res["cpu_baseline"] = None
     elif not args.no_cpu_baseline:
-        res["cpu_baseline"] = wave_cpu_baseline(cfg) if args.config == "wave" else cpu_baseline(cfg)
+        res["cpu_baseline"] = (wave_cpu_baseline(cfg) if args.config == "wave" else
+                               layer_cpu_baseline(cfg) if args.config == "layer" else cpu_baseline(cfg))
     print(json.dumps(res), flush=True)
 
 
