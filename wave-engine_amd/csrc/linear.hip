@@ -45,6 +45,8 @@ struct GemmArgs {
   int batch = 1;       // independent GEMMs, operands offset by the strides below
   int splits = 1;      // blockIdx.z = batch index * splits + split index
   int64_t a_sb = 0, b_sb = 0, c_sb = 0, bias_sb = 0;
+  bool a_vec = false;  // A's base, batch stride and row stride along its contiguous
+  bool b_vec = false;  // direction are 16-byte multiples (set by gemm_t); same for B
 };
 
 // Staging of one ROWS x KT operand tile; element (r, k) of the source is
@@ -63,7 +65,22 @@ struct GemmStage {
   static_assert(NF4 % 256 == 0, "tile must split evenly over 256 threads");
   float4 v[PER];
   __device__ __forceinline__ void load(const float* __restrict__ p, int64_t s_r, int64_t s_k, int r0, int R,
-                                       int k0, int k_end, int tid) {
+                                       int k0, int k_end, int tid, bool full) {
+    if (full) {
+      // whole tile in bounds and 16-byte aligned (block-uniform): unpredicated 128-bit loads
+#pragma unroll
+      for (int q = 0; q < PER; ++q) {
+        const int idx = tid + 256 * q;
+        if (KC) {
+          const int rr = idx / (KT / 4), c = (idx % (KT / 4)) * 4;
+          v[q] = *reinterpret_cast<const float4*>(p + (int64_t)(r0 + rr) * s_r + (k0 + c));
+        } else {
+          const int kr = idx / (ROWS / 4), rc = (idx % (ROWS / 4)) * 4;
+          v[q] = *reinterpret_cast<const float4*>(p + (int64_t)(k0 + kr) * s_k + (r0 + rc));
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
       const int idx = tid + 256 * q;
@@ -164,7 +181,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   const int wave = tid >> 6, lane = tid & 63;
   const int lq = lane & 15, gq = lane >> 4;
   const int wn = wave & 1, wm = wave >> 1;
-  const int n0 = blockIdx.x * kGBN, m0 = blockIdx.y * BM;
+  // XCD-aware tile order: blocks are dealt round-robin to the 8 XCDs by linear
+  // id, so when a split's tile count is a multiple of 8, block j of XCD x takes
+  // tile x*(tiles/8) + j: each XCD then sweeps a contiguous band of m-tiles
+  // across all n-tiles and reuses the band's A rows from its own L2.
+  int tile = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+  const int tiles = (int)(gridDim.x * gridDim.y);
+  if (tiles % 8 == 0) tile = (tile % 8) * (tiles / 8) + tile / 8;
+  const int n0 = (tile % (int)gridDim.x) * kGBN, m0 = (tile / (int)gridDim.x) * BM;
   const int bt = (int)blockIdx.z / g.splits;
   const int k_begin = ((int)blockIdx.z % g.splits) * g.k_chunk;
   const float* __restrict__ A = g.a + bt * g.a_sb;
@@ -179,9 +203,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 
   SA sa;
   SB sb;
+  const bool rows_a = g.a_vec && m0 + BM <= g.M;
+  const bool rows_b = g.b_vec && n0 + kGBN <= g.N;
   if (k_begin < k_end) {
-    sa.load(A, g.a_sm, g.a_sk, m0, g.M, k_begin, k_end, tid);
-    sb.load(Bm, g.b_sn, g.b_sk, n0, g.N, k_begin, k_end, tid);
+    sa.load(A, g.a_sm, g.a_sk, m0, g.M, k_begin, k_end, tid, rows_a && k_begin + KT <= k_end);
+    sb.load(Bm, g.b_sn, g.b_sk, n0, g.N, k_begin, k_end, tid, rows_b && k_begin + KT <= k_end);
   }
   for (int kk = k_begin; kk < k_end; kk += KT) {
     __syncthreads();
@@ -189,8 +215,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     sb.store(Bs, tid);
     __syncthreads();
     if (kk + KT < k_end) {
-      sa.load(A, g.a_sm, g.a_sk, m0, g.M, kk + KT, k_end, tid);
-      sb.load(Bm, g.b_sn, g.b_sk, n0, g.N, kk + KT, k_end, tid);
+      const bool kin = kk + 2 * KT <= k_end;
+      sa.load(A, g.a_sm, g.a_sk, m0, g.M, kk + KT, k_end, tid, rows_a && kin);
+      sb.load(Bm, g.b_sn, g.b_sk, n0, g.N, kk + KT, k_end, tid, rows_b && kin);
     }
 #pragma unroll
     for (int ks = 0; ks < KT; ks += 16) {
@@ -382,14 +409,17 @@ hipError_t gemm_launch(GemmArgs g, float* ws, int splits, const char* name, hipS
   return hipGetLastError();
 }
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 template <bool A_KC, bool B_KC>
 hipError_t gemm_t(GemmArgs g, float* ws, const char* name, hipStream_t stream, int min_k = 256) {
   const int splits = ws ? gemm_splits(g.M, g.N, g.K, g.batch, min_k) : 1;
+  // 128-bit loads need every row start along the contiguous direction 16-byte aligned
+  g.a_vec = aligned16(g.a) && g.a_sb % 4 == 0 && (A_KC ? g.a_sm % 4 == 0 : g.a_sk % 4 == 0);
+  g.b_vec = aligned16(g.b) && g.b_sb % 4 == 0 && (B_KC ? g.b_sn % 4 == 0 : g.b_sk % 4 == 0);
   if (gemm_bm(g.M, g.N, g.batch) == 128) return gemm_launch<128, WHA_GEMM_KT, A_KC, B_KC>(g, ws, splits, name, stream);
   return gemm_launch<64, WHA_GEMM_KT, A_KC, B_KC>(g, ws, splits, name, stream);
 }
-
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
 
