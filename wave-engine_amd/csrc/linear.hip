@@ -64,10 +64,12 @@ struct GemmStage {
   static constexpr int PER = NF4 / 256;
   static_assert(NF4 % 256 == 0, "tile must split evenly over 256 threads");
   float4 v[PER];
-  __device__ __forceinline__ void load(const float* __restrict__ p, int64_t s_r, int64_t s_k, int r0, int R,
-                                       int k0, int k_end, int tid, bool full) {
-    if (full) {
-      // whole tile in bounds and 16-byte aligned (block-uniform): unpredicated 128-bit loads
+  // FULL: the whole ROWS x KT tile is in bounds and every piece 16-byte aligned
+  // (decided per block), so each piece is one unpredicated 128-bit load.
+  template <bool FULL>
+  __device__ __forceinline__ void load(const float* p, int64_t s_r, int64_t s_k, int r0, int R,
+                                       int k0, int k_end, int tid) {
+    if constexpr (FULL) {
 #pragma unroll
       for (int q = 0; q < PER; ++q) {
         const int idx = tid + 256 * q;
@@ -168,6 +170,78 @@ struct GemmStage {
   __device__ __forceinline__ static int row_of(int t, int j, int tpw) { return KC ? 16 * t + j : tpw * j + t; }
 };
 
+// MFMA work of one KT-deep stage held in LDS.
+template <int BM, int KT, bool A_KC, bool B_KC>
+__device__ __forceinline__ void gemm_stage_mfma(const float* As, const float* Bs, floatx4 (&acc)[4][BM / 32]) {
+  using SA = GemmStage<BM, KT, A_KC>;
+  using SB = GemmStage<kGBN, KT, B_KC>;
+  constexpr int MT = BM / 32;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int lq = lane & 15, gq = lane >> 4;
+  const int wn = wave & 1, wm = wave >> 1;
+#pragma unroll
+  for (int ks = 0; ks < KT; ks += 16) {
+    float bvals[4][4], avals[MT][4];
+    SB::template fetch<4>(Bs, 64 * wn, ks, lq, gq, bvals);
+    SA::template fetch<MT>(As, (BM / 2) * wm, ks, lq, gq, avals);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = mfma4(bvals[nt][e], avals[mt][e], acc[nt][mt]);
+      }
+    }
+  }
+}
+
+// k loop of one output tile.  The nfull k-full stages run with stage s+1
+// loaded into registers while stage s is multiplied out of LDS; the loop body
+// has no branch around its loads (the last iteration reloads the final stage),
+// so the loaded registers need no merge copies and the loads stay in flight
+// across the MFMA work.  A partial stage at the end of the k range follows on
+// its own.  FA / FB: the block's A / B rows are all in bounds and 16-byte
+// aligned, so their k-full stages load unpredicated.
+template <int BM, int KT, bool A_KC, bool B_KC, bool FA, bool FB>
+__device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* A,
+                                              const float* Bm, int m0, int n0, int k_begin,
+                                              int k_end, float* As, float* Bs, floatx4 (&acc)[4][BM / 32]) {
+  using SA = GemmStage<BM, KT, A_KC>;
+  using SB = GemmStage<kGBN, KT, B_KC>;
+  const int tid = threadIdx.x;
+  const int nfull = k_end > k_begin ? (k_end - k_begin) / KT : 0;
+  SA sa;
+  SB sb;
+  if (nfull > 0) {
+    sa.template load<FA>(A, g.a_sm, g.a_sk, m0, g.M, k_begin, k_end, tid);
+    sb.template load<FB>(Bm, g.b_sn, g.b_sk, n0, g.N, k_begin, k_end, tid);
+  }
+  for (int i = 0; i < nfull; ++i) {
+    __syncthreads();
+    sa.store(As, tid);
+    sb.store(Bs, tid);
+    __syncthreads();
+    const int kn = k_begin + min(i + 1, nfull - 1) * KT;
+    sa.template load<FA>(A, g.a_sm, g.a_sk, m0, g.M, kn, k_end, tid);
+    sb.template load<FB>(Bm, g.b_sn, g.b_sk, n0, g.N, kn, k_end, tid);
+    // Memory clobber: keeps these loads here instead of letting the optimizer
+    // merge them with the prologue's into one load after the loop-header phi,
+    // right before the LDS store that waits for it.
+    asm volatile("" ::: "memory");
+    gemm_stage_mfma<BM, KT, A_KC, B_KC>(As, Bs, acc);
+  }
+  const int kp = k_begin + nfull * KT;
+  if (kp < k_end) {
+    sa.template load<false>(A, g.a_sm, g.a_sk, m0, g.M, kp, k_end, tid);
+    sb.template load<false>(Bm, g.b_sn, g.b_sk, n0, g.N, kp, k_end, tid);
+    __syncthreads();
+    sa.store(As, tid);
+    sb.store(Bs, tid);
+    __syncthreads();
+    gemm_stage_mfma<BM, KT, A_KC, B_KC>(As, Bs, acc);
+  }
+}
+
 // BM x 128 output tile per 256-thread block, 2 x 2 waves of (BM/2) x 64,
 // KT-deep k stages.  MFMA rows are output columns n, MFMA columns output rows m.
 template <int BM, int KT, bool A_KC, bool B_KC, bool PARTIAL>
@@ -191,8 +265,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   const int n0 = (tile % (int)gridDim.x) * kGBN, m0 = (tile / (int)gridDim.x) * BM;
   const int bt = (int)blockIdx.z / g.splits;
   const int k_begin = ((int)blockIdx.z % g.splits) * g.k_chunk;
-  const float* __restrict__ A = g.a + bt * g.a_sb;
-  const float* __restrict__ Bm = g.b + bt * g.b_sb;
+  const float* A = g.a + bt * g.a_sb;
+  const float* Bm = g.b + bt * g.b_sb;
   const int k_end = min(g.K, k_begin + g.k_chunk);
 
   floatx4 acc[4][MT];
@@ -201,39 +275,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < MT; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  SA sa;
-  SB sb;
-  const bool rows_a = g.a_vec && m0 + BM <= g.M;
-  const bool rows_b = g.b_vec && n0 + kGBN <= g.N;
-  if (k_begin < k_end) {
-    sa.load(A, g.a_sm, g.a_sk, m0, g.M, k_begin, k_end, tid, rows_a && k_begin + KT <= k_end);
-    sb.load(Bm, g.b_sn, g.b_sk, n0, g.N, k_begin, k_end, tid, rows_b && k_begin + KT <= k_end);
-  }
-  for (int kk = k_begin; kk < k_end; kk += KT) {
-    __syncthreads();
-    sa.store(As, tid);
-    sb.store(Bs, tid);
-    __syncthreads();
-    if (kk + KT < k_end) {
-      const bool kin = kk + 2 * KT <= k_end;
-      sa.load(A, g.a_sm, g.a_sk, m0, g.M, kk + KT, k_end, tid, rows_a && kin);
-      sb.load(Bm, g.b_sn, g.b_sk, n0, g.N, kk + KT, k_end, tid, rows_b && kin);
-    }
-#pragma unroll
-    for (int ks = 0; ks < KT; ks += 16) {
-      float bvals[4][4], avals[MT][4];
-      SB::template fetch<4>(Bs, 64 * wn, ks, lq, gq, bvals);
-      SA::template fetch<MT>(As, (BM / 2) * wm, ks, lq, gq, avals);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = mfma4(bvals[nt][e], avals[mt][e], acc[nt][mt]);
-        }
-      }
-    }
-  }
+  // Interior blocks take unpredicated loads for every k stage but a partial last one.
+  const bool fa = g.a_vec && m0 + BM <= g.M;
+  const bool fb = g.b_vec && n0 + kGBN <= g.N;
+  if (fa && fb)
+    gemm_mainloop<BM, KT, A_KC, B_KC, true, true>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc);
+  else if (fa)
+    gemm_mainloop<BM, KT, A_KC, B_KC, true, false>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc);
+  else if (fb)
+    gemm_mainloop<BM, KT, A_KC, B_KC, false, true>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc);
+  else
+    gemm_mainloop<BM, KT, A_KC, B_KC, false, false>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc);
 
   // acc[nt][mt][i] = C[m][n] with m = m0 + (BM/2)wm + SA::row_of(mt, lq) and
   // n = n0 + 64wn + SB::row_of(nt, 4gq + i): four consecutive n over i (B_KC)
