@@ -251,9 +251,11 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
   auto load_tile = [&](int qt) {
     qs.load(Q + base, qt * BMQ, L.T, L.D, L.st, tid);
     os.load(dO + base, qt * BMQ, L.T, L.D, L.st, tid);
+    // raw LSE (scaled when stored to LDS): arithmetic on a value here would wait
+    // for its load and, with it, for the tile loads issued just before
     if (tid < BMQ) {
       const int q = qt * BMQ + tid;
-      lse_r = (!PROBS && q < L.T) ? LSE[rbase + q] * kLog2e : 0.f;
+      lse_r = (!PROBS && q < L.T) ? LSE[rbase + q] : 0.f;
       del_r = q < L.T ? Delta[rbase + q] : 0.f;
     }
   };
@@ -264,7 +266,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
     qs.template store<LD>(Qs, tid);
     os.template store<LD>(Os, tid);
     if (tid < BMQ) {
-      lse_s[tid] = lse_r;
+      lse_s[tid] = lse_r * kLog2e;
       del_s[tid] = del_r;
     }
     __syncthreads();

@@ -308,9 +308,11 @@ __global__ __launch_bounds__(256) void wave_dkv_kernel(const float* __restrict__
   auto load_tile = [&](int qt) {
     fs.load(Fh, qt * BMQ, T, kFP, kFP, tid);
     os.load(dO + vbase, qt * BMQ, T, Lv.D, Lv.st, tid);
+    // raw LSE (scaled when stored to LDS): arithmetic on a value here would wait
+    // for its load and, with it, for the tile loads issued just before
     if (tid < BMQ) {
       const int q = qt * BMQ + tid;
-      lse_r = q < T ? LSE[rbase + q] * kLog2e : 0.f;
+      lse_r = q < T ? LSE[rbase + q] : 0.f;
       del_r = q < T ? Delta[rbase + q] : 0.f;
       qb_r = q < T ? Bh[q] : 0;
     }
@@ -323,7 +325,7 @@ __global__ __launch_bounds__(256) void wave_dkv_kernel(const float* __restrict__
     fs.template store<kLDF>(Fs, tid);
     os.template store<LD>(Os, tid);
     if (tid < BMQ) {
-      lse_s[tid] = lse_r;
+      lse_s[tid] = lse_r * kLog2e;
       del_s[tid] = del_r;
       qb_s[tid] = qb_r;
     }
