@@ -19,8 +19,8 @@
 // MFMA contraction per tile instead of recomputing S and dP (the reference's
 // wgpu tier likewise hands d_score from one kernel to the other through a
 // scratch buffer, src/wgpu_tier/dispatch_backward.rs:367).  dS buffer layout
-// per (b,h): column block kt (keys 64kt..64kt+63) holds rows q = 64kt..T-1,
-// 64 floats each, blocks back to back (ds_block_row below).  When that buffer
+// per (b,h): column block kt (keys 64kt..64kt+63) holds rows q = 64kt..Tp-1
+// (Tp = T rounded up to 64), 64 floats each, blocks back to back (ds_block_row).  When that buffer
 // would be too large, attn_bwd_dq_kernel recomputes S and dP instead.
 // The "from probabilities" variants read P from the caller's att tensor instead
 // of recomputing it (the reference contract, att used as given), and obtain
@@ -330,16 +330,15 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
     }
 
     if (DS_OUT) {
-      // dS[q][64kt + 16*wave + lq] for this lane's 16 queries
-      float* dsb = DS + ((int64_t)bh * ds_rows(L.T) + ds_block_row(kt, L.T) - (int64_t)64 * kt) * 64 +
+      // dS[q][64kt + 16*wave + lq] for this lane's 16 queries q = qb + 16mt + 4g + i:
+      // the workspace has rows up to T rounded up to 64, so the whole tile is
+      // stored without per-row checks, at constant offsets from one address
+      float* dsq = DS + ((int64_t)bh * ds_rows(L.T) + ds_block_row(kt, L.T) - (int64_t)64 * kt + qb + 4 * g) * 64 +
                    wave * 16 + lq;
 #pragma unroll
       for (int mt = 0; mt < NQT; ++mt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int q = qb + 16 * mt + 4 * g + i;
-          if (q < L.T) dsb[(int64_t)q * 64] = dp[mt][i];
-        }
+        for (int i = 0; i < 4; ++i) dsq[(16 * mt + i) * 64] = dp[mt][i];
       }
     }
 

@@ -391,12 +391,13 @@ __global__ __launch_bounds__(256) void wave_dkv_kernel(const float* __restrict__
       }
     }
 
+    {
+      // rows up to T rounded up to 64 exist in the workspace: no per-row checks
+      float* dsq = dsb + (int64_t)(qbase + 4 * g) * 64;
 #pragma unroll
-    for (int mt = 0; mt < NQT; ++mt) {
+      for (int mt = 0; mt < NQT; ++mt) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int q = qbase + 16 * mt + 4 * g + i;
-        if (q < T) dsb[(int64_t)q * 64] = dp[mt][i];
+        for (int i = 0; i < 4; ++i) dsq[(16 * mt + i) * 64] = dp[mt][i];
       }
     }
 

@@ -214,11 +214,14 @@ __device__ __forceinline__ void store_row_frag(float* __restrict__ base, int row
   }
 }
 
-// dS workspace of the backward, per (b,h): column block kt (keys 64kt..64kt+63)
-// holds rows q = 64kt..T-1, 64 floats each, blocks back to back.
-// First row of column block kt: sum_{j<kt} (T - 64 j).
+// dS workspace of the backward, per (b,h), with Tp = T rounded up to 64:
+// column block kt (keys 64kt..64kt+63) holds rows q = 64kt..Tp-1, 64 floats
+// each, blocks back to back.  Rows past T exist so that a 64-query tile is
+// written without a bounds check per row; they are never read.
+// First row of column block kt: sum_{j<kt} (Tp - 64 j).
 __host__ __device__ __forceinline__ int64_t ds_block_row(int kt, int T) {
-  return (int64_t)kt * T - (int64_t)32 * kt * (kt - 1);
+  const int64_t Tp = ((int64_t)T + 63) / 64 * 64;
+  return (int64_t)kt * Tp - (int64_t)32 * kt * (kt - 1);
 }
 // Rows of dS per (b,h).
 __host__ __device__ __forceinline__ int64_t ds_rows(int T) { return ds_block_row((T + 63) / 64, T); }
