@@ -261,7 +261,7 @@ def run_wave(args, cfg, pkg, torch):
         step()
     torch.cuda.synchronize()
     names = ("wave_feat", "wave_fwd", "wave_bwd_delta", "wave_bwd_dkv", "wave_bwd_dq", "wave_feat_bwd",
-             "wave_harmonic", "linear_fwd", "linear_bwd_dx", "linear_bwd_dw", "linear_bwd_db")
+             "wave_harmonic", "linear_fwd", "linear_bwd_dx", "linear_bwd_dw")
     pkg.timing_reset()
     pkg.timing_enable(True)
     torch.cuda.synchronize()
@@ -427,7 +427,7 @@ def run_layer(args, cfg, pkg, torch):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    names = ("linear_fwd", "linear_bwd_dx", "linear_bwd_dw", "linear_bwd_db", "attn_fwd", "attn_bwd_delta",
+    names = ("linear_fwd", "linear_bwd_dx", "linear_bwd_dw", "attn_fwd", "attn_bwd_delta",
              "attn_bwd_dkv", "attn_bwd_dq")
     pkg.timing_reset()
     pkg.timing_enable(True)

@@ -47,6 +47,13 @@ struct GemmArgs {
   int64_t a_sb = 0, b_sb = 0, c_sb = 0, bias_sb = 0;
   bool a_vec = false;  // A's base, batch stride and row stride along its contiguous
   bool b_vec = false;  // direction are 16-byte multiples (set by gemm_t); same for B
+  // Row sums of A over the k range (A k-contiguous only, i.e. the weight-gradient
+  // GEMM, where they are the bias gradient): rowsum[bt*rowsum_sb + m] = sum_k A(m,k),
+  // written by the blocks of the first column tile; with split-K each split writes
+  // rowsum_part[(bt*splits + split)*M + m] and the reduce adds the splits in order.
+  float* rowsum = nullptr;
+  int64_t rowsum_sb = 0;
+  float* rowsum_part = nullptr;
 };
 
 // Staging of one ROWS x KT operand tile; element (r, k) of the source is
@@ -117,6 +124,17 @@ struct GemmStage {
         }
       }
       v[q] = val;
+    }
+  }
+  // Sum of this thread's pieces (not KC: all of a thread's pieces cover the same
+  // four rows rc..rc+3, rc = (tid % (ROWS/4))*4, at different k).
+  __device__ __forceinline__ void add_to(float4& rs) const {
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      rs.x += v[q].x;
+      rs.y += v[q].y;
+      rs.z += v[q].z;
+      rs.w += v[q].w;
     }
   }
   __device__ __forceinline__ void store(float* lds, int tid) const {
@@ -205,7 +223,8 @@ __device__ __forceinline__ void gemm_stage_mfma(const float* As, const float* Bs
 template <int BM, int KT, bool A_KC, bool B_KC, bool FA, bool FB>
 __device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* A,
                                               const float* Bm, int m0, int n0, int k_begin,
-                                              int k_end, float* As, float* Bs, floatx4 (&acc)[4][BM / 32]) {
+                                              int k_end, float* As, float* Bs, floatx4 (&acc)[4][BM / 32],
+                                              float4& rs) {
   using SA = GemmStage<BM, KT, A_KC>;
   using SB = GemmStage<kGBN, KT, B_KC>;
   const int tid = threadIdx.x;
@@ -220,6 +239,7 @@ __device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* A,
     __syncthreads();
     sa.store(As, tid);
     sb.store(Bs, tid);
+    if (!A_KC) sa.add_to(rs);
     __syncthreads();
     const int kn = k_begin + min(i + 1, nfull - 1) * KT;
     sa.template load<FA>(A, g.a_sm, g.a_sk, m0, g.M, kn, k_end, tid);
@@ -237,6 +257,7 @@ __device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* A,
     __syncthreads();
     sa.store(As, tid);
     sb.store(Bs, tid);
+    if (!A_KC) sa.add_to(rs);
     __syncthreads();
     gemm_stage_mfma<BM, KT, A_KC, B_KC>(As, Bs, acc);
   }
@@ -278,14 +299,42 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   // Interior blocks take unpredicated loads for every k stage but a partial last one.
   const bool fa = g.a_vec && m0 + BM <= g.M;
   const bool fb = g.b_vec && n0 + kGBN <= g.N;
+  float4 rs = make_float4(0.f, 0.f, 0.f, 0.f);
   if (fa && fb)
-    gemm_mainloop<BM, KT, A_KC, B_KC, true, true>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc);
+    gemm_mainloop<BM, KT, A_KC, B_KC, true, true>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc, rs);
   else if (fa)
-    gemm_mainloop<BM, KT, A_KC, B_KC, true, false>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc);
+    gemm_mainloop<BM, KT, A_KC, B_KC, true, false>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc, rs);
   else if (fb)
-    gemm_mainloop<BM, KT, A_KC, B_KC, false, true>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc);
+    gemm_mainloop<BM, KT, A_KC, B_KC, false, true>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc, rs);
   else
-    gemm_mainloop<BM, KT, A_KC, B_KC, false, false>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc);
+    gemm_mainloop<BM, KT, A_KC, B_KC, false, false>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc, rs);
+
+  if (!A_KC && n0 == 0 && (PARTIAL ? g.rowsum_part : g.rowsum) != nullptr) {
+    // rows rc..rc+3 (rc = 4*(tid % R4)) are summed by the 256/R4 threads tid % R4 == rc/4,
+    // in increasing tid order, through LDS (As is free once every wave passed its MFMA reads)
+    constexpr int R4 = BM / 4;
+    static_assert(SA::ELEMS >= 4 * 256, "row-sum exchange fits in the A stage");
+    float4* red = reinterpret_cast<float4*>(As);
+    __syncthreads();
+    red[tid] = rs;
+    __syncthreads();
+    if (tid < R4) {
+      float4 t = red[tid];
+      for (int j = 1; j < 256 / R4; ++j) {
+        const float4 u = red[tid + R4 * j];
+        t.x += u.x;
+        t.y += u.y;
+        t.z += u.z;
+        t.w += u.w;
+      }
+      float* dst = PARTIAL ? g.rowsum_part + (int64_t)blockIdx.z * g.M : g.rowsum + bt * g.rowsum_sb;
+      const int m = m0 + 4 * tid;
+      if (m + 0 < g.M) dst[m + 0] = t.x;
+      if (m + 1 < g.M) dst[m + 1] = t.y;
+      if (m + 2 < g.M) dst[m + 2] = t.z;
+      if (m + 3 < g.M) dst[m + 3] = t.w;
+    }
+  }
 
   // acc[nt][mt][i] = C[m][n] with m = m0 + (BM/2)wm + SA::row_of(mt, lq) and
   // n = n0 + 64wn + SB::row_of(nt, 4gq + i): four consecutive n over i (B_KC)
@@ -354,67 +403,11 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
   float* dst = g.c + bt * g.c_sb + (int64_t)m * g.ldc + n;
   const float r = (g.bias != nullptr ? g.bias[bt * g.bias_sb + n] : 0.f) + s;
   *dst = g.accumulate ? *dst + r : r;
-}
-
-// out[bt][n] = sum_m y[bt][m][n] (column sums, for the bias gradient).  Block =
-// 64 columns x one chunk of rows: 16 lanes cover the 64 columns with 128-bit
-// loads (32-bit where the row is not 16-byte aligned), 16 row lanes stride
-// through the chunk, and the 16 row partials are added in a fixed order in
-// LDS; blockIdx.z = batch index (operand offset bt * y_sb).  The chunk partials
-// are then added in order by colsum_final_kernel.
-__global__ __launch_bounds__(256) void colsum_partial_kernel(const float* __restrict__ y, int64_t ldy,
-                                                             int64_t y_sb, int M, int N, int rows_per,
-                                                             float* __restrict__ part) {
-  __shared__ float4 red[16][16];
-  const int cq = threadIdx.x & 15, rl = threadIdx.x >> 4;
-  const int n = blockIdx.x * 64 + 4 * cq;
-  const float* yb = y + (int64_t)blockIdx.z * y_sb;
-  const int r0 = blockIdx.y * rows_per, r1 = min(M, r0 + rows_per);
-  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (n < N) {
-    const bool vec = n + 3 < N && ((((uintptr_t)(yb + n)) | ((uintptr_t)ldy * 4)) & 15) == 0;
-    for (int m = r0 + rl; m < r1; m += 16) {
-      const float* src = yb + (int64_t)m * ldy + n;
-      if (vec) {
-        const float4 v = *reinterpret_cast<const float4*>(src);
-        s.x += v.x;
-        s.y += v.y;
-        s.z += v.z;
-        s.w += v.w;
-      } else {
-        s.x += src[0];
-        if (n + 1 < N) s.y += src[1];
-        if (n + 2 < N) s.z += src[2];
-        if (n + 3 < N) s.w += src[3];
-      }
-    }
+  if (n == 0 && g.rowsum != nullptr) {
+    float t = 0.f;
+    for (int z = 0; z < g.splits; ++z) t += g.rowsum_part[((int64_t)bt * g.splits + z) * g.M + m];
+    g.rowsum[bt * g.rowsum_sb + m] = t;
   }
-  red[rl][cq] = s;
-  __syncthreads();
-  if (rl == 0 && n < N) {
-    float4 t = red[0][cq];
-    for (int j = 1; j < 16; ++j) {
-      t.x += red[j][cq].x;
-      t.y += red[j][cq].y;
-      t.z += red[j][cq].z;
-      t.w += red[j][cq].w;
-    }
-    float* dst = part + ((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * N + n;
-    dst[0] = t.x;
-    if (n + 1 < N) dst[1] = t.y;
-    if (n + 2 < N) dst[2] = t.z;
-    if (n + 3 < N) dst[3] = t.w;
-  }
-}
-
-__global__ __launch_bounds__(256) void colsum_final_kernel(const float* __restrict__ part, int chunks, int N,
-                                                           float* __restrict__ out) {
-  const int n = blockIdx.x * 256 + threadIdx.x;
-  if (n >= N) return;
-  const float* pb = part + (int64_t)blockIdx.z * chunks * N;
-  float s = 0.f;
-  for (int z = 0; z < chunks; ++z) s += pb[(int64_t)z * N + n];
-  out[(int64_t)blockIdx.z * N + n] = s;
 }
 
 namespace {
@@ -435,7 +428,6 @@ int gemm_splits(int M, int N, int K, int batch, int min_k = 256) {
   return splits;
 }
 
-int colsum_chunks(int M) { return M >= 4096 ? 16 : (M >= 256 ? 4 : 1); }
 
 template <int BM, int KT, bool A_KC, bool B_KC>
 hipError_t gemm_launch(GemmArgs g, float* ws, int splits, const char* name, hipStream_t stream) {
@@ -476,10 +468,10 @@ hipError_t gemm_t(GemmArgs g, float* ws, const char* name, hipStream_t stream, i
 }  // namespace
 
 size_t linear_dw_workspace_floats(int N, int K, int64_t M, int batch) {
-  // split-K partials of the [batch][N][K] weight gradient plus column-sum partials
+  // split-K partials of the [batch][N][K] weight gradient and of the bias gradient
   const int splits = gemm_splits(N, K, (int)(M > 0x7fffffff ? 0x7fffffff : M), batch);
-  const size_t part = splits > 1 ? (size_t)splits * batch * N * K : 0;
-  return part + (size_t)colsum_chunks((int)M) * N * batch + 64;
+  const size_t part = splits > 1 ? (size_t)splits * batch * N * (K + 1) : 0;
+  return part + 64;
 }
 
 // Few output tiles (decode-sized M): split K down to 64 per split.
@@ -520,7 +512,8 @@ hipError_t launch_linear_bwd_dx_batched(const float* dy, int64_t lddy, int64_t d
 }
 
 // dw[bt] = dy[bt]^T x[bt] over the M rows:  dy [M][N], x [M][K], dw [N][K];
-// db[bt*N + n] = sum_m dy[bt][m][n] when db != nullptr.  ws: linear_dw_workspace_floats.
+// db[bt*N + n] = sum_m dy[bt][m][n] when db != nullptr, summed inside the same GEMM (row
+// sums of its A operand).  ws: linear_dw_workspace_floats.
 hipError_t launch_linear_bwd_dw_batched(const float* dy, int64_t lddy, int64_t dy_sb, const float* x,
                                         int64_t ldx, int64_t x_sb, float* dw, int64_t dw_sb, float* db, int M,
                                         int N, int K, int batch, float* ws, hipStream_t stream) {
@@ -534,19 +527,12 @@ hipError_t launch_linear_bwd_dw_batched(const float* dy, int64_t lddy, int64_t d
   g.c_sb = dw_sb;
   const int splits = gemm_splits(N, K, M, batch);
   float* part = splits > 1 ? ws : nullptr;
-  hipError_t e = gemm_t<false, false>(g, part, "linear_bwd_dw", stream);
-  if (e != hipSuccess || db == nullptr) return e;
-  float* cs = ws + (splits > 1 ? (size_t)splits * batch * N * K : 0);
-  const int chunks = colsum_chunks(M);
-  const int rows_per = (M + chunks - 1) / chunks;
-  TimingScope ts("linear_bwd_db", stream);
-  hipLaunchKernelGGL(colsum_partial_kernel, dim3((unsigned)((N + 63) / 64), (unsigned)chunks, (unsigned)batch),
-                     dim3(256), 0, stream, dy, lddy, dy_sb, M, N, rows_per, cs);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(colsum_final_kernel, dim3((unsigned)((N + 255) / 256), 1, (unsigned)batch), dim3(256), 0,
-                     stream, (const float*)cs, chunks, N, db);
-  return hipGetLastError();
+  if (db != nullptr) {
+    g.rowsum = db;
+    g.rowsum_sb = N;
+    if (splits > 1) g.rowsum_part = ws + (size_t)splits * batch * N * K;
+  }
+  return gemm_t<false, false>(g, part, "linear_bwd_dw", stream);
 }
 
 size_t linear_dw_workspace_floats(int N, int K, int64_t M) { return linear_dw_workspace_floats(N, K, M, 1); }
