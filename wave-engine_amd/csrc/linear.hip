@@ -27,7 +27,9 @@
 namespace wha {
 
 namespace {
-constexpr int kGBN = 128;  // output columns per block (2 waves x 64)
+// Output columns per block: 64 per wave along n, WN = 2 waves along n (128
+// columns) or WN = 1 (64 columns, for N <= 64: the per-head value projections).
+constexpr int kGBN = 128;
 }
 
 struct GemmArgs {
@@ -189,19 +191,20 @@ struct GemmStage {
 };
 
 // MFMA work of one KT-deep stage held in LDS.
-template <int BM, int KT, bool A_KC, bool B_KC>
-__device__ __forceinline__ void gemm_stage_mfma(const float* As, const float* Bs, floatx4 (&acc)[4][BM / 32]) {
+template <int BM, int KT, int WN, bool A_KC, bool B_KC>
+__device__ __forceinline__ void gemm_stage_mfma(const float* As, const float* Bs,
+                                                floatx4 (&acc)[4][BM * WN / 64]) {
   using SA = GemmStage<BM, KT, A_KC>;
-  using SB = GemmStage<kGBN, KT, B_KC>;
-  constexpr int MT = BM / 32;
+  using SB = GemmStage<64 * WN, KT, B_KC>;
+  constexpr int MT = BM * WN / 64;  // 16-row m tiles per wave
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int lq = lane & 15, gq = lane >> 4;
-  const int wn = wave & 1, wm = wave >> 1;
+  const int wn = wave % WN, wm = wave / WN;
 #pragma unroll
   for (int ks = 0; ks < KT; ks += 16) {
     float bvals[4][4], avals[MT][4];
     SB::template fetch<4>(Bs, 64 * wn, ks, lq, gq, bvals);
-    SA::template fetch<MT>(As, (BM / 2) * wm, ks, lq, gq, avals);
+    SA::template fetch<MT>(As, 16 * MT * wm, ks, lq, gq, avals);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
 #pragma unroll
@@ -220,13 +223,13 @@ __device__ __forceinline__ void gemm_stage_mfma(const float* As, const float* Bs
 // across the MFMA work.  A partial stage at the end of the k range follows on
 // its own.  FA / FB: the block's A / B rows are all in bounds and 16-byte
 // aligned, so their k-full stages load unpredicated.
-template <int BM, int KT, bool A_KC, bool B_KC, bool FA, bool FB>
+template <int BM, int KT, int WN, bool A_KC, bool B_KC, bool FA, bool FB>
 __device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* A,
                                               const float* Bm, int m0, int n0, int k_begin,
-                                              int k_end, float* As, float* Bs, floatx4 (&acc)[4][BM / 32],
-                                              float4& rs) {
+                                              int k_end, float* As, float* Bs,
+                                              floatx4 (&acc)[4][BM * WN / 64], float4& rs) {
   using SA = GemmStage<BM, KT, A_KC>;
-  using SB = GemmStage<kGBN, KT, B_KC>;
+  using SB = GemmStage<64 * WN, KT, B_KC>;
   const int tid = threadIdx.x;
   const int nfull = k_end > k_begin ? (k_end - k_begin) / KT : 0;
   SA sa;
@@ -248,7 +251,7 @@ __device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* A,
     // merge them with the prologue's into one load after the loop-header phi,
     // right before the LDS store that waits for it.
     asm volatile("" ::: "memory");
-    gemm_stage_mfma<BM, KT, A_KC, B_KC>(As, Bs, acc);
+    gemm_stage_mfma<BM, KT, WN, A_KC, B_KC>(As, Bs, acc);
   }
   const int kp = k_begin + nfull * KT;
   if (kp < k_end) {
@@ -259,23 +262,25 @@ __device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* A,
     sb.store(Bs, tid);
     if (!A_KC) sa.add_to(rs);
     __syncthreads();
-    gemm_stage_mfma<BM, KT, A_KC, B_KC>(As, Bs, acc);
+    gemm_stage_mfma<BM, KT, WN, A_KC, B_KC>(As, Bs, acc);
   }
 }
 
-// BM x 128 output tile per 256-thread block, 2 x 2 waves of (BM/2) x 64,
-// KT-deep k stages.  MFMA rows are output columns n, MFMA columns output rows m.
-template <int BM, int KT, bool A_KC, bool B_KC, bool PARTIAL>
+// BM x 64*WN output tile per 256-thread block, (4/WN) x WN waves of
+// (BM*WN/4) x 64, KT-deep k stages.  MFMA rows are output columns n, MFMA
+// columns output rows m.
+template <int BM, int KT, int WN, bool A_KC, bool B_KC, bool PARTIAL>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+  constexpr int BN = 64 * WN;
   using SA = GemmStage<BM, KT, A_KC>;
-  using SB = GemmStage<kGBN, KT, B_KC>;
-  constexpr int MT = BM / 32;  // 16-row m tiles per wave
+  using SB = GemmStage<BN, KT, B_KC>;
+  constexpr int MT = BM * WN / 64;  // 16-row m tiles per wave
   __shared__ __align__(16) float As[SA::ELEMS];
   __shared__ __align__(16) float Bs[SB::ELEMS];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int lq = lane & 15, gq = lane >> 4;
-  const int wn = wave & 1, wm = wave >> 1;
+  const int wn = wave % WN, wm = wave / WN;
   // XCD-aware tile order: blocks are dealt round-robin to the 8 XCDs by linear
   // id, so when a split's tile count is a multiple of 8, block j of XCD x takes
   // tile x*(tiles/8) + j: each XCD then sweeps a contiguous band of m-tiles
@@ -283,7 +288,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   int tile = (int)(blockIdx.y * gridDim.x + blockIdx.x);
   const int tiles = (int)(gridDim.x * gridDim.y);
   if (tiles % 8 == 0) tile = (tile % 8) * (tiles / 8) + tile / 8;
-  const int n0 = (tile % (int)gridDim.x) * kGBN, m0 = (tile / (int)gridDim.x) * BM;
+  const int n0 = (tile % (int)gridDim.x) * BN, m0 = (tile / (int)gridDim.x) * BM;
   const int bt = (int)blockIdx.z / g.splits;
   const int k_begin = ((int)blockIdx.z % g.splits) * g.k_chunk;
   const float* A = g.a + bt * g.a_sb;
@@ -298,16 +303,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 
   // Interior blocks take unpredicated loads for every k stage but a partial last one.
   const bool fa = g.a_vec && m0 + BM <= g.M;
-  const bool fb = g.b_vec && n0 + kGBN <= g.N;
+  const bool fb = g.b_vec && n0 + BN <= g.N;
   float4 rs = make_float4(0.f, 0.f, 0.f, 0.f);
   if (fa && fb)
-    gemm_mainloop<BM, KT, A_KC, B_KC, true, true>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc, rs);
+    gemm_mainloop<BM, KT, WN, A_KC, B_KC, true, true>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc, rs);
   else if (fa)
-    gemm_mainloop<BM, KT, A_KC, B_KC, true, false>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc, rs);
+    gemm_mainloop<BM, KT, WN, A_KC, B_KC, true, false>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc, rs);
   else if (fb)
-    gemm_mainloop<BM, KT, A_KC, B_KC, false, true>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc, rs);
+    gemm_mainloop<BM, KT, WN, A_KC, B_KC, false, true>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc, rs);
   else
-    gemm_mainloop<BM, KT, A_KC, B_KC, false, false>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc, rs);
+    gemm_mainloop<BM, KT, WN, A_KC, B_KC, false, false>(g, A, Bm, m0, n0, k_begin, k_end, As, Bs, acc, rs);
 
   if (!A_KC && n0 == 0 && (PARTIAL ? g.rowsum_part : g.rowsum) != nullptr) {
     // rows rc..rc+3 (rc = 4*(tid % R4)) are summed by the 256/R4 threads tid % R4 == rc/4,
@@ -336,14 +341,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     }
   }
 
-  // acc[nt][mt][i] = C[m][n] with m = m0 + (BM/2)wm + SA::row_of(mt, lq) and
+  // acc[nt][mt][i] = C[m][n] with m = m0 + 16*MT*wm + SA::row_of(mt, lq) and
   // n = n0 + 64wn + SB::row_of(nt, 4gq + i): four consecutive n over i (B_KC)
   // or over nt (otherwise) go out as one 128-bit store.
   const bool vec = PARTIAL ? (g.N % 4 == 0) : g.c_vec;
   const float* bias = (!PARTIAL && g.bias != nullptr) ? g.bias + bt * g.bias_sb : nullptr;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const int m = m0 + (BM / 2) * wm + SA::row_of(mt, lq, MT);
+    const int m = m0 + 16 * MT * wm + SA::row_of(mt, lq, MT);
     if (m >= g.M) continue;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -412,31 +417,35 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
 
 namespace {
 
+// Tile width: 64 columns for N <= 64, else 128.
+int gemm_bn(int N) { return N <= 64 ? 64 : kGBN; }
+
 // Tile height: 128 rows unless that leaves fewer than two blocks per CU.
 constexpr int kCUs = 256;
 int gemm_bm(int M, int N, int batch) {
-  const int tiles128 = ((M + 127) / 128) * ((N + kGBN - 1) / kGBN) * batch;
+  const int bn = gemm_bn(N);
+  const int tiles128 = ((M + 127) / 128) * ((N + bn - 1) / bn) * batch;
   return tiles128 >= 2 * kCUs ? 128 : 64;
 }
 
 // Split-K factor: aim for >= 512 blocks while keeping >= min_k k per split.
 int gemm_splits(int M, int N, int K, int batch, int min_k = 256) {
-  const int bm = gemm_bm(M, N, batch);
-  const int tiles = ((M + bm - 1) / bm) * ((N + kGBN - 1) / kGBN) * batch;
+  const int bm = gemm_bm(M, N, batch), bn = gemm_bn(N);
+  const int tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch;
   int splits = 1;
   while (tiles * splits < 512 && (K / (splits * 2)) >= min_k) splits *= 2;
   return splits;
 }
 
 
-template <int BM, int KT, bool A_KC, bool B_KC>
+template <int BM, int KT, int WN, bool A_KC, bool B_KC>
 hipError_t gemm_launch(GemmArgs g, float* ws, int splits, const char* name, hipStream_t stream) {
-  const dim3 grid((g.N + kGBN - 1) / kGBN, (g.M + BM - 1) / BM, splits * g.batch);
+  const dim3 grid((g.N + 64 * WN - 1) / (64 * WN), (g.M + BM - 1) / BM, splits * g.batch);
   g.splits = splits;
   TimingScope ts(name, stream);
   if (splits == 1) {
     g.k_chunk = ((g.K + KT - 1) / KT) * KT;
-    hipLaunchKernelGGL((gemm_kernel<BM, KT, A_KC, B_KC, false>), grid, dim3(256), 0, stream, g);
+    hipLaunchKernelGGL((gemm_kernel<BM, KT, WN, A_KC, B_KC, false>), grid, dim3(256), 0, stream, g);
     return hipGetLastError();
   }
   const int per = (g.K + splits - 1) / splits;
@@ -444,7 +453,7 @@ hipError_t gemm_launch(GemmArgs g, float* ws, int splits, const char* name, hipS
   p.k_chunk = ((per + KT - 1) / KT) * KT;
   p.c = ws;
   p.bias = nullptr;
-  hipLaunchKernelGGL((gemm_kernel<BM, KT, A_KC, B_KC, true>), grid, dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((gemm_kernel<BM, KT, WN, A_KC, B_KC, true>), grid, dim3(256), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t total = (int64_t)g.M * g.N * g.batch;
@@ -461,8 +470,12 @@ hipError_t gemm_t(GemmArgs g, float* ws, const char* name, hipStream_t stream, i
   // 128-bit loads need every row start along the contiguous direction 16-byte aligned
   g.a_vec = aligned16(g.a) && g.a_sb % 4 == 0 && (A_KC ? g.a_sm % 4 == 0 : g.a_sk % 4 == 0);
   g.b_vec = aligned16(g.b) && g.b_sb % 4 == 0 && (B_KC ? g.b_sn % 4 == 0 : g.b_sk % 4 == 0);
-  if (gemm_bm(g.M, g.N, g.batch) == 128) return gemm_launch<128, WHA_GEMM_KT, A_KC, B_KC>(g, ws, splits, name, stream);
-  return gemm_launch<64, WHA_GEMM_KT, A_KC, B_KC>(g, ws, splits, name, stream);
+  const bool bm128 = gemm_bm(g.M, g.N, g.batch) == 128;
+  if (gemm_bn(g.N) == 64)
+    return bm128 ? gemm_launch<128, WHA_GEMM_KT, 1, A_KC, B_KC>(g, ws, splits, name, stream)
+                 : gemm_launch<64, WHA_GEMM_KT, 1, A_KC, B_KC>(g, ws, splits, name, stream);
+  return bm128 ? gemm_launch<128, WHA_GEMM_KT, 2, A_KC, B_KC>(g, ws, splits, name, stream)
+               : gemm_launch<64, WHA_GEMM_KT, 2, A_KC, B_KC>(g, ws, splits, name, stream);
 }
 
 }  // namespace
