@@ -53,32 +53,59 @@ __device__ __forceinline__ bool bucket_near(int kb, int qb) { return ((kb - qb +
 
 // proj [B][T][H][P] (P = 2 + C: r, s, content) -> feat [B][H][T][32]
 // (cos n phi, sin n phi, content, zeros), phase and bucket [B][H][T].
+// Block = positions t0 .. t0+TT-1 of one b, all H heads.  Each position is
+// computed by one thread in proj's order (consecutive threads read consecutive
+// rows), staged in LDS head-major (odd pitch, conflict-free) and written out in
+// the outputs' order: per head a contiguous run of TT feature rows, phases and
+// buckets.
 __global__ __launch_bounds__(256) void wave_feat_kernel(const float* __restrict__ proj,
                                                         const float* __restrict__ hraw, float* __restrict__ feat,
                                                         float* __restrict__ phase, int* __restrict__ bucket, int B,
-                                                        int H, int T, int C, int C_used) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)B * H * T) return;
-  const int t = (int)(i % T);
-  const int64_t bh = i / T;
-  const int b = (int)(bh / H), h = (int)(bh % H);
+                                                        int H, int T, int C, int C_used, int TT) {
+  extern __shared__ float sm[];
+  constexpr int FPITCH = kFP + 1;
+  const int nbt = (T + TT - 1) / TT;
+  const int b = (int)blockIdx.x / nbt, t0 = ((int)blockIdx.x % nbt) * TT;
+  const int tn = min(TT, T - t0);
   const int P = 2 + C;
-  const float* pr = proj + (((int64_t)b * T + t) * H + h) * P;
-  const float phi = atan2f(pr[1], pr[0]);
-  const float n = softplus_f(hraw[h]);
-  float sn, cn;
-  sincosf(n * phi, &sn, &cn);
-  float f[kFP];
-#pragma unroll
-  for (int j = 0; j < kFP; ++j) f[j] = 0.f;
-  f[0] = cn;
-  f[1] = sn;
-  for (int j = 0; j < C_used; ++j) f[2 + j] = pr[2 + j];
-  float4* dst = reinterpret_cast<float4*>(feat + i * kFP);
-#pragma unroll
-  for (int j = 0; j < kFP / 4; ++j) dst[j] = make_float4(f[4 * j], f[4 * j + 1], f[4 * j + 2], f[4 * j + 3]);
-  phase[i] = phi;
-  bucket[i] = phase_bucket(phi);
+  const int npos = tn * H;
+  float* fs = sm;                                // [H][tn][FPITCH]
+  float* ps = sm + (size_t)H * TT * FPITCH;      // [H][tn] phase
+  int* bs = reinterpret_cast<int*>(ps + H * TT);  // [H][tn] bucket
+  const float* pblk = proj + ((int64_t)b * T + t0) * H * P;
+  for (int pidx = threadIdx.x; pidx < npos; pidx += 256) {
+    const int tt = pidx / H, h = pidx % H;
+    const float* pr = pblk + (int64_t)pidx * P;
+    const float phi = atan2f(pr[1], pr[0]);
+    const float n = softplus_f(hraw[h]);
+    float sn, cn;
+    sincosf(n * phi, &sn, &cn);
+    float* f = fs + (h * tn + tt) * FPITCH;
+    f[0] = cn;
+    f[1] = sn;
+    for (int j = 0; j < kFP - 2; ++j) {
+      float v = 0.f;
+      if (j < C_used) v = pr[2 + j];
+      f[2 + j] = v;
+    }
+    ps[h * tn + tt] = phi;
+    bs[h * tn + tt] = phase_bucket(phi);
+  }
+  __syncthreads();
+  // per head: tn feature rows (tn*8 float4), tn phases and buckets, each contiguous in memory
+  for (int e = threadIdx.x; e < H * tn * (kFP / 4); e += 256) {
+    const int r = e / (kFP / 4), q = e % (kFP / 4);  // r = h*tn + tt
+    const int h = r / tn, tt = r % tn;
+    const float* f = fs + r * FPITCH + 4 * q;
+    const int64_t i = ((int64_t)b * H + h) * T + t0 + tt;
+    reinterpret_cast<float4*>(feat + i * kFP)[q] = make_float4(f[0], f[1], f[2], f[3]);
+  }
+  for (int r = threadIdx.x; r < H * tn; r += 256) {
+    const int h = r / tn, tt = r % tn;
+    const int64_t i = ((int64_t)b * H + h) * T + t0 + tt;
+    phase[i] = ps[r];
+    bucket[i] = bs[r];
+  }
 }
 
 // Fused forward.  Block = 16*NW queries of one (b,h), heaviest query tiles
@@ -420,12 +447,16 @@ __global__ __launch_bounds__(256) void wave_dkv_kernel(const float* __restrict__
   store_row_frag<DP, VEC>(dV + vbase, krow, T, Lv.D, Lv.st, g, dvacc, 1.f);
 }
 
-// Per position: total raw feature gradient G = dF_q + dF_k (weights applied
-// here: 1 for cos/sin, cs for content), u = G . d f / d(n phi), d phi = n u,
-// then atan2's backward with the reference's guards (attn_backward.rs:203-218)
-// into dproj [B][T][H][P] = (d r, d s, d content), the layout of the forward
-// projection so that the input and weight gradients are two GEMMs.  Harmonic
-// partial phi * u goes to hpart[h][b*T + t].
+// Feature backward.  G = dF_q + dF_k (the score is symmetric in the two
+// feature rows); dphi = n (cos nphi G1 - sin nphi G0); atan2's backward with the
+// reference's guards (attn_backward.rs:203-218) gives d r, d s; the content
+// gradient is cs G[2..]; the harmonic partial is phi * dphi / n.  Block =
+// positions t0 .. t0+TT-1 of one b, all H heads: the head-major inputs (G rows,
+// cos/sin, phase) are read as contiguous per-head runs and staged in LDS in
+// proj's order (odd pitch), one thread per position computes its dproj row
+// into LDS, the block's dproj rows (contiguous in memory) are written out
+// coalesced, and the block's harmonic partial per head (its positions summed
+// in order) goes to hpart[block][h].
 __global__ __launch_bounds__(256) void wave_feat_bwd_kernel(const float* __restrict__ proj,
                                                             const float* __restrict__ feat,
                                                             const float* __restrict__ phase,
@@ -433,48 +464,82 @@ __global__ __launch_bounds__(256) void wave_feat_bwd_kernel(const float* __restr
                                                             const float* __restrict__ dFk,
                                                             const float* __restrict__ hraw,
                                                             float* __restrict__ dproj, float* __restrict__ hpart,
-                                                            int B, int H, int T, int C, float cs) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)B * H * T) return;
-  const int t = (int)(i % T);
-  const int64_t bh = i / T;
-  const int b = (int)(bh / H), h = (int)(bh % H);
+                                                            int B, int H, int T, int C, float cs, int TT) {
+  extern __shared__ float sm[];
+  const int nbt = (T + TT - 1) / TT;
+  const int b = (int)blockIdx.x / nbt, t0 = ((int)blockIdx.x % nbt) * TT;
+  const int tn = min(TT, T - t0);
   const int P = 2 + C;
-  const float* gq = dFq + i * kFP;
-  const float* gk = dFk + i * kFP;
-  const float cn = feat[i * kFP + 0], sn = feat[i * kFP + 1];
-  const float g0 = gq[0] + gk[0], g1 = gq[1] + gk[1];
-  const float u = cn * g1 - sn * g0;
-  const float n = softplus_f(hraw[h]);
-  const float dphi = n * u;
-  const int64_t prow = ((int64_t)b * T + t) * H + h;
-  const float* pr = proj + prow * P;
-  float* dp = dproj + prow * P;
-  const float r = pr[0], s = pr[1];
-  const float mag_sq = r * r + s * s;
-  float d_r = 0.f, d_s = 0.f;
-  if (fabsf(dphi) >= 1e-12f && mag_sq >= 1e-8f) {
-    const float m = fmaxf(mag_sq, 1e-12f);
-    d_r = dphi * (-s / m);
-    d_s = dphi * (r / m);
+  const int P4 = (P + 3) / 4;                  // float4 pieces of a gradient row that hold G
+  const int GP = (P + 3) | 1;                  // odd pitch: G[0..P-1], cos, sin, phi
+  const int npos = tn * H;
+  float* gs = sm;                              // [tn*H][GP], proj order
+  float* ds = sm + (size_t)TT * H * GP;        // [tn*H][P]
+  float* hs = ds + (size_t)TT * H * P;         // [tn*H] harmonic partials
+  // G rows: per head, tn consecutive rows of 32 floats, the first 4*P4 used
+  for (int e = threadIdx.x; e < H * tn * P4; e += 256) {
+    const int r = e / P4, q = e % P4;          // r = h*tn + tt
+    const int h = r / tn, tt = r % tn;
+    const int64_t i = ((int64_t)b * H + h) * T + t0 + tt;
+    const float4 x = reinterpret_cast<const float4*>(dFq + i * kFP)[q];
+    const float4 y = reinterpret_cast<const float4*>(dFk + i * kFP)[q];
+    float* g = gs + (tt * H + h) * GP + 4 * q;
+    const float v[4] = {x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (4 * q + k < P) g[k] = v[k];
   }
-  dp[0] = d_r;
-  dp[1] = d_s;
-  for (int j = 0; j < C; ++j) dp[2 + j] = cs * (gq[2 + j] + gk[2 + j]);
-  hpart[(int64_t)h * B * T + (int64_t)b * T + t] = phase[i] * u;
+  for (int r = threadIdx.x; r < H * tn; r += 256) {
+    const int h = r / tn, tt = r % tn;
+    const int64_t i = ((int64_t)b * H + h) * T + t0 + tt;
+    const float2 cs2 = *reinterpret_cast<const float2*>(feat + i * kFP);
+    float* g = gs + (tt * H + h) * GP + P;
+    g[0] = cs2.x;
+    g[1] = cs2.y;
+    g[2] = phase[i];
+  }
+  __syncthreads();
+  const float* pblk = proj + ((int64_t)b * T + t0) * H * P;
+  for (int pidx = threadIdx.x; pidx < npos; pidx += 256) {
+    const int h = pidx % H;
+    const float* g = gs + pidx * GP;
+    const float cn = g[P], sn = g[P + 1], phi = g[P + 2];
+    const float u = cn * g[1] - sn * g[0];
+    const float dphi = softplus_f(hraw[h]) * u;
+    const float r0 = pblk[(int64_t)pidx * P], s0 = pblk[(int64_t)pidx * P + 1];
+    const float mag_sq = r0 * r0 + s0 * s0;
+    float d_r = 0.f, d_s = 0.f;
+    if (fabsf(dphi) >= 1e-12f && mag_sq >= 1e-8f) {
+      const float m = fmaxf(mag_sq, 1e-12f);
+      d_r = dphi * (-s0 / m);
+      d_s = dphi * (r0 / m);
+    }
+    float* d = ds + pidx * P;
+    d[0] = d_r;
+    d[1] = d_s;
+    for (int j = 0; j < C; ++j) d[2 + j] = cs * g[2 + j];
+    hs[pidx] = phi * u;
+  }
+  __syncthreads();
+  float* dblk = dproj + ((int64_t)b * T + t0) * H * P;
+  for (int e = threadIdx.x; e < npos * P; e += 256) dblk[e] = ds[e];
+  if ((int)threadIdx.x < H) {
+    float acc = 0.f;
+    for (int tt = 0; tt < tn; ++tt) acc += hs[tt * H + threadIdx.x];
+    hpart[(int64_t)blockIdx.x * H + threadIdx.x] = acc;
+  }
 }
 
-// d_harmonic_raw[h] (+)= sigmoid(raw) * sum_{b,t} hpart[h][b*T + t]: one block
-// per head, fixed per-thread strides and a fixed tree, so the sum is
-// deterministic (attn.rs:372, :418).
+// d_harmonic_raw[h] (+)= sigmoid(raw) * sum over the feature-backward blocks of
+// hpart[block][h]: one block per head, fixed per-thread strides and a fixed
+// tree, so the sum is deterministic (attn.rs:372, :418).
 __global__ __launch_bounds__(256) void wave_harmonic_kernel(const float* __restrict__ hpart,
                                                             const float* __restrict__ hraw,
-                                                            float* __restrict__ d_hraw, int64_t n_per_head) {
+                                                            float* __restrict__ d_hraw, int nblk, int H) {
   __shared__ float red[256];
   const int h = blockIdx.x;
-  const float* src = hpart + (int64_t)h * n_per_head;
   float acc = 0.f;
-  for (int64_t j = threadIdx.x; j < n_per_head; j += 256) acc += src[j];
+  for (int j = threadIdx.x; j < nblk; j += 256) acc += hpart[(int64_t)j * H + h];
   red[threadIdx.x] = acc;
   __syncthreads();
   for (int w = 128; w > 0; w >>= 1) {
@@ -523,12 +588,31 @@ __global__ __launch_bounds__(256) void wave_probs_rows_kernel(const float* __res
 
 // ------------------------------------------------------------------ launchers
 
+namespace {
+// Positions per block of the feature kernels: the largest power of two up to 64
+// whose LDS staging fits in kFeatLds bytes.
+constexpr size_t kFeatLds = 40 * 1024;
+size_t feat_fwd_lds(int H, int TT) { return (size_t)H * TT * (kFP + 1 + 2) * sizeof(float); }
+size_t feat_bwd_lds(int H, int TT, int C) {
+  const int P = 2 + C;
+  return (size_t)H * TT * (((P + 3) | 1) + P + 1) * sizeof(float);
+}
+int feat_tile(int H, int T, size_t (*lds)(int, int, int), int C) {
+  int tt = 64;
+  while (tt > 1 && (lds(H, tt, C) > kFeatLds || tt >= 2 * T)) tt /= 2;
+  return tt;
+}
+size_t feat_fwd_lds3(int H, int TT, int) { return feat_fwd_lds(H, TT); }
+}  // namespace
+
 hipError_t launch_wave_features(const float* proj, const float* hraw, float* feat, float* phase, int* bucket,
                                 int B, int H, int T, int C, int C_used, hipStream_t stream) {
-  const int64_t n = (int64_t)B * H * T;
+  const int tt = feat_tile(H, T, feat_fwd_lds3, C);
+  if (feat_fwd_lds(H, tt) > kFeatLds) return hipErrorInvalidValue;  // more heads than one block stages
+  const int nblk = B * ((T + tt - 1) / tt);
   TimingScope ts("wave_feat", stream);
-  hipLaunchKernelGGL(wave_feat_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, proj, hraw, feat,
-                     phase, bucket, B, H, T, C, C_used);
+  hipLaunchKernelGGL(wave_feat_kernel, dim3((unsigned)nblk), dim3(256), feat_fwd_lds(H, tt), stream, proj, hraw,
+                     feat, phase, bucket, B, H, T, C, C_used, tt);
   return hipGetLastError();
 }
 
@@ -601,18 +685,20 @@ hipError_t launch_wave_bwd_core(const float* feat, const int* bucket, const floa
 hipError_t launch_wave_feat_bwd(const float* proj, const float* feat, const float* phase, const float* dfq,
                                 const float* dfk, const float* hraw, float* dproj, float* hpart, float* d_hraw,
                                 int B, int H, int T, int C, float cs, hipStream_t stream) {
-  const int64_t n = (int64_t)B * H * T;
+  const int tt = feat_tile(H, T, feat_bwd_lds, C);
+  if (feat_bwd_lds(H, tt, C) > kFeatLds) return hipErrorInvalidValue;  // more heads than one block stages
+  const int nblk = B * ((T + tt - 1) / tt);
   {
     TimingScope ts("wave_feat_bwd", stream);
-    hipLaunchKernelGGL(wave_feat_bwd_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, proj, feat,
-                       phase, dfq, dfk, hraw, dproj, hpart, B, H, T, C, cs);
+    hipLaunchKernelGGL(wave_feat_bwd_kernel, dim3((unsigned)nblk), dim3(256), feat_bwd_lds(H, tt, C), stream, proj,
+                       feat, phase, dfq, dfk, hraw, dproj, hpart, B, H, T, C, cs, tt);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (d_hraw == nullptr) return hipSuccess;
   TimingScope ts("wave_harmonic", stream);
   hipLaunchKernelGGL(wave_harmonic_kernel, dim3((unsigned)H), dim3(256), 0, stream, (const float*)hpart, hraw,
-                     d_hraw, (int64_t)B * T);
+                     d_hraw, nblk, H);
   return hipGetLastError();
 }
 

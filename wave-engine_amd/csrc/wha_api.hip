@@ -439,6 +439,8 @@ static int check_wave_shape(const wha_wave_shape* sh, const char* fn) {
   if (sh->content_dim < 0 || sh->content_dim > wha::kWaveFeatures - 2)
     return fail(WHA_ERR_UNSUPPORTED, "%s: content_dim must be in [0, %d] (got %d)", fn, wha::kWaveFeatures - 2,
                 sh->content_dim);
+  if (sh->n_head > 128)  // the feature kernels stage every head of a position block in LDS
+    return fail(WHA_ERR_UNSUPPORTED, "%s: n_head %d exceeds the supported maximum of 128", fn, sh->n_head);
   if ((int64_t)sh->B * sh->n_head * sh->T > ((int64_t)1 << 31) || (int64_t)sh->B * sh->T * sh->n_embd > ((int64_t)1 << 40))
     return fail(WHA_ERR_UNSUPPORTED, "%s: shape too large", fn);
   return WHA_OK;

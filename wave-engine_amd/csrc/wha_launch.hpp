@@ -119,7 +119,8 @@ hipError_t launch_wave_bwd_core(const float* feat, const int* bucket, const floa
 // Rows of the wave attention probabilities: out [B][H][rl.n][T].
 hipError_t launch_wave_probs_rows(const float* feat, const int* bucket, const float* lse, const RowList& rl,
                                   float* out, int B, int H, int T, float cs, hipStream_t stream);
-// Feature gradients -> dproj [B][T][H][2+C]; hpart [H][B*T] scratch; d_hraw [H] or nullptr.
+// Feature gradients -> dproj [B][T][H][2+C]; hpart: scratch of at least B*H*T floats (per-block
+// harmonic partials); d_hraw [H] or nullptr.
 hipError_t launch_wave_feat_bwd(const float* proj, const float* feat, const float* phase, const float* dfq,
                                 const float* dfk, const float* hraw, float* dproj, float* hpart, float* d_hraw,
                                 int B, int H, int T, int C, float cs, hipStream_t stream);
