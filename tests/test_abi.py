@@ -153,7 +153,7 @@ def test_wave_entry_points_validate_before_device_use(pkg):
     p = ctypes.c_void_p(1 << 20)
     sh, w, cache = _wave_structs(pkg)
     for bad, msg in ((dict(E=63), b"divisible"), (dict(C=31), b"content_dim"), (dict(E=258, H=1), b"128"),
-                     (dict(T=0), b"positive")):
+                     (dict(E=258, H=129), b"n_head"), (dict(T=0), b"positive")):
         s2, _, _ = _wave_structs(pkg, **bad)
         rc = L.wha_wave_fwd(p, ctypes.byref(w), ctypes.byref(s2), p, ctypes.byref(cache), None)
         assert rc in (WHA_ERR_INVALID, WHA_ERR_UNSUPPORTED) and msg in L.wha_last_error(), L.wha_last_error()
