@@ -40,26 +40,63 @@ enum DqMode { kFused = 0, kProbs = 1, kDeltaFromProbs = 2 };
 
 
 // Delta_t = sum_d dO[t][d] * O[t][d]; 16 lanes per row, 16 rows per block.
+// Delta[r] = sum_d dO[r][d] O[r][d]: 16 lanes per row, each 16-lane group
+// kDeltaRows rows (all loads issued before the sums).  VEC: 128-bit loads
+// (D, the strides and both bases 16-byte aligned, checked on the host).
+constexpr int kDeltaRows = 4;
+template <bool VEC>
 __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const float* __restrict__ O,
                                                              const float* __restrict__ dO,
                                                              float* __restrict__ Delta, View L) {
   const int64_t rows = (int64_t)L.B * L.H * L.T;
-  const int64_t r = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int64_t rbase = ((int64_t)blockIdx.x * 16 + (threadIdx.x >> 4)) * kDeltaRows;
   const int sub = threadIdx.x & 15;
-  float acc = 0.f;
-  if (r < rows) {
+  float acc[kDeltaRows];
+#pragma unroll
+  for (int j = 0; j < kDeltaRows; ++j) {
+    acc[j] = 0.f;
+    const int64_t r = rbase + j;
+    if (r >= rows) continue;
     const int t = (int)(r % L.T);
     const int64_t bh = r / L.T;
     const int b = (int)(bh / L.H), h = (int)(bh % L.H);
     const int64_t off = (int64_t)b * L.sb + (int64_t)h * L.sh + (int64_t)t * L.st;
-    for (int d = sub; d < L.D; d += 16) acc += dO[off + d] * O[off + d];
+    if (VEC) {
+      for (int d = 4 * sub; d < L.D; d += 64) {
+        const float4 x = *reinterpret_cast<const float4*>(dO + off + d);
+        const float4 y = *reinterpret_cast<const float4*>(O + off + d);
+        acc[j] += x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
+      }
+    } else {
+      for (int d = sub; d < L.D; d += 16) acc[j] += dO[off + d] * O[off + d];
+    }
   }
-  acc += __shfl_xor(acc, 8, 16);
-  acc += __shfl_xor(acc, 4, 16);
-  acc += __shfl_xor(acc, 2, 16);
-  acc += __shfl_xor(acc, 1, 16);
-  if (r < rows && sub == 0) Delta[r] = acc;
+#pragma unroll
+  for (int j = 0; j < kDeltaRows; ++j) {
+    float a = acc[j];
+    a += __shfl_xor(a, 8, 16);
+    a += __shfl_xor(a, 4, 16);
+    a += __shfl_xor(a, 2, 16);
+    a += __shfl_xor(a, 1, 16);
+    if (rbase + j < rows && sub == 0) Delta[rbase + j] = a;
+  }
 }
+
+namespace {
+bool delta_vec(const float* o, const float* d_o, const View& L) {
+  return ((reinterpret_cast<uintptr_t>(o) | reinterpret_cast<uintptr_t>(d_o)) & 15) == 0 && L.D % 4 == 0 &&
+         L.st % 4 == 0 && L.sh % 4 == 0 && L.sb % 4 == 0;
+}
+hipError_t delta_launch(const float* o, const float* d_o, float* delta, const View& L, hipStream_t stream) {
+  const int64_t rows = (int64_t)L.B * L.H * L.T;
+  const dim3 grid((unsigned)((rows + 16 * kDeltaRows - 1) / (16 * kDeltaRows)));
+  if (delta_vec(o, d_o, L))
+    hipLaunchKernelGGL(attn_bwd_delta_kernel<true>, grid, dim3(256), 0, stream, o, d_o, delta, L);
+  else
+    hipLaunchKernelGGL(attn_bwd_delta_kernel<false>, grid, dim3(256), 0, stream, o, d_o, delta, L);
+  return hipGetLastError();
+}
+}  // namespace
 
 // Query-stationary kernel: dQ (modes kFused, kProbs) or Delta (kDeltaFromProbs).
 template <int DP, int NW, bool VEC, int MODE>
@@ -462,15 +499,13 @@ hipError_t bwd_fused_t(const float* q, const float* k, const float* v, const flo
                        float* delta, float* ds, const View& L, float scale, hipStream_t stream) {
   constexpr int NWQ = 4, NWK = 4;
   const float sl2 = (float)((double)scale * 1.4426950408889634);
-  const int64_t rows = (int64_t)L.B * L.H * L.T;
   const int n_qt = (L.T + NWQ * 16 - 1) / (NWQ * 16);
   const int n_kt = (L.T + NWK * 16 - 1) / (NWK * 16);
+  hipError_t e;
   {
     TimingScope ts("attn_bwd_delta", stream);
-    hipLaunchKernelGGL(attn_bwd_delta_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, stream,
-                       o, d_o, delta, L);
+    e = delta_launch(o, d_o, delta, L, stream);
   }
-  hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (ds != nullptr) {
     {
@@ -543,11 +578,8 @@ size_t bwd_ds_floats(const View& L) { return (size_t)L.B * L.H * (size_t)ds_rows
 
 hipError_t launch_attn_bwd_delta(const float* o, const float* d_o, float* delta, const View& L, const char* name,
                                  hipStream_t stream) {
-  const int64_t rows = (int64_t)L.B * L.H * L.T;
   TimingScope ts(name, stream);
-  hipLaunchKernelGGL(attn_bwd_delta_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, stream, o, d_o,
-                     delta, L);
-  return hipGetLastError();
+  return delta_launch(o, d_o, delta, L, stream);
 }
 
 hipError_t launch_dq_from_ds(const float* k, const float* ds, float* dq, const View& L, float scale,
