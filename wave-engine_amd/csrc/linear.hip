@@ -396,21 +396,68 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 }
 
 // C[bt][m][n] (+)= bias[bt][n] + sum_s part[bt*splits + s][m][n], s in increasing order.
+// W consecutive n per thread (W = 4 when N % 4 == 0: 128-bit loads); the
+// partials are loaded eight splits at a time, then added in split order.
+template <int W>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part, GemmArgs g) {
   const int64_t MN = (int64_t)g.M * g.N;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * W;
   if (i >= MN * g.batch) return;
   const int bt = (int)(i / MN);
   const int64_t e = i - bt * MN;
   const int m = (int)(e / g.N), n = (int)(e % g.N);
-  float s = 0.f;
-  for (int z = 0; z < g.splits; ++z) s += part[((int64_t)bt * g.splits + z) * MN + e];
+  const float* src = part + (int64_t)bt * g.splits * MN + e;
+  float s[W];
+#pragma unroll
+  for (int w = 0; w < W; ++w) s[w] = 0.f;
+  for (int z0 = 0; z0 < g.splits; z0 += 8) {
+    float v[8][W];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const bool in = z0 + u < g.splits;
+      const float* p = src + (int64_t)(in ? z0 + u : 0) * MN;
+      if (W == 4) {
+        const float4 x = *reinterpret_cast<const float4*>(p);
+        v[u][0] = x.x;
+        v[u][1 % W] = x.y;
+        v[u][2 % W] = x.z;
+        v[u][3 % W] = x.w;
+      } else {
+        v[u][0] = p[0];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (z0 + u < g.splits) {
+#pragma unroll
+        for (int w = 0; w < W; ++w) s[w] += v[u][w];
+      }
+    }
+  }
   float* dst = g.c + bt * g.c_sb + (int64_t)m * g.ldc + n;
-  const float r = (g.bias != nullptr ? g.bias[bt * g.bias_sb + n] : 0.f) + s;
-  *dst = g.accumulate ? *dst + r : r;
+  float r[W];
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    r[w] = (g.bias != nullptr ? g.bias[bt * g.bias_sb + n + w] : 0.f) + s[w];
+    if (g.accumulate) r[w] = dst[w] + r[w];
+  }
+  if (W == 4 && g.c_vec) {
+    *reinterpret_cast<float4*>(dst) = make_float4(r[0], r[1 % W], r[2 % W], r[3 % W]);
+  } else {
+#pragma unroll
+    for (int w = 0; w < W; ++w) dst[w] = r[w];
+  }
   if (n == 0 && g.rowsum != nullptr) {
+    const float* rp = g.rowsum_part + (int64_t)bt * g.splits * g.M + m;
     float t = 0.f;
-    for (int z = 0; z < g.splits; ++z) t += g.rowsum_part[((int64_t)bt * g.splits + z) * g.M + m];
+    for (int z0 = 0; z0 < g.splits; z0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = rp[(int64_t)(z0 + u < g.splits ? z0 + u : 0) * g.M];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (z0 + u < g.splits) t += v[u];
+    }
     g.rowsum[bt * g.rowsum_sb + m] = t;
   }
 }
@@ -457,8 +504,12 @@ hipError_t gemm_launch(GemmArgs g, float* ws, int splits, const char* name, hipS
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t total = (int64_t)g.M * g.N * g.batch;
-  hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
-                     (const float*)ws, g);
+  if (g.N % 4 == 0)
+    hipLaunchKernelGGL(gemm_splitk_reduce_kernel<4>, dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0,
+                       stream, (const float*)ws, g);
+  else
+    hipLaunchKernelGGL(gemm_splitk_reduce_kernel<1>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                       (const float*)ws, g);
   return hipGetLastError();
 }
 
