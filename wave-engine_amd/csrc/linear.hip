@@ -464,21 +464,25 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
 
 namespace {
 
-// Tile width: 64 columns for N <= 64, else 128.
-int gemm_bn(int N) { return N <= 64 ? 64 : kGBN; }
-
-// Tile height: 128 rows unless that leaves fewer than two blocks per CU.
+// Output tile: the largest of 128 x 128, 64 x 128 that gives at least two
+// blocks per CU; 64-column tiles when N <= 64, and for N <= 256 when 64 x 128
+// tiles would leave CUs without a second block (same padding, twice the blocks).
 constexpr int kCUs = 256;
-int gemm_bm(int M, int N, int batch) {
-  const int bn = gemm_bn(N);
-  const int tiles128 = ((M + 127) / 128) * ((N + bn - 1) / bn) * batch;
-  return tiles128 >= 2 * kCUs ? 128 : 64;
+struct GemmTile {
+  int bm, bn;
+};
+GemmTile gemm_tile(int M, int N, int batch) {
+  auto blocks = [&](int bm, int bn) { return (int64_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
+  if (N <= 64) return {blocks(128, 64) >= 2 * kCUs ? 128 : 64, 64};
+  if (blocks(128, kGBN) >= 2 * kCUs) return {128, kGBN};
+  if (blocks(64, kGBN) >= 2 * kCUs || N > 256) return {64, kGBN};
+  return {64, 64};
 }
 
 // Split-K factor: aim for >= 512 blocks while keeping >= min_k k per split.
 int gemm_splits(int M, int N, int K, int batch, int min_k = 256) {
-  const int bm = gemm_bm(M, N, batch), bn = gemm_bn(N);
-  const int tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch;
+  const GemmTile t = gemm_tile(M, N, batch);
+  const int tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) * batch;
   int splits = 1;
   while (tiles * splits < 512 && (K / (splits * 2)) >= min_k) splits *= 2;
   return splits;
@@ -521,8 +525,9 @@ hipError_t gemm_t(GemmArgs g, float* ws, const char* name, hipStream_t stream, i
   // 128-bit loads need every row start along the contiguous direction 16-byte aligned
   g.a_vec = aligned16(g.a) && g.a_sb % 4 == 0 && (A_KC ? g.a_sm % 4 == 0 : g.a_sk % 4 == 0);
   g.b_vec = aligned16(g.b) && g.b_sb % 4 == 0 && (B_KC ? g.b_sn % 4 == 0 : g.b_sk % 4 == 0);
-  const bool bm128 = gemm_bm(g.M, g.N, g.batch) == 128;
-  if (gemm_bn(g.N) == 64)
+  const GemmTile t = gemm_tile(g.M, g.N, g.batch);
+  const bool bm128 = t.bm == 128;
+  if (t.bn == 64)
     return bm128 ? gemm_launch<128, WHA_GEMM_KT, 1, A_KC, B_KC>(g, ws, splits, name, stream)
                  : gemm_launch<64, WHA_GEMM_KT, 1, A_KC, B_KC>(g, ws, splits, name, stream);
   return bm128 ? gemm_launch<128, WHA_GEMM_KT, 2, A_KC, B_KC>(g, ws, splits, name, stream)
