@@ -21,6 +21,7 @@ projections (ComputeBackend::attention) forward and backward.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -44,6 +45,8 @@ CONFIGS = {
     "wavedecode": dict(name="768-dim wave-attention KV-cache decode (serve tier), 64 sequences x 8192 cached",
                        B=64, H=12, T=8192, D=64, C=16),
     "layer": dict(name="768-dim ComputeBackend::attention layer (c_attn, causal core, c_proj), fwd+bwd",
+                  B=8, H=12, T=1024, D=64),
+    "probs": dict(name="768-dim core, backward from the given att (the exact attention_backward contract)",
                   B=8, H=12, T=1024, D=64),
 }
 
@@ -217,6 +220,72 @@ def run_decode(args, cfg, pkg, torch):
             "kernel_ms": {"decode_split": ms_split / n, "decode_merge": ms_merge / n},
             "roofline": {"kernel": "decode_split", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic("decode_split", cfg)}}
+
+
+def run_probs(args, cfg, pkg, torch):
+    """Fused forward plus the exact-contract backward (wha_attn_bwd_from_probs:
+    att [B,H,T,T] read as given, never recomputed).  att is built once, outside
+    the timed region, from the forward's LSE (wha_attn_probs_rows, 256 rows per
+    call).  The backward's Delta and dK/dV passes each stream the causal half
+    of att (4 B per causal pair); dK/dV also writes the dS tiles, which the dQ
+    pass reads back.  The roofline is reported against HBM with algorithmic
+    bytes per launch = those streams plus the [T][D] operands each kernel reads
+    and writes."""
+    B, H, T, D = cfg["B"], cfg["H"], cfg["T"], cfg["D"]
+    dev = torch.device("cuda:0")
+    q, k, v, do = (torch.from_numpy(a).to(dev) for a in pkg.synth_inputs(B, H, T, D, seed=42))
+    o, lse = pkg.attn_fwd(q, k, v)
+    att = torch.cat([pkg.attn_probs_rows(q, k, lse, range(r, min(T, r + 256))) for r in range(0, T, 256)], dim=2)
+    att = att.contiguous()
+    ws = torch.empty(int(pkg.lib().wha_attn_bwd_from_probs_workspace_size(ctypes.byref(pkg.layout_of(q)))) // 4 + 64,
+                     device=dev)
+    lse_o = torch.empty_like(lse)
+
+    def step():
+        pkg.attn_fwd(q, k, v, out=o, lse=lse_o)
+        pkg.attn_bwd_from_probs(do, q, k, v, att, workspace=ws)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    names = ("attn_fwd", "attn_bwd_probs_delta", "attn_bwd_probs_dq", "attn_bwd_probs_dkv")
+    pkg.timing_reset()
+    pkg.timing_enable(True)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    pkg.timing_enable(False)
+    kern = {n: pkg.timing_read(n) for n in names}
+    pkg.timing_reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    avg = {n: kern[n][0] / max(kern[n][1], 1) for n in names}
+    P = B * H * (T * (T + 1) // 2)
+    rows = B * H * T * D * 4
+    nkt = (T + 63) // 64
+    ds = B * H * (nkt * 64 * nkt - 32 * nkt * (nkt - 1)) * 64 * 4     # dS tiles: causal 64-key column blocks
+    alg = {"attn_bwd_probs_delta": 4 * P + 2 * rows + B * H * T * 4,      # att, V, dO; Delta out
+           "attn_bwd_probs_dkv": 4 * P + 5 * rows + B * H * T * 4 + ds,   # att, Q, V, dO, Delta; dK, dV, dS out
+           "attn_bwd_probs_dq": ds + 2 * rows}                            # dS, K; dQ out
+    dom = max(alg, key=lambda n: avg[n])
+    achieved = alg[dom] / (avg[dom] * 1e-3) / 1e9
+    flops = credited_flops(B, H, T, D)["total"]
+    return {"metric": "causal attn fwd + exact-contract bwd (att given) tokens/s, 768-dim seq1024",
+            "value": B * T / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded xorshift64 + Box-Muller, seed 42)",
+            "config": {"workload": cfg["name"], "batch": B, "heads": H, "seq_len": T, "head_dim": D,
+                       "parallelism": "none (1 GPU)"},
+            "tflops": flops / (ms * 1e-3) / 1e12,
+            "kernel_ms": {n: round(avg[n], 5) for n in names},
+            "bwd_ms": sum(avg[n] for n in names[1:]),
+            "roofline": {"kernel": dom, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes_per_launch": alg[dom],
+                         "avg_launch_ms": avg[dom]}}
 
 
 def wave_credited_flops(B, H, T, D, C):
@@ -593,9 +662,11 @@ def main():
         res = run_wave_decode(args, cfg, pkg, torch)
     elif args.config == "layer":
         res = run_layer(args, cfg, pkg, torch)
+    elif args.config == "probs":
+        res = run_probs(args, cfg, pkg, torch)
     else:
         res = run_attention(args, cfg, pkg, torch)
-    if args.config in ("decode", "wavedecode"):
+    if args.config in ("decode", "wavedecode", "probs"):
         res["cpu_baseline"] = None
     elif not args.no_cpu_baseline:
         res["cpu_baseline"] = (wave_cpu_baseline(cfg) if args.config == "wave" else

@@ -92,7 +92,8 @@ int wha_attn_bwd(const float* q, const float* k, const float* v,
 size_t wha_attn_bwd_from_probs_workspace_size(const wha_layout* layout);
 
 /* Backward with the reference's exact contract: att [B][H][T][T] (post-softmax
- * rows, att[b][h][t][j] read only for j <= t) is used as given and never
+ * rows; entries j > t never reach the result and may hold anything, NaN
+ * included) is used as given and never
  * recomputed, exactly as ComputeBackend::attention_backward
  * (src/common/compute.rs:163-173, :286-314) and attention_backward_single
  * (src/cpu/backward.rs:313-363) use it.  d_pre_proj is the gradient flowing

@@ -99,7 +99,12 @@ hipError_t delta_launch(const float* o, const float* d_o, float* delta, const Vi
 }  // namespace
 
 // Query-stationary kernel: dQ (modes kFused, kProbs) or Delta (kDeltaFromProbs).
-template <int DP, int NW, bool VEC, int MODE>
+// In the two att modes each lane's 16 probabilities of a key tile (keys
+// key0+16mt+4g+0..3 of its query row) are loaded one tile ahead, as 128-bit
+// loads when AV (T % 4 == 0 and att 16-byte aligned, checked on the host);
+// columns are clamped into the row and masked entries are selected away, so
+// the loads need no branch and never leave att.
+template <int DP, int NW, bool VEC, int MODE, bool AV = false>
 __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ LSE, float* __restrict__ Delta,
@@ -144,6 +149,26 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
   TileStage<DP, BN, NT, VEC> ks, vs;
   if (kNeedK) ks.load(K + base, 0, L.T, L.D, L.st, tid);
   vs.load(V + base, 0, L.T, L.D, L.st, tid);
+  constexpr int NA = MODE != kFused ? NKT * 4 : 1;
+  float acur[NA], anext[NA];
+  auto load_att = [&](int kt) {
+    if (MODE == kFused) return;
+#pragma unroll
+    for (int mt = 0; mt < NKT; ++mt) {
+      const int c0 = kt * BN + 16 * mt + 4 * g;
+      if (AV) {
+        const float4 x = *reinterpret_cast<const float4*>(att_row + min(c0, L.T - 4));
+        anext[4 * mt + 0] = x.x;
+        anext[4 * mt + 1] = x.y;
+        anext[4 * mt + 2] = x.z;
+        anext[4 * mt + 3] = x.w;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) anext[4 * mt + i] = att_row[min(c0 + i, L.T - 1)];
+      }
+    }
+  };
+  load_att(0);
 
   floatx4 dqacc[NDT];
 #pragma unroll
@@ -154,10 +179,15 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
     __syncthreads();
     if (kNeedK) ks.template store<LD>(Ks, tid);
     vs.template store<LD>(Vs, tid);
+    if (MODE != kFused) {
+#pragma unroll
+      for (int a = 0; a < NA; ++a) acur[a] = anext[a];
+    }
     __syncthreads();
     if (kt + 1 < n_kt) {
       if (kNeedK) ks.load(K + base, (kt + 1) * BN, L.T, L.D, L.st, tid);
       vs.load(V + base, (kt + 1) * BN, L.T, L.D, L.st, tid);
+      load_att(kt + 1);
     }
     const int key0 = kt * BN;
     if (key0 > q0 + 15) continue;
@@ -194,14 +224,13 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
     for (int mt = 0; mt < NKT; ++mt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int key = key0 + 16 * mt + 4 * g + i;
         const bool valid = 16 * mt + 4 * g + i <= key_lim;
         float p;
         if (MODE == kFused) {
           p = fast_exp2(s[mt][i] - lse2);
           p = valid ? p : 0.f;
         } else {
-          p = valid ? att_row[key] : 0.f;
+          p = valid ? acur[4 * mt + i] : 0.f;
         }
         if (MODE == kDeltaFromProbs) {
           dsum += p * dp[mt][i];
@@ -285,9 +314,23 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
 
   TileStage<DP, BMQ, NT, VEC> qs, os;
   float lse_r = 0.f, del_r = 0.f;
+  // PROBS: this lane's 16 entries att[q][krow] of the next query tile
+  // (q = qt*BMQ + 16mt + 4g + i), loaded with the tile; row and column are
+  // clamped into att and masked entries are selected away after the MFMAs
+  constexpr int NA = PROBS ? NQT * 4 : 1;
+  float acur[NA], anext[NA];
+  const float* att_col = PROBS ? ATT + rbase * L.T + min(krow, L.T - 1) : nullptr;
   auto load_tile = [&](int qt) {
     qs.load(Q + base, qt * BMQ, L.T, L.D, L.st, tid);
     os.load(dO + base, qt * BMQ, L.T, L.D, L.st, tid);
+    if (PROBS) {
+#pragma unroll
+      for (int mt = 0; mt < NQT; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          anext[4 * mt + i] = att_col[(int64_t)min(qt * BMQ + 16 * mt + 4 * g + i, L.T - 1) * L.T];
+      }
+    }
     // raw LSE (scaled when stored to LDS): arithmetic on a value here would wait
     // for its load and, with it, for the tile loads issued just before
     if (tid < BMQ) {
@@ -305,6 +348,10 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
     if (tid < BMQ) {
       lse_s[tid] = lse_r * kLog2e;
       del_s[tid] = del_r;
+    }
+    if (PROBS) {
+#pragma unroll
+      for (int a = 0; a < NA; ++a) acur[a] = anext[a];
     }
     __syncthreads();
     if (qt + 1 < n_qt) load_tile(qt + 1);
@@ -359,7 +406,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
           p = fast_exp2(s[mt][i] - lq4[i]);
           p = valid ? p : 0.f;
         } else {
-          p = valid ? ATT[(rbase + q) * L.T + krow] : 0.f;
+          p = valid ? acur[4 * mt + i] : 0.f;
         }
         s[mt][i] = p;
         dp[mt][i] = p * (dp[mt][i] - dq4[i]);
@@ -540,24 +587,41 @@ hipError_t bwd_fused_t(const float* q, const float* k, const float* v, const flo
   return hipGetLastError();
 }
 
-template <int DP, bool VEC>
+template <int DP, bool VEC, bool AV>
 hipError_t bwd_probs_t(const float* d_o, const float* q, const float* k, const float* v,
-                       const float* att, float* dq, float* dk, float* dv, float* delta,
+                       const float* att, float* dq, float* dk, float* dv, float* delta, float* ds,
                        const View& L, float scale, hipStream_t stream) {
   constexpr int NWQ = 4, NWK = 4;
   const int n_qt = (L.T + NWQ * 16 - 1) / (NWQ * 16);
   const int n_kt = (L.T + NWK * 16 - 1) / (NWK * 16);
   {
     TimingScope ts("attn_bwd_probs_delta", stream);
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<DP, NWQ, VEC, kDeltaFromProbs>),
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<DP, NWQ, VEC, kDeltaFromProbs, AV>),
                        dim3((unsigned)(n_qt * L.B * L.H)), dim3(NWQ * 64), 0, stream, q, k, v, d_o,
                        (const float*)nullptr, delta, att, (float*)nullptr, L, scale, 0.f);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (ds != nullptr) {
+    // dK, dV and the dS tiles in one key-stationary pass; dQ = scale * dS K from them
+    {
+      TimingScope ts("attn_bwd_probs_dkv", stream);
+      hipLaunchKernelGGL((attn_bwd_dkv_kernel<DP, NWK, VEC, true, true>), dim3((unsigned)(n_kt * L.B * L.H)),
+                         dim3(NWK * 64), 0, stream, q, k, v, d_o, (const float*)nullptr,
+                         (const float*)delta, att, dk, dv, ds, L, scale, 0.f);
+    }
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    TimingScope ts("attn_bwd_probs_dq", stream);
+    constexpr int NWD = WHA_DQ_NW;
+    const int n_qt_d = (L.T + NWD * 16 - 1) / (NWD * 16);
+    hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<DP, NWD, VEC>), dim3((unsigned)(n_qt_d * L.B * L.H)),
+                       dim3(NWD * 64), 0, stream, k, (const float*)ds, dq, L, scale);
+    return hipGetLastError();
+  }
   {
     TimingScope ts("attn_bwd_probs_dq", stream);
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<DP, NWQ, VEC, kProbs>), dim3((unsigned)(n_qt * L.B * L.H)),
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<DP, NWQ, VEC, kProbs, AV>), dim3((unsigned)(n_qt * L.B * L.H)),
                        dim3(NWQ * 64), 0, stream, q, k, v, d_o, (const float*)nullptr, delta, att, dq, L,
                        scale, 0.f);
   }
@@ -612,10 +676,14 @@ hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const
 
 hipError_t launch_attn_bwd_probs(const float* d_o, const float* q, const float* k, const float* v,
                                  const float* att, float* dq, float* dk, float* dv, float* delta,
-                                 const View& L, bool vec, float scale, hipStream_t stream) {
-#define WHA_BWDP(DP)                                                                            \
-  return vec ? bwd_probs_t<DP, true>(d_o, q, k, v, att, dq, dk, dv, delta, L, scale, stream) \
-             : bwd_probs_t<DP, false>(d_o, q, k, v, att, dq, dk, dv, delta, L, scale, stream)
+                                 float* ds, const View& L, bool vec, float scale, hipStream_t stream) {
+  // 128-bit att loads need every row start 16-byte aligned (the non-VEC build
+  // keeps scalar loads: it only serves unaligned operands)
+  const bool av = vec && L.T % 4 == 0 && (reinterpret_cast<uintptr_t>(att) & 15) == 0;
+#define WHA_BWDP(DP)                                                                                           \
+  return !vec ? bwd_probs_t<DP, false, false>(d_o, q, k, v, att, dq, dk, dv, delta, ds, L, scale, stream)    \
+         : av ? bwd_probs_t<DP, true, true>(d_o, q, k, v, att, dq, dk, dv, delta, ds, L, scale, stream)      \
+              : bwd_probs_t<DP, true, false>(d_o, q, k, v, att, dq, dk, dv, delta, ds, L, scale, stream)
   switch (padded_dim(L.D)) {
     case 48: WHA_BWDP(48);
     case 64: WHA_BWDP(64);

@@ -47,10 +47,12 @@ hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const
                            float* delta, float* ds, const View& L, bool vec, float scale,
                            hipStream_t stream);
 
-// Backward from given probabilities att [B][H][T][T].  delta: [B*H*T] scratch.
+// Backward from given probabilities att [B][H][T][T].  delta: [B*H*T] scratch;
+// ds: bwd_ds_floats(L) scratch for the dS tiles, or nullptr to recompute dP in
+// a query-stationary dQ pass instead.
 hipError_t launch_attn_bwd_probs(const float* d_o, const float* q, const float* k, const float* v,
                                  const float* att, float* dq, float* dk, float* dv, float* delta,
-                                 const View& L, bool vec, float scale, hipStream_t stream);
+                                 float* ds, const View& L, bool vec, float scale, hipStream_t stream);
 
 // Split-K decode.  Workspace layout and size: decode_workspace_floats().
 size_t decode_workspace_floats(const View& cache);
