@@ -97,7 +97,9 @@ size_t wha_attn_bwd_from_probs_workspace_size(const wha_layout* layout);
  * recomputed, exactly as ComputeBackend::attention_backward
  * (src/common/compute.rs:163-173, :286-314) and attention_backward_single
  * (src/cpu/backward.rs:313-363) use it.  d_pre_proj is the gradient flowing
- * into the pre-c_proj attention output.  Bandwidth-bound on att. */
+ * into the pre-c_proj attention output.  Workspace: Delta plus the dS tiles
+ * (as wha_attn_bwd); the causal half of att is streamed twice (the Delta pass
+ * and the dK/dV pass). */
 int wha_attn_bwd_from_probs(const float* d_pre_proj, const float* q,
                             const float* k, const float* v, const float* att,
                             float* dq, float* dk, float* dv, void* workspace,
