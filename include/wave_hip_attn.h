@@ -45,7 +45,8 @@ extern "C" {
  *   device layout [B,H,T,D] contiguous: stride_b=H*T*D, stride_h=T*D, stride_t=D
  *   reference per-sequence layout [T][H*D] (src/common/compute.rs:370-374,
  *   :384-386) batched as [B][T][H*D]: stride_b=T*H*D, stride_h=D, stride_t=H*D
- * lse and the backward workspace are always [B][H][T] contiguous. */
+ * lse is always [B][H][T] contiguous; workspaces are opaque scratch whose
+ * size the matching *_workspace_size function reports. */
 typedef struct wha_layout {
   int32_t B, H, T, D;
   int64_t stride_b, stride_h, stride_t;
@@ -69,7 +70,10 @@ int wha_attn_fwd(const float* q, const float* k, const float* v, float* o,
                  float* lse, const wha_layout* layout, float scale,
                  void* stream);
 
-/* Bytes of device workspace wha_attn_bwd needs for this layout. */
+/* Bytes of device workspace wha_attn_bwd needs for this layout: per-row
+ * statistics (Delta_t = dO_t . O_t, and for head dim 64 the scaled LSE beside
+ * it, in 32-row blocks) plus the causal half of dS in 64-key column blocks,
+ * which the key-stationary pass writes and the dQ pass reads. */
 size_t wha_attn_bwd_workspace_size(const wha_layout* layout);
 
 /* Fused causal backward from the forward's o and lse: recomputes P on chip and

@@ -32,6 +32,8 @@
 // key-stationary kernel a wave keeps its 16 keys in registers and forms S/dP
 // with queries on rows and its keys on columns, so P and dS are directly the B
 // operands of dV^T += dO^T P and dK^T += Q^T dS.
+#include <type_traits>
+
 #include "wha_launch.hpp"
 
 namespace wha {
@@ -82,6 +84,56 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const float* __rest
   }
 }
 
+// Row statistics for attn_bwd_dkv_dma_kernel, per (b,h) in blocks of 32 rows
+// (Tb = T rounded up to 32): block j holds -LSE_t*log2(e) for t = 32j..32j+31,
+// then -Delta_t for the same rows (rows past T hold 0).  The key-stationary
+// kernel fetches a block with one 256-byte load and starts its S and dP
+// accumulators from it, so p = exp2(acc) and dS = p * acc need no further
+// arithmetic.  Same 16-lanes-per-row dot product as attn_bwd_delta_kernel.
+__global__ __launch_bounds__(256) void attn_bwd_stats_kernel(const float* __restrict__ O,
+                                                             const float* __restrict__ dO,
+                                                             const float* __restrict__ LSE,
+                                                             float* __restrict__ stats, View L) {
+  const int Tb = (L.T + 31) / 32 * 32;
+  const int64_t rows = (int64_t)L.B * L.H * Tb;
+  const int64_t rbase = ((int64_t)blockIdx.x * 16 + (threadIdx.x >> 4)) * kDeltaRows;
+  const int sub = threadIdx.x & 15;
+  float acc[kDeltaRows];
+#pragma unroll
+  for (int j = 0; j < kDeltaRows; ++j) {
+    acc[j] = 0.f;
+    const int64_t r = rbase + j;
+    const int t = (int)(r % Tb);
+    if (r >= rows || t >= L.T) continue;
+    const int64_t bh = r / Tb;
+    const int b = (int)(bh / L.H), h = (int)(bh % L.H);
+    const int64_t off = (int64_t)b * L.sb + (int64_t)h * L.sh + (int64_t)t * L.st;
+    for (int d = 4 * sub; d < L.D; d += 64) {
+      const float4 x = *reinterpret_cast<const float4*>(dO + off + d);
+      const float4 y = *reinterpret_cast<const float4*>(O + off + d);
+      acc[j] += x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kDeltaRows; ++j) {
+    float a = acc[j];
+    a += __shfl_xor(a, 8, 16);
+    a += __shfl_xor(a, 4, 16);
+    a += __shfl_xor(a, 2, 16);
+    a += __shfl_xor(a, 1, 16);
+    const int64_t r = rbase + j;
+    if (r < rows && sub == 0) {
+      const int t = (int)(r % Tb);
+      const int64_t bh = r / Tb;
+      float* blk = stats + (bh * (Tb / 32) + t / 32) * 64 + (t % 32);
+      blk[0] = t < L.T ? -LSE[bh * L.T + t] * kLog2e : 0.f;
+      blk[32] = t < L.T ? -a : 0.f;
+    }
+  }
+}
+
+size_t bwd_stats_floats(const View& L) { return (size_t)L.B * L.H * ((L.T + 31) / 32 * 32) * 2; }
+
 namespace {
 bool delta_vec(const float* o, const float* d_o, const View& L) {
   return ((reinterpret_cast<uintptr_t>(o) | reinterpret_cast<uintptr_t>(d_o)) & 15) == 0 && L.D % 4 == 0 &&
@@ -112,7 +164,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
   constexpr int NT = NW * 64;
   constexpr int BM = NW * 16;
   constexpr int BN = 64;
-  constexpr int LD = DP + WHA_LDS_PAD;
+  constexpr int LD = Lds<DP>::PITCH;
   constexpr int DG = DP / 4;
   constexpr int NDT = DP / 16;
   constexpr int NKT = BN / 16;
@@ -177,8 +229,8 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
 
   for (int kt = 0; kt < n_kt; ++kt) {
     __syncthreads();
-    if (kNeedK) ks.template store<LD>(Ks, tid);
-    vs.template store<LD>(Vs, tid);
+    if (kNeedK) ks.store_tile(Ks, tid);
+    vs.store_tile(Vs, tid);
     if (MODE != kFused) {
 #pragma unroll
       for (int a = 0; a < NA; ++a) acur[a] = anext[a];
@@ -203,13 +255,13 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
 #pragma unroll
       for (int mt = 0; mt < NKT; ++mt) {
         if (MODE == kFused) {
-          const float4 a = *reinterpret_cast<const float4*>(&Ks[(16 * mt + lq) * LD + g * DG + 4 * j]);
+          const float4 a = lds_read_quad<DP>(Ks, 16 * mt + lq, g * (DG / 4) + j);
           s[mt] = mfma4(a.x, qf[4 * j + 0], s[mt]);
           s[mt] = mfma4(a.y, qf[4 * j + 1], s[mt]);
           s[mt] = mfma4(a.z, qf[4 * j + 2], s[mt]);
           s[mt] = mfma4(a.w, qf[4 * j + 3], s[mt]);
         }
-        const float4 c = *reinterpret_cast<const float4*>(&Vs[(16 * mt + lq) * LD + g * DG + 4 * j]);
+        const float4 c = lds_read_quad<DP>(Vs, 16 * mt + lq, g * (DG / 4) + j);
         dp[mt] = mfma4(c.x, of[4 * j + 0], dp[mt]);
         dp[mt] = mfma4(c.y, of[4 * j + 1], dp[mt]);
         dp[mt] = mfma4(c.z, of[4 * j + 2], dp[mt]);
@@ -247,7 +299,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float ka[NDT];
-          lds_read_vec<NDT>(&Ks[(16 * mt + 4 * g + i) * LD + NDT * lq], ka);
+          lds_read_seg<DP, NDT>(Ks, 16 * mt + 4 * g + i, lq, ka);
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt) dqacc[dt] = mfma4(ka[dt], dp[mt][i], dqacc[dt]);
         }
@@ -274,7 +326,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
   constexpr int NT = NW * 64;
   constexpr int BNK = NW * 16;  // keys per block
   constexpr int BMQ = 64;       // queries per tile
-  constexpr int LD = DP + WHA_LDS_PAD;
+  constexpr int LD = Lds<DP>::PITCH;
   constexpr int DG = DP / 4;
   constexpr int NDT = DP / 16;
   constexpr int NQT = BMQ / 16;
@@ -343,8 +395,8 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
 
   for (int qt = qt0; qt < n_qt; ++qt) {
     __syncthreads();
-    qs.template store<LD>(Qs, tid);
-    os.template store<LD>(Os, tid);
+    qs.store_tile(Qs, tid);
+    os.store_tile(Os, tid);
     if (tid < BMQ) {
       lse_s[tid] = lse_r * kLog2e;
       del_s[tid] = del_r;
@@ -371,8 +423,8 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
       float4 a[NQT], c[NQT];
 #pragma unroll
       for (int mt = 0; mt < NQT; ++mt) {
-        if (!PROBS) a[mt] = *reinterpret_cast<const float4*>(&Qs[(16 * mt + lq) * LD + g * DG + 4 * j]);
-        c[mt] = *reinterpret_cast<const float4*>(&Os[(16 * mt + lq) * LD + g * DG + 4 * j]);
+        if (!PROBS) a[mt] = lds_read_quad<DP>(Qs, 16 * mt + lq, g * (DG / 4) + j);
+        c[mt] = lds_read_quad<DP>(Os, 16 * mt + lq, g * (DG / 4) + j);
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -433,8 +485,8 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float oa[NDT], qa[NDT];
-        lds_read_vec<NDT>(&Os[(16 * mt + 4 * g + i) * LD + NDT * lq], oa);
-        lds_read_vec<NDT>(&Qs[(16 * mt + 4 * g + i) * LD + NDT * lq], qa);
+        lds_read_seg<DP, NDT>(Os, 16 * mt + 4 * g + i, lq, oa);
+        lds_read_seg<DP, NDT>(Qs, 16 * mt + 4 * g + i, lq, qa);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
           dvacc[dt] = mfma4(oa[dt], s[mt][i], dvacc[dt]);
@@ -448,6 +500,218 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
   store_row_frag<DP, VEC>(dV + base, krow, L.T, L.D, L.st, g, dvacc, 1.f);
 }
 
+// Key-stationary dK/dV (and dS) for head dim 64 with 128-bit-aligned operands:
+// the contractions of attn_bwd_dkv_kernel<64, 4, true, false, DS_OUT>,
+// arranged to keep the MFMA pipe fed.  On gfx950 every VALU instruction a SIMD
+// issues costs MFMA issue time (an fp32 MFMA and a VALU op do not overlap), so
+// the loop is built to need as little VALU work as possible:
+//   - 32-query sub-tiles of Q and dO go from global memory straight into LDS
+//     (global_load_lds), two LDS slots, one barrier per sub-tile: the next
+//     sub-tile streams in while the current one is consumed, no registers hold
+//     staged data, and every lane's fetch offsets are computed once (only a
+//     uniform base moves per sub-tile).  The two slots are separate LDS arrays
+//     and the loop is unrolled by two, so the compiler can tell the reads of
+//     one slot from the loads into the other and does not wait for those loads
+//     before reading;
+//   - the row statistics arrive as one 256-byte block per sub-tile
+//     (attn_bwd_stats_kernel: -LSE*log2(e), then -Delta) and initialise the S
+//     and dP accumulators, so P = exp2(S) and dS = P * dP;
+//   - masking runs only on sub-tiles that touch the diagonal or the end of the
+//     sequence (a wave-uniform test);
+//   - Q and dO sit in the swizzled Lds<64> layout (a DMA instruction fills four
+//     unpadded rows; lane l fetches the logical quad that belongs at position l);
+//   - each accumulator is one dependent MFMA chain (back-to-back accumulation
+//     into the same registers issues at full rate), so S and dP of a sub-tile
+//     take 8 registers each.
+// Rows past T are fetched from row T-1 (in bounds) and masked.  Every dS entry
+// the dQ kernel reads is stored: a wave skips a sub-tile only when all its rows
+// precede the wave's keys.  A block handles key tiles p and n_kt-1-p (n_kt+1
+// key-tile x query-tile products for every block), so equal blocks fill the
+// CUs to the end instead of leaving a tail of short blocks;
+// grid = B*H*ceil(n_kt/2).
+#ifndef WHA_DMA_WPE
+#define WHA_DMA_WPE __attribute__((amdgpu_waves_per_eu(3)))
+#endif
+#ifndef WHA_FENCE
+#define WHA_FENCE() __builtin_amdgcn_sched_barrier(0)
+#endif
+template <bool DS_OUT>
+__global__ __launch_bounds__(256) WHA_DMA_WPE void attn_bwd_dkv_dma_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, const float* __restrict__ stats, float* __restrict__ dK,
+    float* __restrict__ dV, float* __restrict__ DS, View L, float scale, float scale_log2) {
+  constexpr int DP = 64, DG = 16, NDT = 4;
+  constexpr int BSUB = 32;         // queries per sub-tile
+  constexpr int TILE = BSUB * DP;  // floats per operand sub-tile
+  static_assert(Lds<DP, true>::SWZ, "the DMA layout is the swizzled 64-float row");
+  __shared__ __align__(16) float Qs0[TILE], Qs1[TILE];
+  __shared__ __align__(16) float Os0[TILE], Os1[TILE];
+  __shared__ __align__(16) float St0[2 * BSUB], St1[2 * BSUB];
+
+  const int BH = L.B * L.H;
+  const int bh = blockIdx.x % BH;
+  const int pair = (int)(blockIdx.x / BH);
+  const int n_kt = (L.T + 63) / 64;
+  const int n_st = (L.T + BSUB - 1) / BSUB;
+  const int b = bh / L.H, h = bh % L.H;
+  const int64_t base = (int64_t)b * L.sb + (int64_t)h * L.sh;
+  const char* qg = reinterpret_cast<const char*>(Q + base);
+  const char* og = reinterpret_cast<const char*>(dO + base);
+  const float* stg = stats + (int64_t)bh * n_st * 64;
+  const int64_t sub_bytes = (int64_t)BSUB * L.st * 4;  // one sub-tile of rows
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 15, g = lane >> 4;
+
+  // This lane's fetch: wave w fills LDS quads 64(2w+u) .. +63 of both operands
+  // (u = 0, 1): row r = 4(2w+u) + lane/16 of the sub-tile, position lane%16,
+  // which holds logical quad (lane%16) ^ (r & 11).  Byte offsets from the
+  // sub-tile's first row; the last sub-tile clamps rows to T-1.
+  int rrow[2];
+  uint32_t roff[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    rrow[u] = 4 * (2 * wave + u) + (lane >> 4);
+    roff[u] = (uint32_t)(rrow[u] * L.st + 4 * ((lane & 15) ^ (rrow[u] & 11))) * 4u;
+  }
+  auto fetch = [&](int st, float* Qd, float* Od, float* Sd) {
+    const int q0 = st * BSUB;
+    const char* qs = qg + st * sub_bytes;
+    const char* os = og + st * sub_bytes;
+    uint32_t off[2] = {roff[0], roff[1]};
+    if (q0 + BSUB > L.T) {  // last sub-tile: rows past T read row T-1
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        off[u] = (uint32_t)((min(q0 + rrow[u], L.T - 1) - q0) * L.st + 4 * ((lane & 15) ^ (rrow[u] & 11))) * 4u;
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      dma_quad(reinterpret_cast<const float*>(qs + off[u]), Qd + 256 * (2 * wave + u));
+      dma_quad(reinterpret_cast<const float*>(os + off[u]), Od + 256 * (2 * wave + u));
+    }
+    if (wave == 0) dma_dword(stg + st * 64 + lane, Sd);
+  };
+
+  // key tiles pair and n_kt-1-pair: every block does n_kt+1 tiles of work.
+  // One key tile: 64 keys, wave w owns keys 64kt + 16w .. +15.
+  const int n_pass = (n_kt - 1 - pair != pair) ? 2 : 1;
+  for (int pass = 0; pass < n_pass; ++pass) {
+    const int kt = pass == 0 ? pair : n_kt - 1 - pair;
+    const int k0w = kt * 64 + wave * 16;
+    const int krow = k0w + lq;
+    float kf[DG], vf[DG];
+    load_row_frag<DP, true>(K + base, krow, L.T, L.D, L.st, g, scale_log2, kf);
+    load_row_frag<DP, true>(V + base, krow, L.T, L.D, L.st, g, 1.f, vf);
+    floatx4 dkacc[NDT], dvacc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      dkacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      dvacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    const int q_end = krow < L.T ? L.T : 0;  // valid queries: krow <= q < q_end
+    float* dsw = DS_OUT ? DS + ((int64_t)bh * ds_rows(L.T) + ds_block_row(kt, L.T) - (int64_t)64 * kt) * 64 +
+                              wave * 16 + lq
+                        : nullptr;
+
+    // one sub-tile's contractions; MASKED: the sub-tile touches the diagonal or
+    // the end of the sequence (a separate copy, so the common case carries no
+    // compare or select)
+    auto compute = [&](auto masked, int qb, const float* Qs, const float* Os, const float* Sts) {
+      constexpr bool MASKED = decltype(masked)::value;
+      // S (log2 units) and dP, started from -LSE*log2(e) and -Delta of their rows
+      floatx4 s[2], dp[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        WHA_FENCE();
+        s[mt] = *reinterpret_cast<const floatx4*>(&Sts[16 * mt + 4 * g]);
+        dp[mt] = *reinterpret_cast<const floatx4*>(&Sts[BSUB + 16 * mt + 4 * g]);
+#pragma unroll
+        for (int j = 0; j < DG / 4; ++j) {
+          const float4 a = lds_read_quad<DP, true>(Qs, 16 * mt + lq, 4 * g + j);
+          const float4 c = lds_read_quad<DP, true>(Os, 16 * mt + lq, 4 * g + j);
+          s[mt] = mfma4(a.x, kf[4 * j + 0], s[mt]);
+          s[mt] = mfma4(a.y, kf[4 * j + 1], s[mt]);
+          s[mt] = mfma4(a.z, kf[4 * j + 2], s[mt]);
+          s[mt] = mfma4(a.w, kf[4 * j + 3], s[mt]);
+          dp[mt] = mfma4(c.x, vf[4 * j + 0], dp[mt]);
+          dp[mt] = mfma4(c.y, vf[4 * j + 1], dp[mt]);
+          dp[mt] = mfma4(c.z, vf[4 * j + 2], dp[mt]);
+          dp[mt] = mfma4(c.w, vf[4 * j + 3], dp[mt]);
+        }
+      }
+      WHA_FENCE();
+      // lane element (mt,i): query qb+16mt+4g+i, key krow
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = fast_exp2(s[mt][i]);
+          if (MASKED) {
+            const int q = qb + 16 * mt + 4 * g + i;
+            const bool valid = (q >= krow) & (q < q_end);
+            s[mt][i] = valid ? p : 0.f;
+            dp[mt][i] = valid ? p * dp[mt][i] : 0.f;
+          } else {
+            s[mt][i] = p;
+            dp[mt][i] = p * dp[mt][i];
+          }
+        }
+      }
+
+      if (DS_OUT) {
+        float* dsq = dsw + (int64_t)(qb + 4 * g) * 64;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dsq[(16 * mt + i) * 64] = dp[mt][i];
+        }
+      }
+
+      // dV^T[d][key] += dO^T[d][query] P[query][key];  dK^T[d][key] += Q^T[d][query] dS[query][key]
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        WHA_FENCE();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float oa[NDT], qa[NDT];
+          lds_read_seg<DP, NDT, true>(Os, 16 * mt + 4 * g + i, lq, oa);
+          lds_read_seg<DP, NDT, true>(Qs, 16 * mt + 4 * g + i, lq, qa);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            dvacc[dt] = mfma4(oa[dt], s[mt][i], dvacc[dt]);
+            dkacc[dt] = mfma4(qa[dt], dp[mt][i], dkacc[dt]);
+          }
+        }
+      }
+    };
+
+    // one sub-tile: wait for its loads, start the next one's, then consume it
+    auto step = [&](int st, const float* Qs, const float* Os, const float* Sts, float* Qn, float* On,
+                    float* Sn) {
+      wait_vmem();
+      __syncthreads();  // sub-tile st is in LDS; every wave is done with sub-tile st-1
+      if (st + 1 < n_st) fetch(st + 1, Qn, On, Sn);
+      const int qb = st * BSUB;
+      if (qb + BSUB - 1 < k0w) return;  // every row precedes every key of the wave
+      if (qb >= k0w + 15 && qb + BSUB <= L.T && k0w + 16 <= L.T)
+        compute(std::false_type{}, qb, Qs, Os, Sts);
+      else
+        compute(std::true_type{}, qb, Qs, Os, Sts);
+    };
+
+    const int st0 = 2 * kt;
+    __syncthreads();  // the previous key tile's last sub-tile has been read by every wave
+    fetch(st0, Qs0, Os0, St0);
+    for (int st = st0; st < n_st; st += 2) {
+      step(st, Qs0, Os0, St0, Qs1, Os1, St1);
+      if (st + 1 < n_st) step(st + 1, Qs1, Os1, St1, Qs0, Os0, St0);
+    }
+    store_row_frag<DP, true>(dK + base, krow, L.T, L.D, L.st, g, dkacc, scale);
+    store_row_frag<DP, true>(dV + base, krow, L.T, L.D, L.st, g, dvacc, 1.f);
+  }
+}
+
 // Query-stationary dQ from stored dS: dQ^T[d][q] += K^T[d][key] dS^T[key][q] over
 // the causal 64-key tiles; K tiles staged through LDS (A operand, d = NDT*m + dt
 // on MFMA rows), dS read from the workspace with 128-bit loads straight into the
@@ -459,7 +723,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_ds_kernel(const float* __
   constexpr int NT = NW * 64;
   constexpr int BM = NW * 16;
   constexpr int BN = 64;
-  constexpr int LD = DP + WHA_LDS_PAD;
+  constexpr int LD = Lds<DP, true>::PITCH;
   constexpr int NDT = DP / 16;
   __shared__ __align__(16) float Ks[BN * LD];
 
@@ -503,7 +767,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_ds_kernel(const float* __
 
   for (int kt = 0; kt < n_kt; ++kt) {
     __syncthreads();
-    ks.template store<LD>(Ks, tid);
+    ks.template store_tile<true>(Ks, tid);
     __syncthreads();
     if (kt + 1 < n_kt) {
       ks.load(K + base, (kt + 1) * BN, L.T, L.D, L.st, tid);
@@ -520,8 +784,8 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_ds_kernel(const float* __
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float ka[NDT], kb[NDT];
-          lds_read_vec<NDT>(&Ks[(16 * c + 4 * g + e) * LD + NDT * lq], ka);
-          lds_read_vec<NDT>(&Ks[(16 * (c + 1) + 4 * g + e) * LD + NDT * lq], kb);
+          lds_read_seg<DP, NDT, true>(Ks, 16 * c + 4 * g + e, lq, ka);
+          lds_read_seg<DP, NDT, true>(Ks, 16 * (c + 1) + 4 * g + e, lq, kb);
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt) {
             acc[dt] = mfma4(ka[dt], d0[e], acc[dt]);
@@ -549,6 +813,31 @@ hipError_t bwd_fused_t(const float* q, const float* k, const float* v, const flo
   const int n_qt = (L.T + NWQ * 16 - 1) / (NWQ * 16);
   const int n_kt = (L.T + NWK * 16 - 1) / (NWK * 16);
   hipError_t e;
+  if (ds != nullptr && WHA_DKV_DMA && DP == 64 && VEC && L.D == 64) {
+    // head dim 64 with 128-bit operands: row statistics in 32-row blocks, the
+    // direct-to-LDS key-stationary kernel (dK, dV, dS), then dQ from dS
+    {
+      TimingScope ts("attn_bwd_delta", stream);
+      const int64_t rows = (int64_t)L.B * L.H * ((L.T + 31) / 32 * 32);
+      hipLaunchKernelGGL(attn_bwd_stats_kernel, dim3((unsigned)((rows + 16 * kDeltaRows - 1) / (16 * kDeltaRows))),
+                         dim3(256), 0, stream, o, d_o, lse, delta, L);
+      e = hipGetLastError();
+    }
+    if (e != hipSuccess) return e;
+    {
+      TimingScope ts("attn_bwd_dkv", stream);
+      hipLaunchKernelGGL((attn_bwd_dkv_dma_kernel<true>), dim3((unsigned)((n_kt + 1) / 2 * L.B * L.H)), dim3(256),
+                         0, stream, q, k, v, d_o, (const float*)delta, dk, dv, ds, L, scale, sl2);
+      e = hipGetLastError();
+    }
+    if (e != hipSuccess) return e;
+    TimingScope ts("attn_bwd_dq", stream);
+    constexpr int NWD = WHA_DQ_NW;
+    const int n_qt_d = (L.T + NWD * 16 - 1) / (NWD * 16);
+    hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<DP, NWD, VEC>), dim3((unsigned)(n_qt_d * L.B * L.H)),
+                       dim3(NWD * 64), 0, stream, k, (const float*)ds, dq, L, scale);
+    return hipGetLastError();
+  }
   {
     TimingScope ts("attn_bwd_delta", stream);
     e = delta_launch(o, d_o, delta, L, stream);

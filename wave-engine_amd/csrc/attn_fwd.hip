@@ -34,7 +34,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
   constexpr int NT = NW * 64;
   constexpr int BM = NW * 16;   // queries per block
   constexpr int BN = 64;        // keys per tile
-  constexpr int LD = DP + 4;    // LDS row pitch (floats): conflict-free b128 and b32 reads
+  constexpr int LD = Lds<DP>::PITCH;  // LDS row pitch (floats)
   constexpr int DG = DP / 4;    // head-dim slice per lane group
   constexpr int NDT = DP / 16;  // 16-row d tiles of O^T (row m of tile dt is d = NDT*m + dt)
   constexpr int NKT = BN / 16;  // 16-key sub-tiles of a tile
@@ -71,8 +71,8 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
 
   for (int kt = 0; kt < n_kt; ++kt) {
     __syncthreads();
-    ks.template store<LD>(Ks, tid);
-    vs.template store<LD>(Vs, tid);
+    ks.store_tile(Ks, tid);
+    vs.store_tile(Vs, tid);
     __syncthreads();
     if (kt + 1 < n_kt) {
       ks.load(K + base, (kt + 1) * BN, L.T, L.D, L.st, tid);
@@ -90,7 +90,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
       float4 a[NKT];
 #pragma unroll
       for (int mt = 0; mt < NKT; ++mt)
-        a[mt] = *reinterpret_cast<const float4*>(&Ks[(16 * mt + lq) * LD + g * DG + 4 * j]);
+        a[mt] = lds_read_quad<DP>(Ks, 16 * mt + lq, g * (DG / 4) + j);
 #pragma unroll
       for (int mt = 0; mt < NKT; ++mt) s[mt] = mfma4(a[mt].x, qf[4 * j + 0], s[mt]);
 #pragma unroll
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float va[NDT];
-        lds_read_vec<NDT>(&Vs[(16 * mt + 4 * g + i) * LD + NDT * lq], va);
+        lds_read_seg<DP, NDT>(Vs, 16 * mt + 4 * g + i, lq, va);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma4(va[dt], s[mt][i], oacc[dt]);
       }

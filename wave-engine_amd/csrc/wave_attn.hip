@@ -123,7 +123,7 @@ __global__ __launch_bounds__(NW * 64) void wave_fwd_kernel(const float* __restri
   constexpr int NT = NW * 64;
   constexpr int BM = NW * 16;
   constexpr int BN = 64;
-  constexpr int LD = DP + 4;
+  constexpr int LD = Lds<DP>::PITCH;
   constexpr int NDT = DP / 16;
   constexpr int NKT = BN / 16;
   constexpr int FG = kFP / 4;
@@ -176,7 +176,7 @@ __global__ __launch_bounds__(NW * 64) void wave_fwd_kernel(const float* __restri
   for (int kt = 0; kt < n_kt; ++kt) {
     __syncthreads();
     fs.template store<kLDF>(Fs, tid);
-    vs.template store<LD>(Vs, tid);
+    vs.store_tile(Vs, tid);
     if (tid < BN) Bs[tid] = kb_r;
     __syncthreads();
     if (kt + 1 < n_kt) {
@@ -247,7 +247,7 @@ __global__ __launch_bounds__(NW * 64) void wave_fwd_kernel(const float* __restri
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float va[NDT];
-        lds_read_vec<NDT>(&Vs[(16 * mt + 4 * g + i) * LD + NDT * lq], va);
+        lds_read_seg<DP, NDT>(Vs, 16 * mt + 4 * g + i, lq, va);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma4(va[dt], s[mt][i], oacc[dt]);
       }
@@ -280,7 +280,7 @@ __global__ __launch_bounds__(256) void wave_dkv_kernel(const float* __restrict__
                                                        float cs) {
   constexpr int NT = 256;
   constexpr int BMQ = 64;
-  constexpr int LD = DP + 4;
+  constexpr int LD = Lds<DP>::PITCH;
   constexpr int DG = DP / 4;
   constexpr int NDT = DP / 16;
   constexpr int NQT = BMQ / 16;
@@ -350,7 +350,7 @@ __global__ __launch_bounds__(256) void wave_dkv_kernel(const float* __restrict__
   for (int qt = kt; qt < n_qt; ++qt) {
     __syncthreads();
     fs.template store<kLDF>(Fs, tid);
-    os.template store<LD>(Os, tid);
+    os.store_tile(Os, tid);
     if (tid < BMQ) {
       lse_s[tid] = lse_r * kLog2e;
       del_s[tid] = del_r;
@@ -387,7 +387,7 @@ __global__ __launch_bounds__(256) void wave_dkv_kernel(const float* __restrict__
       float4 c[NQT];
 #pragma unroll
       for (int mt = 0; mt < NQT; ++mt)
-        c[mt] = *reinterpret_cast<const float4*>(&Os[(16 * mt + lq) * LD + g * DG + 4 * j]);
+        c[mt] = lds_read_quad<DP>(Os, 16 * mt + lq, g * (DG / 4) + j);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
 #pragma unroll
@@ -433,7 +433,7 @@ __global__ __launch_bounds__(256) void wave_dkv_kernel(const float* __restrict__
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float oa[NDT], fa[NFT];
-        lds_read_vec<NDT>(&Os[(16 * mt + 4 * g + i) * LD + NDT * lq], oa);
+        lds_read_seg<DP, NDT>(Os, 16 * mt + 4 * g + i, lq, oa);
         lds_read_vec<NFT>(&Fs[(16 * mt + 4 * g + i) * kLDF + NFT * lq], fa);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) dvacc[dt] = mfma4(oa[dt], s[mt][i], dvacc[dt]);

@@ -315,9 +315,16 @@ static size_t ds_bytes(const wha_layout* layout) {
   return n <= kMaxDsBytes ? round256(n) : 0;
 }
 
+// Row statistics of the fused backward (Delta, or the blocked -LSE*log2(e) /
+// -Delta pairs the head-dim-64 path uses).
+static size_t stats_bytes(const wha_layout* layout) {
+  wha::View V{layout->B, layout->H, layout->T, layout->D, 0, 0, 0};
+  return round256(wha::bwd_stats_floats(V) * sizeof(float));
+}
+
 size_t wha_attn_bwd_workspace_size(const wha_layout* layout) {
   if (!layout || layout->B <= 0 || layout->H <= 0 || layout->T <= 0) return 0;
-  return delta_bytes(layout) + ds_bytes(layout);
+  return stats_bytes(layout) + ds_bytes(layout);
 }
 
 int wha_attn_bwd(const float* q, const float* k, const float* v, const float* o, const float* d_o,
@@ -337,7 +344,7 @@ int wha_attn_bwd(const float* q, const float* k, const float* v, const float* o,
   const bool vec = vec_ok(V, {q, k, v, o, d_o, dq, dk, dv});
   float* delta = static_cast<float*>(ws);
   const size_t dsb = ds_bytes(layout);
-  float* ds = dsb ? reinterpret_cast<float*>(static_cast<char*>(ws) + delta_bytes(layout)) : nullptr;
+  float* ds = dsb ? reinterpret_cast<float*>(static_cast<char*>(ws) + stats_bytes(layout)) : nullptr;
   hipError_t e = wha::launch_attn_bwd(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, V, vec, scale, s);
   if (e != hipSuccess) return hip_fail(e, "wha_attn_bwd launch");
   g_err[0] = 0;

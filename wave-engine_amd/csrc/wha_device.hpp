@@ -26,6 +26,12 @@
 #ifndef WHA_DQ_NW
 #define WHA_DQ_NW 4
 #endif
+#ifndef WHA_LDS_SWZ
+#define WHA_LDS_SWZ 1
+#endif
+#ifndef WHA_DKV_DMA
+#define WHA_DKV_DMA 1
+#endif
 
 namespace wha {
 
@@ -72,6 +78,31 @@ __device__ __forceinline__ float pair_sum32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+
+// LDS layout of a staged [rows][DP] operand tile, addressed by 16-byte quads
+// (four consecutive head-dim entries).  The kernels read such tiles in two
+// patterns: lane (lq, g) reads quad c(g, j) of row r0 + lq (the A operand of
+// contractions over the head dimension), or quad lq of row r0 + 4g + i (the A
+// operand of contractions over rows); TileStage writes quad lane%16 of row
+// r0 + lane/16.  A gfx950 ds_read_b128 runs in 4 cycles when the 16 lanes the
+// LDS serves together hit 16 different 4-bank groups (measured with an LDS
+// probe: a padded pitch such as DP+4 leaves both read patterns 2-way
+// conflicted).  For DP = 64 rows are unpadded and quad c of row r is stored at
+// quad c ^ (r & 11), which keeps all three patterns conflict-free for every
+// lane grouping consistent with the probe.  Kernels opt in (ALLOW_SWZ): the
+// XOR costs per-lane address registers, which only pays where LDS traffic
+// matters more than VGPRs.  Other DP, and kernels that do not opt in, keep a
+// 4-float pad.
+template <int DP, bool ALLOW_SWZ = false>
+struct Lds {
+  static constexpr bool SWZ = WHA_LDS_SWZ && ALLOW_SWZ && DP == 64;
+  static constexpr int PITCH = SWZ ? DP : DP + WHA_LDS_PAD;
+  // float offset of quad c of row r
+  __device__ __forceinline__ static int at(int r, int c) { return r * PITCH + 4 * (SWZ ? (c ^ (r & 11)) : c); }
+  // float offset of head-dim entry d of row r (a quad-aligned group of N <= 4
+  // entries starting at d stays contiguous)
+  __device__ __forceinline__ static int at_d(int r, int d) { return SWZ ? at(r, d >> 2) + (d & 3) : r * PITCH + d; }
+};
 
 // Cooperative global -> register -> LDS staging of a ROWS x DP tile of one
 // (b,h) matrix, rows [row0, row0+ROWS), zero-filled past T and past D.
@@ -132,7 +163,67 @@ struct TileStage {
       }
     }
   }
+
+  // store in the Lds<DP, SW> layout
+  template <bool SW = false>
+  __device__ __forceinline__ void store_tile(float* lds, int tid) const {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int idx = tid + p * NT;
+      if (NF4 % NT == 0 || idx < NF4) *reinterpret_cast<float4*>(lds + Lds<DP, SW>::at(idx / C4, idx % C4)) = r[p];
+    }
+  }
 };
+
+// Reads the N head-dim entries [N*lq, N*lq + N) of row r of an Lds<DP, SW> tile.
+template <int DP, int N, bool SW = false>
+__device__ __forceinline__ void lds_read_seg(const float* tile, int r, int lq, float* out) {
+  using LT = Lds<DP, SW>;
+  if (LT::SWZ && N == 4) {
+    const float4 v = *reinterpret_cast<const float4*>(tile + LT::at(r, lq));
+    out[0] = v.x;
+    out[1] = v.y;
+    out[2] = v.z;
+    out[3] = v.w;
+  } else {
+    static_assert(!LT::SWZ || N == 4, "swizzled tiles are read in whole quads");
+    const float* p = tile + r * LT::PITCH + N * lq;
+    if (N % 4 == 0) {
+#pragma unroll
+      for (int c = 0; c < N / 4; ++c) {
+        const float4 v = *reinterpret_cast<const float4*>(p + 4 * c);
+        out[4 * c + 0] = v.x;
+        out[4 * c + 1] = v.y;
+        out[4 * c + 2] = v.z;
+        out[4 * c + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < N; ++c) out[c] = p[c];
+    }
+  }
+}
+
+// gfx950 direct global -> LDS loads (global_load_lds_dword / _dwordx4): every
+// lane supplies its own global address and its data lands at
+// lds_base + lane * bytes (lds_base wave-uniform; checked on the box with a
+// probe).  They count in vmcnt like other vector-memory loads.
+__device__ __forceinline__ void dma_quad(const float* gsrc, float* lds_base) {
+  __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)gsrc,
+                                   (void __attribute__((address_space(3)))*)lds_base, 16, 0, 0);
+}
+__device__ __forceinline__ void dma_dword(const float* gsrc, float* lds_base) {
+  __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)gsrc,
+                                   (void __attribute__((address_space(3)))*)lds_base, 4, 0, 0);
+}
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Reads quad c of row r of an Lds<DP, SW> tile.
+template <int DP, bool SW = false>
+__device__ __forceinline__ float4 lds_read_quad(const float* tile, int r, int c) {
+  return *reinterpret_cast<const float4*>(tile + Lds<DP, SW>::at(r, c));
+}
 
 // Per-lane operand fragment of one row: lane group g = lane/16 holds
 // x[row][g*DP/4 + s], s = 0 .. DP/4-1, multiplied by mul; zero past T and D.

@@ -38,10 +38,15 @@ hipError_t launch_attn_fwd(const float* q, const float* k, const float* v, float
 // score matrix in 64-key column blocks, fp32).
 size_t bwd_ds_floats(const View& L);
 
+// Floats of the row-statistics scratch of the fused backward (Delta, or for
+// head dim 64 the -LSE*log2(e) / -Delta blocks of attn_bwd_stats_kernel).
+size_t bwd_stats_floats(const View& L);
+
 // Fused backward: Delta pre-pass, then either (ds != nullptr) the key-stationary
 // dK/dV kernel writing dS to ds and a query-stationary dQ = dS K kernel, or
 // (ds == nullptr) a query-stationary dQ kernel that recomputes S and dP and the
-// key-stationary dK/dV kernel.  Both deterministic.  delta: [B*H*T] scratch.
+// key-stationary dK/dV kernel.  Both deterministic.  delta: bwd_stats_floats(L)
+// floats of scratch.
 hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const float* o,
                            const float* d_o, const float* lse, float* dq, float* dk, float* dv,
                            float* delta, float* ds, const View& L, bool vec, float scale,
