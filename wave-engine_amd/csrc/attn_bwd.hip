@@ -532,9 +532,6 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
 #ifndef WHA_DMA_WPE
 #define WHA_DMA_WPE __attribute__((amdgpu_waves_per_eu(3)))
 #endif
-#ifndef WHA_FENCE
-#define WHA_FENCE() __builtin_amdgcn_sched_barrier(0)
-#endif
 template <bool DS_OUT>
 __global__ __launch_bounds__(256) WHA_DMA_WPE void attn_bwd_dkv_dma_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
@@ -712,6 +709,138 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE void attn_bwd_dkv_dma_kernel(
   }
 }
 
+// dQ = scale * dS K for head dim 64 with 128-bit-aligned operands, written for
+// few VALU instructions per MFMA like attn_bwd_dkv_dma_kernel:
+//   - 64-key K tiles go from global memory straight into LDS (global_load_lds,
+//     swizzled Lds<64> layout, two slots in separate arrays, loop unrolled by
+//     two, one barrier per tile);
+//   - a lane's 16 dS values of the next tile come as four 128-bit loads from
+//     one address (dS rows sit at 256-byte pitch), straight into the MFMA B
+//     operand (k-step (c, e) <-> key 16c + 4g + e);
+//   - one dependent accumulator chain per d-tile; 16-key chunks that lie after
+//     every query of the wave are skipped (only in the diagonal tile, a
+//     wave-uniform test).  Every dS entry read there was written by the
+//     key-stationary pass (zeros where masked); rows past T feed only dQ rows
+//     that are never stored.
+// A block handles query tiles p and n_qt-1-p (n_qt+1 key tiles of work for
+// every block); grid = B*H*ceil(n_qt/2).
+#ifndef WHA_DQ_WPE
+#define WHA_DQ_WPE
+#endif
+template <bool UNUSED = false>
+__global__ __launch_bounds__(256) WHA_DQ_WPE void attn_bwd_dq_dma_kernel(const float* __restrict__ K,
+                                                              const float* __restrict__ DS,
+                                                              float* __restrict__ dQ, View L, float scale) {
+  constexpr int DP = 64, NDT = 4, BN = 64;
+  constexpr int TILE = BN * DP;
+  __shared__ __align__(16) float Ks0[TILE], Ks1[TILE];
+
+  const int BH = L.B * L.H;
+  const int bh = blockIdx.x % BH;
+  const int pair = (int)(blockIdx.x / BH);
+  const int n_qt = (L.T + 63) / 64;
+  const int b = bh / L.H, h = bh % L.H;
+  const int64_t base = (int64_t)b * L.sb + (int64_t)h * L.sh;
+  const char* kg = reinterpret_cast<const char*>(K + base);
+  const int64_t tile_bytes = (int64_t)BN * L.st * 4;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 15, g = lane >> 4;
+
+  // this lane's part of a K tile fetch: wave w fills LDS quads 64(4w+u) .. +63
+  // (u = 0..3): row 4(4w+u) + lane/16, position lane%16 <- logical quad
+  // (lane%16) ^ (row & 11); byte offsets from the tile's first row
+  uint32_t koff[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int r = 4 * (4 * wave + u) + (lane >> 4);
+    koff[u] = (uint32_t)(r * L.st + 4 * ((lane & 15) ^ (r & 11))) * 4u;
+  }
+  auto fetch = [&](int kt, float* Kd) {
+    const char* ks = kg + kt * tile_bytes;
+    if ((kt + 1) * BN > L.T) {  // last tile: rows past T read row T-1
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int r = 4 * (4 * wave + u) + (lane >> 4);
+        const uint32_t off = (uint32_t)((min(kt * BN + r, L.T - 1) - kt * BN) * L.st + 4 * ((lane & 15) ^ (r & 11))) * 4u;
+        dma_quad(reinterpret_cast<const float*>(ks + off), Kd + 256 * (4 * wave + u));
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) dma_quad(reinterpret_cast<const float*>(ks + koff[u]), Kd + 256 * (4 * wave + u));
+    }
+  };
+
+  const float* dsh = DS + (int64_t)bh * ds_rows(L.T) * 64;
+  const int n_pass = (n_qt - 1 - pair != pair) ? 2 : 1;
+  for (int pass = 0; pass < n_pass; ++pass) {
+    const int qt = pass == 0 ? n_qt - 1 - pair : pair;  // the longer row of tiles first
+    const int q0 = qt * 64 + wave * 16;
+    const int qrow = q0 + lq;
+    const int n_kt = qt + 1;
+    // dS of key tile kt for this lane: row qrow of column block kt, keys 16c + 4g .. +3
+    auto load_ds = [&](int kt, float4* dsv) {
+      const float* src = dsh + (ds_block_row(kt, L.T) + qrow - 64 * kt) * 64 + 4 * g;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) dsv[c] = *reinterpret_cast<const float4*>(src + 16 * c);
+    };
+    floatx4 acc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float4 dcur[4], dnext[4];
+
+    auto step = [&](int kt, const float* Ks, float* Kn) {
+      wait_vmem();
+      __syncthreads();  // K tile kt is in LDS; every wave is done with tile kt-1
+#pragma unroll
+      for (int c = 0; c < 4; ++c) dcur[c] = dnext[c];
+      if (kt + 1 < n_kt) {
+        fetch(kt + 1, Kn);
+        load_ds(kt + 1, dnext);
+      }
+      if (kt < qt) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          WHA_FENCE();
+          const float dv[4] = {dcur[c].x, dcur[c].y, dcur[c].z, dcur[c].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float ka[NDT];
+            lds_read_seg<DP, NDT, true>(Ks, 16 * c + 4 * g + e, lq, ka);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma4(ka[dt], dv[e], acc[dt]);
+          }
+        }
+      } else {
+        // diagonal tile: chunks after every query of the wave are skipped
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (16 * c > wave * 16 + 15) break;
+          WHA_FENCE();
+          const float dv[4] = {dcur[c].x, dcur[c].y, dcur[c].z, dcur[c].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float ka[NDT];
+            lds_read_seg<DP, NDT, true>(Ks, 16 * c + 4 * g + e, lq, ka);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma4(ka[dt], dv[e], acc[dt]);
+          }
+        }
+      }
+    };
+
+    __syncthreads();  // the previous pass's last tile has been read by every wave
+    fetch(0, Ks0);
+    load_ds(0, dnext);
+    for (int kt = 0; kt < n_kt; kt += 2) {
+      step(kt, Ks0, Ks1);
+      if (kt + 1 < n_kt) step(kt + 1, Ks1, Ks0);
+    }
+    store_row_frag<DP, true>(dQ + base, qrow, L.T, L.D, L.st, g, acc, scale);
+  }
+}
+
 // Query-stationary dQ from stored dS: dQ^T[d][q] += K^T[d][key] dS^T[key][q] over
 // the causal 64-key tiles; K tiles staged through LDS (A operand, d = NDT*m + dt
 // on MFMA rows), dS read from the workspace with 128-bit loads straight into the
@@ -832,10 +961,9 @@ hipError_t bwd_fused_t(const float* q, const float* k, const float* v, const flo
     }
     if (e != hipSuccess) return e;
     TimingScope ts("attn_bwd_dq", stream);
-    constexpr int NWD = WHA_DQ_NW;
-    const int n_qt_d = (L.T + NWD * 16 - 1) / (NWD * 16);
-    hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<DP, NWD, VEC>), dim3((unsigned)(n_qt_d * L.B * L.H)),
-                       dim3(NWD * 64), 0, stream, k, (const float*)ds, dq, L, scale);
+    const int n_qt64 = (L.T + 63) / 64;
+    hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<>), dim3((unsigned)((n_qt64 + 1) / 2 * L.B * L.H)), dim3(256), 0,
+                       stream, k, (const float*)ds, dq, L, scale);
     return hipGetLastError();
   }
   {

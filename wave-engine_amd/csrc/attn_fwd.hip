@@ -20,7 +20,14 @@
 // needs only two cross-lane steps (VALU lane swaps), the running sum stays
 // lane-local until the end, and the probabilities are already in the B-operand layout of
 // O^T += V^T P^T -- no transpose through LDS.
+#include <type_traits>
+
 #include "wha_launch.hpp"
+
+#ifndef WHA_FWD_DMA
+#define WHA_FWD_DMA 1
+#endif
+
 
 namespace wha {
 
@@ -158,6 +165,197 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
     LSE[(int64_t)bh * L.T + qrow] = (m_i + log2f(l_sum)) * kLn2;
 }
 
+// Forward for head dim 64 with 128-bit-aligned operands, arranged like the
+// backward's direct-to-LDS kernels because on gfx950 every VALU instruction
+// costs MFMA issue time:
+//   - 32-key sub-tiles of K and V go from global memory straight into LDS
+//     (global_load_lds, swizzled Lds<64> layout, two slots in separate arrays,
+//     loop unrolled by two, one barrier per sub-tile, per-lane fetch offsets
+//     computed once);
+//   - masking runs only on sub-tiles that reach past a query of the wave or
+//     past T (a wave-uniform test, separate code);
+//   - the running max is refreshed, and O and the row sum rescaled, only when
+//     some lane's max grew by more than kLazyMax (log2 units; a wave-uniform
+//     ballot): until then the probabilities are taken against the older,
+//     smaller max, so they stay below 2^kLazyMax and the fp32 sums cannot
+//     overflow.  The result is the same softmax, rounded differently.
+// A block handles query tiles p and n_qt-1-p (n_qt+1 key tiles of work for
+// every block); grid = B*H*ceil(n_qt/2).
+constexpr float kLazyMax = 8.f;
+#ifndef WHA_FWD_WPE
+#define WHA_FWD_WPE __attribute__((amdgpu_waves_per_eu(3)))
+#endif
+template <bool UNUSED = false>
+__global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const float* __restrict__ Q,
+                                                                     const float* __restrict__ K,
+                                                                     const float* __restrict__ V,
+                                                                     float* __restrict__ O,
+                                                                     float* __restrict__ LSE, View L,
+                                                                     float scale_log2) {
+  constexpr int DP = 64, DG = 16, NDT = 4;
+  constexpr int BSUB = 32;         // keys per sub-tile
+  constexpr int TILE = BSUB * DP;  // floats per operand sub-tile
+  __shared__ __align__(16) float Ks0[TILE], Ks1[TILE];
+  __shared__ __align__(16) float Vs0[TILE], Vs1[TILE];
+
+  const int BH = L.B * L.H;
+  const int bh = blockIdx.x % BH;
+  const int pair = (int)(blockIdx.x / BH);
+  const int n_qt = (L.T + 63) / 64;
+  const int b = bh / L.H, h = bh % L.H;
+  const int64_t base = (int64_t)b * L.sb + (int64_t)h * L.sh;
+  const char* kg = reinterpret_cast<const char*>(K + base);
+  const char* vg = reinterpret_cast<const char*>(V + base);
+  const int64_t sub_bytes = (int64_t)BSUB * L.st * 4;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 15, g = lane >> 4;
+
+  // this lane's fetch: wave w fills LDS quads 64(2w+u) .. +63 of K and V
+  // (u = 0, 1): row 4(2w+u) + lane/16, position lane%16 <- logical quad
+  // (lane%16) ^ (row & 11); byte offsets from the sub-tile's first row
+  int rrow[2];
+  uint32_t roff[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    rrow[u] = 4 * (2 * wave + u) + (lane >> 4);
+    roff[u] = (uint32_t)(rrow[u] * L.st + 4 * ((lane & 15) ^ (rrow[u] & 11))) * 4u;
+  }
+  auto fetch = [&](int st, float* Kd, float* Vd) {
+    const int k0 = st * BSUB;
+    const char* ks = kg + st * sub_bytes;
+    const char* vs = vg + st * sub_bytes;
+    uint32_t off[2] = {roff[0], roff[1]};
+    if (k0 + BSUB > L.T) {  // last sub-tile: rows past T read row T-1
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        off[u] = (uint32_t)((min(k0 + rrow[u], L.T - 1) - k0) * L.st + 4 * ((lane & 15) ^ (rrow[u] & 11))) * 4u;
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      dma_quad(reinterpret_cast<const float*>(ks + off[u]), Kd + 256 * (2 * wave + u));
+      dma_quad(reinterpret_cast<const float*>(vs + off[u]), Vd + 256 * (2 * wave + u));
+    }
+  };
+
+  const int n_pass = (n_qt - 1 - pair != pair) ? 2 : 1;
+  for (int pass = 0; pass < n_pass; ++pass) {
+    const int qt = pass == 0 ? n_qt - 1 - pair : pair;  // the longer row of tiles first
+    const int q0 = qt * 64 + wave * 16;                  // first query of this wave
+    const int qrow = q0 + lq;                            // this lane's query
+    float qf[DG];
+    load_row_frag<DP, true>(Q + base, qrow, L.T, L.D, L.st, g, scale_log2, qf);
+    // running max m_i (log2 units) and row sum; -m_i in every element of neg_m,
+    // from which the S accumulators start (MFMA srcC), so the scores come out
+    // already shifted by the running max.  The first sub-tile sets m_i exactly.
+    float m_i = 0.f, l_i = 0.f;
+    bool fresh = true;
+    floatx4 neg_m = floatx4{0.f, 0.f, 0.f, 0.f};
+    floatx4 oacc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) oacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int n_sub = (min(L.T, (qt + 1) * 64) + BSUB - 1) / BSUB;
+    const int key_last = min(qrow, L.T - 1);  // keys above it are masked
+
+    auto compute = [&](auto masked, int k0, const float* Ks, const float* Vs) {
+      constexpr bool MASKED = decltype(masked)::value;
+      // S^T[key][query] in log2 units: MFMA rows are keys 16mt + lq, columns the wave's queries
+      floatx4 s[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        WHA_FENCE();
+#pragma unroll
+        for (int j = 0; j < DG / 4; ++j) {
+          const float4 a = lds_read_quad<DP, true>(Ks, 16 * mt + lq, 4 * g + j);
+          s[mt] = mfma4(a.x, qf[4 * j + 0], j == 0 ? neg_m : s[mt]);
+          s[mt] = mfma4(a.y, qf[4 * j + 1], s[mt]);
+          s[mt] = mfma4(a.z, qf[4 * j + 2], s[mt]);
+          s[mt] = mfma4(a.w, qf[4 * j + 3], s[mt]);
+        }
+      }
+      WHA_FENCE();
+      // lane element (mt,i): key k0 + 16mt + 4g + i of query qrow, as s - m_i
+      if (MASKED) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            s[mt][i] = (k0 + 16 * mt + 4 * g + i > key_last) ? -INFINITY : s[mt][i];
+        }
+      }
+      // largest shifted score of the query (its 8 keys here, then the 4 lane groups)
+      float mx = vmax3(vmax3(s[0][0], s[0][1], s[0][2]), vmax3(s[0][3], s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3]));
+      mx = pair_max32(pair_max16(mx));
+      if (fresh) {
+        // first sub-tile: the running max is this one's (k0 <= every query here,
+        // so every lane has a finite score)
+        asm volatile("" ::: "memory");
+        fresh = false;
+        m_i = mx;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) s[mt] -= mx;
+        neg_m = floatx4{-m_i, -m_i, -m_i, -m_i};
+      } else if (__builtin_amdgcn_ballot_w64(mx > kLazyMax) != 0) {
+        // a real branch (not if-converted): rescale to the new max
+        asm volatile("" ::: "memory");
+        const float d = fmaxf(mx, 0.f);  // the max grows by d; scores shift down by d
+        const float alpha = fast_exp2(-d);
+        l_i *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
+        m_i += d;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) s[mt] -= d;
+        neg_m = floatx4{-m_i, -m_i, -m_i, -m_i};
+      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[mt][i] = fast_exp2(s[mt][i]);
+      }
+      l_i += ((s[0][0] + s[0][1]) + (s[0][2] + s[0][3])) + ((s[1][0] + s[1][1]) + (s[1][2] + s[1][3]));
+
+      // O^T[d][query] += V^T[d][key] P^T[key][query] (d = NDT*m + dt on MFMA rows)
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        WHA_FENCE();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float va[NDT];
+          lds_read_seg<DP, NDT, true>(Vs, 16 * mt + 4 * g + i, lq, va);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma4(va[dt], s[mt][i], oacc[dt]);
+        }
+      }
+    };
+
+    // one sub-tile: wait for its loads, start the next one's, then consume it
+    auto step = [&](int st, const float* Ks, const float* Vs, float* Kn, float* Vn) {
+      wait_vmem();
+      __syncthreads();  // sub-tile st is in LDS; every wave is done with sub-tile st-1
+      if (st + 1 < n_sub) fetch(st + 1, Kn, Vn);
+      const int k0 = st * BSUB;
+      if (k0 > q0 + 15) return;  // every key follows every query of the wave
+      if (k0 + BSUB - 1 <= q0 && k0 + BSUB <= L.T)
+        compute(std::false_type{}, k0, Ks, Vs);
+      else
+        compute(std::true_type{}, k0, Ks, Vs);
+    };
+
+    __syncthreads();  // the previous pass's last sub-tile has been read by every wave
+    fetch(0, Ks0, Vs0);
+    for (int st = 0; st < n_sub; st += 2) {
+      step(st, Ks0, Vs0, Ks1, Vs1);
+      if (st + 1 < n_sub) step(st + 1, Ks1, Vs1, Ks0, Vs0);
+    }
+
+    const float l_sum = pair_sum32(pair_sum16(l_i));
+    store_row_frag<DP, true>(O + base, qrow, L.T, L.D, L.st, g, oacc, 1.f / l_sum);
+    if (LSE != nullptr && g == 0 && qrow < L.T) LSE[(int64_t)bh * L.T + qrow] = (m_i + log2f(l_sum)) * kLn2;
+  }
+}
+
 template <int DP, int NW, bool VEC>
 static hipError_t launch_fwd_t(const float* q, const float* k, const float* v, float* o, float* lse,
                                const View& L, float scale, hipStream_t stream) {
@@ -178,6 +376,14 @@ hipError_t launch_attn_fwd(const float* q, const float* k, const float* v, float
       return vec ? launch_fwd_t<48, 4, true>(q, k, v, o, lse, L, scale, stream)
                  : launch_fwd_t<48, 4, false>(q, k, v, o, lse, L, scale, stream);
     case 64:
+      if (vec && L.D == 64 && WHA_FWD_DMA) {
+        const int n_qt = (L.T + 63) / 64;
+        const float scale_log2 = (float)((double)scale * 1.4426950408889634);
+        TimingScope ts("attn_fwd", stream);
+        hipLaunchKernelGGL((attn_fwd_dma_kernel<>), dim3((unsigned)((n_qt + 1) / 2 * L.B * L.H)), dim3(256), 0,
+                           stream, q, k, v, o, lse, L, scale_log2);
+        return hipGetLastError();
+      }
       return vec ? launch_fwd_t<64, 4, true>(q, k, v, o, lse, L, scale, stream)
                  : launch_fwd_t<64, 4, false>(q, k, v, o, lse, L, scale, stream);
     case 128:

@@ -32,6 +32,12 @@
 #ifndef WHA_DKV_DMA
 #define WHA_DKV_DMA 1
 #endif
+// Scheduling fence between the phases of a loop body: keeps the machine
+// scheduler from hoisting every LDS operand read of an iteration to its top,
+// which costs registers (and occupancy) for no gain.
+#ifndef WHA_FENCE
+#define WHA_FENCE() __builtin_amdgcn_sched_barrier(0)
+#endif
 
 namespace wha {
 
@@ -62,13 +68,29 @@ __device__ __forceinline__ float xor_shfl(float x, int mask) { return __shfl_xor
 // v_permlane16_swap leaves lane l holding {x[l], x[l^16]} (in some order) and
 // v_permlane32_swap {x[l], x[l^32]}; max and + are commutative, so both lanes of
 // a pair get bit-identical results.
+// max(a, b, c) in one VALU instruction.  fmaxf lowers to v_max_f32 with every
+// operand first quieted (IEEE mode), doubling the instruction count of a max
+// reduction; a NaN operand here only ever comes from a NaN input, which the
+// exp of the scores propagates anyway (a quiet NaN operand yields the other
+// operand, as fmaxf does).
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// max(a, b) in one VALU instruction
+__device__ __forceinline__ float vmax2(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 __device__ __forceinline__ float pair_max16(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return vmax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float pair_max32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return vmax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float pair_sum16(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
