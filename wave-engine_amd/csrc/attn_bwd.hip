@@ -593,6 +593,9 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE void attn_bwd_dkv_dma_kernel(
   // key tiles pair and n_kt-1-pair: every block does n_kt+1 tiles of work.
   // One key tile: 64 keys, wave w owns keys 64kt + 16w .. +15.
   const int n_pass = (n_kt - 1 - pair != pair) ? 2 : 1;
+  // sub-tiles this block sweeps, and how many it has left
+  const int work = (n_st - 2 * pair) + (n_pass == 2 ? n_st - 2 * (n_kt - 1 - pair) : 0);
+  int left = work;
   for (int pass = 0; pass < n_pass; ++pass) {
     const int kt = pass == 0 ? pair : n_kt - 1 - pair;
     const int k0w = kt * 64 + wave * 16;
@@ -688,6 +691,7 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE void attn_bwd_dkv_dma_kernel(
                     float* Sn) {
       wait_vmem();
       __syncthreads();  // sub-tile st is in LDS; every wave is done with sub-tile st-1
+      prio_by_remaining(left--, work);
       if (st + 1 < n_st) fetch(st + 1, Qn, On, Sn);
       const int qb = st * BSUB;
       if (qb + BSUB - 1 < k0w) return;  // every row precedes every key of the wave
@@ -774,6 +778,8 @@ __global__ __launch_bounds__(256) WHA_DQ_WPE void attn_bwd_dq_dma_kernel(const f
 
   const float* dsh = DS + (int64_t)bh * ds_rows(L.T) * 64;
   const int n_pass = (n_qt - 1 - pair != pair) ? 2 : 1;
+  const int work = (n_qt - pair) + (n_pass == 2 ? pair + 1 : 0);  // key tiles this block sweeps
+  int left = work;
   for (int pass = 0; pass < n_pass; ++pass) {
     const int qt = pass == 0 ? n_qt - 1 - pair : pair;  // the longer row of tiles first
     const int q0 = qt * 64 + wave * 16;
@@ -793,6 +799,7 @@ __global__ __launch_bounds__(256) WHA_DQ_WPE void attn_bwd_dq_dma_kernel(const f
     auto step = [&](int kt, const float* Ks, float* Kn) {
       wait_vmem();
       __syncthreads();  // K tile kt is in LDS; every wave is done with tile kt-1
+      prio_by_remaining(left--, work);
 #pragma unroll
       for (int c = 0; c < 4; ++c) dcur[c] = dnext[c];
       if (kt + 1 < n_kt) {

@@ -240,6 +240,10 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
   };
 
   const int n_pass = (n_qt - 1 - pair != pair) ? 2 : 1;
+  // sub-tiles this block sweeps, and how many it has left
+  auto subs_of = [&](int qt) { return (min(L.T, (qt + 1) * 64) + BSUB - 1) / BSUB; };
+  const int work = subs_of(n_qt - 1 - pair) + (n_pass == 2 ? subs_of(pair) : 0);
+  int left = work;
   for (int pass = 0; pass < n_pass; ++pass) {
     const int qt = pass == 0 ? n_qt - 1 - pair : pair;  // the longer row of tiles first
     const int q0 = qt * 64 + wave * 16;                  // first query of this wave
@@ -334,6 +338,7 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
     auto step = [&](int st, const float* Ks, const float* Vs, float* Kn, float* Vn) {
       wait_vmem();
       __syncthreads();  // sub-tile st is in LDS; every wave is done with sub-tile st-1
+      prio_by_remaining(left--, work);
       if (st + 1 < n_sub) fetch(st + 1, Kn, Vn);
       const int k0 = st * BSUB;
       if (k0 > q0 + 15) return;  // every key follows every query of the wave

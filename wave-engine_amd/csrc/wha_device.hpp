@@ -35,6 +35,9 @@
 // Scheduling fence between the phases of a loop body: keeps the machine
 // scheduler from hoisting every LDS operand read of an iteration to its top,
 // which costs registers (and occupancy) for no gain.
+#ifndef WHA_PRIO
+#define WHA_PRIO 1
+#endif
 #ifndef WHA_FENCE
 #define WHA_FENCE() __builtin_amdgcn_sched_barrier(0)
 #endif
@@ -238,6 +241,22 @@ __device__ __forceinline__ void dma_dword(const float* gsrc, float* lds_base) {
   __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)gsrc,
                                    (void __attribute__((address_space(3)))*)lds_base, 4, 0, 0);
 }
+// Wave priority from the share of a block's work still ahead of it
+// (remaining / total in quarters -> s_setprio 3 .. 0).  The instruction
+// arbiter otherwise favours the oldest waves, so of the blocks sharing a CU the
+// first-dispatched one races ahead and the last one finishes alone, with the
+// MFMA pipe mostly idle; ranking by remaining work keeps blocks of equal work
+// finishing together.
+__device__ __forceinline__ void prio_by_remaining(int remaining, int total) {
+#if WHA_PRIO
+  const int q = 4 * remaining;
+  if (q > 3 * total) __builtin_amdgcn_s_setprio(3);
+  else if (q > 2 * total) __builtin_amdgcn_s_setprio(2);
+  else if (q > total) __builtin_amdgcn_s_setprio(1);
+  else __builtin_amdgcn_s_setprio(0);
+#endif
+}
+
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
