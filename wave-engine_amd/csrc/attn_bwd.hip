@@ -794,14 +794,14 @@ __global__ __launch_bounds__(256) WHA_DQ_WPE void attn_bwd_dq_dma_kernel(const f
     floatx4 acc[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float4 dcur[4], dnext[4];
+    // dS of even tiles in dA, odd tiles in dB (the two unrolled steps swap
+    // roles, so no register copies)
+    float4 dA[4], dB[4];
 
-    auto step = [&](int kt, const float* Ks, float* Kn) {
+    auto step = [&](int kt, const float* Ks, float* Kn, const float4* dcur, float4* dnext) {
       wait_vmem();
       __syncthreads();  // K tile kt is in LDS; every wave is done with tile kt-1
       prio_by_remaining(left--, work);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) dcur[c] = dnext[c];
       if (kt + 1 < n_kt) {
         fetch(kt + 1, Kn);
         load_ds(kt + 1, dnext);
@@ -839,10 +839,10 @@ __global__ __launch_bounds__(256) WHA_DQ_WPE void attn_bwd_dq_dma_kernel(const f
 
     __syncthreads();  // the previous pass's last tile has been read by every wave
     fetch(0, Ks0);
-    load_ds(0, dnext);
+    load_ds(0, dA);
     for (int kt = 0; kt < n_kt; kt += 2) {
-      step(kt, Ks0, Ks1);
-      if (kt + 1 < n_kt) step(kt + 1, Ks1, Ks0);
+      step(kt, Ks0, Ks1, dA, dB);
+      if (kt + 1 < n_kt) step(kt + 1, Ks1, Ks0, dB, dA);
     }
     store_row_frag<DP, true>(dQ + base, qrow, L.T, L.D, L.st, g, acc, scale);
   }
