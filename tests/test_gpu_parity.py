@@ -50,7 +50,7 @@ def report(tag, got, ref32, ref64=None):
 
 SMALL = [(1, 1, 1, 64), (1, 2, 17, 64), (2, 3, 63, 48), (1, 2, 65, 42), (2, 2, 100, 64),
          (1, 1, 257, 128), (2, 2, 130, 32), (1, 1, 64, 16), (1, 4, 200, 8), (1, 2, 129, 100),
-         (3, 1, 48, 64)]
+         (3, 1, 48, 64), (2, 2, 97, 56), (1, 3, 40, 52)]
 
 
 @pytest.mark.parametrize("B,H,T,D", SMALL)

@@ -532,7 +532,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
 #ifndef WHA_DMA_WPE
 #define WHA_DMA_WPE __attribute__((amdgpu_waves_per_eu(3)))
 #endif
-template <bool DS_OUT>
+template <bool DS_OUT, bool PADQ>
 __global__ __launch_bounds__(256) WHA_DMA_WPE void attn_bwd_dkv_dma_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ stats, float* __restrict__ dK,
@@ -567,10 +567,13 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE void attn_bwd_dkv_dma_kernel(
   // sub-tile's first row; the last sub-tile clamps rows to T-1.
   int rrow[2];
   uint32_t roff[2];
+  bool pad[2];  // PADQ: this lane's quad lies past the head dim (fetched from g_zero_quad)
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     rrow[u] = 4 * (2 * wave + u) + (lane >> 4);
-    roff[u] = (uint32_t)(rrow[u] * L.st + 4 * ((lane & 15) ^ (rrow[u] & 11))) * 4u;
+    const int c = (lane & 15) ^ (rrow[u] & 11);
+    pad[u] = PADQ && 4 * c >= L.D;
+    roff[u] = (uint32_t)(rrow[u] * L.st + 4 * c) * 4u;
   }
   auto fetch = [&](int st, float* Qd, float* Od, float* Sd) {
     const int q0 = st * BSUB;
@@ -584,8 +587,11 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE void attn_bwd_dkv_dma_kernel(
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      dma_quad(reinterpret_cast<const float*>(qs + off[u]), Qd + 256 * (2 * wave + u));
-      dma_quad(reinterpret_cast<const float*>(os + off[u]), Od + 256 * (2 * wave + u));
+      const float* qp = reinterpret_cast<const float*>(qs + off[u]);
+      const float* op = reinterpret_cast<const float*>(os + off[u]);
+      if (PADQ && pad[u]) qp = op = g_zero_quad;
+      dma_quad(qp, Qd + 256 * (2 * wave + u));
+      dma_quad(op, Od + 256 * (2 * wave + u));
     }
     if (wave == 0) dma_dword(stg + st * 64 + lane, Sd);
   };
@@ -731,7 +737,7 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE void attn_bwd_dkv_dma_kernel(
 #ifndef WHA_DQ_WPE
 #define WHA_DQ_WPE
 #endif
-template <bool UNUSED = false>
+template <bool PADQ>
 __global__ __launch_bounds__(256) WHA_DQ_WPE void attn_bwd_dq_dma_kernel(const float* __restrict__ K,
                                                               const float* __restrict__ DS,
                                                               float* __restrict__ dQ, View L, float scale) {
@@ -756,10 +762,13 @@ __global__ __launch_bounds__(256) WHA_DQ_WPE void attn_bwd_dq_dma_kernel(const f
   // (u = 0..3): row 4(4w+u) + lane/16, position lane%16 <- logical quad
   // (lane%16) ^ (row & 11); byte offsets from the tile's first row
   uint32_t koff[4];
+  bool pad[4];  // PADQ: this lane's quad lies past the head dim (fetched from g_zero_quad)
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int r = 4 * (4 * wave + u) + (lane >> 4);
-    koff[u] = (uint32_t)(r * L.st + 4 * ((lane & 15) ^ (r & 11))) * 4u;
+    const int c = (lane & 15) ^ (r & 11);
+    pad[u] = PADQ && 4 * c >= L.D;
+    koff[u] = (uint32_t)(r * L.st + 4 * c) * 4u;
   }
   auto fetch = [&](int kt, float* Kd) {
     const char* ks = kg + kt * tile_bytes;
@@ -768,11 +777,17 @@ __global__ __launch_bounds__(256) WHA_DQ_WPE void attn_bwd_dq_dma_kernel(const f
       for (int u = 0; u < 4; ++u) {
         const int r = 4 * (4 * wave + u) + (lane >> 4);
         const uint32_t off = (uint32_t)((min(kt * BN + r, L.T - 1) - kt * BN) * L.st + 4 * ((lane & 15) ^ (r & 11))) * 4u;
-        dma_quad(reinterpret_cast<const float*>(ks + off), Kd + 256 * (4 * wave + u));
+        const float* kp = reinterpret_cast<const float*>(ks + off);
+        if (PADQ && pad[u]) kp = g_zero_quad;
+        dma_quad(kp, Kd + 256 * (4 * wave + u));
       }
     } else {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) dma_quad(reinterpret_cast<const float*>(ks + koff[u]), Kd + 256 * (4 * wave + u));
+      for (int u = 0; u < 4; ++u) {
+        const float* kp = reinterpret_cast<const float*>(ks + koff[u]);
+        if (PADQ && pad[u]) kp = g_zero_quad;
+        dma_quad(kp, Kd + 256 * (4 * wave + u));
+      }
     }
   };
 
@@ -940,6 +955,37 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_ds_kernel(const float* __
 
 namespace {
 
+// Head dims dma_head_dim() accepts, 128-bit operands, dS buffer present: row
+// statistics in 32-row blocks, the direct-to-LDS key-stationary kernel (dK,
+// dV, dS), then dQ from dS.
+template <bool PADQ>
+hipError_t bwd_dma_t(const float* q, const float* k, const float* v, const float* o, const float* d_o,
+                     const float* lse, float* dq, float* dk, float* dv, float* stats, float* ds, const View& L,
+                     float scale, hipStream_t stream) {
+  const float sl2 = (float)((double)scale * 1.4426950408889634);
+  const int n_t64 = (L.T + 63) / 64;
+  const dim3 grid((unsigned)((n_t64 + 1) / 2 * L.B * L.H));
+  hipError_t e;
+  {
+    TimingScope ts("attn_bwd_delta", stream);
+    const int64_t rows = (int64_t)L.B * L.H * ((L.T + 31) / 32 * 32);
+    hipLaunchKernelGGL(attn_bwd_stats_kernel, dim3((unsigned)((rows + 16 * kDeltaRows - 1) / (16 * kDeltaRows))),
+                       dim3(256), 0, stream, o, d_o, lse, stats, L);
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) return e;
+  {
+    TimingScope ts("attn_bwd_dkv", stream);
+    hipLaunchKernelGGL((attn_bwd_dkv_dma_kernel<true, PADQ>), grid, dim3(256), 0, stream, q, k, v, d_o,
+                       (const float*)stats, dk, dv, ds, L, scale, sl2);
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) return e;
+  TimingScope ts("attn_bwd_dq", stream);
+  hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<PADQ>), grid, dim3(256), 0, stream, k, (const float*)ds, dq, L, scale);
+  return hipGetLastError();
+}
+
 template <int DP, bool VEC>
 hipError_t bwd_fused_t(const float* q, const float* k, const float* v, const float* o,
                        const float* d_o, const float* lse, float* dq, float* dk, float* dv,
@@ -949,30 +995,6 @@ hipError_t bwd_fused_t(const float* q, const float* k, const float* v, const flo
   const int n_qt = (L.T + NWQ * 16 - 1) / (NWQ * 16);
   const int n_kt = (L.T + NWK * 16 - 1) / (NWK * 16);
   hipError_t e;
-  if (ds != nullptr && WHA_DKV_DMA && DP == 64 && VEC && L.D == 64) {
-    // head dim 64 with 128-bit operands: row statistics in 32-row blocks, the
-    // direct-to-LDS key-stationary kernel (dK, dV, dS), then dQ from dS
-    {
-      TimingScope ts("attn_bwd_delta", stream);
-      const int64_t rows = (int64_t)L.B * L.H * ((L.T + 31) / 32 * 32);
-      hipLaunchKernelGGL(attn_bwd_stats_kernel, dim3((unsigned)((rows + 16 * kDeltaRows - 1) / (16 * kDeltaRows))),
-                         dim3(256), 0, stream, o, d_o, lse, delta, L);
-      e = hipGetLastError();
-    }
-    if (e != hipSuccess) return e;
-    {
-      TimingScope ts("attn_bwd_dkv", stream);
-      hipLaunchKernelGGL((attn_bwd_dkv_dma_kernel<true>), dim3((unsigned)((n_kt + 1) / 2 * L.B * L.H)), dim3(256),
-                         0, stream, q, k, v, d_o, (const float*)delta, dk, dv, ds, L, scale, sl2);
-      e = hipGetLastError();
-    }
-    if (e != hipSuccess) return e;
-    TimingScope ts("attn_bwd_dq", stream);
-    const int n_qt64 = (L.T + 63) / 64;
-    hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<>), dim3((unsigned)((n_qt64 + 1) / 2 * L.B * L.H)), dim3(256), 0,
-                       stream, k, (const float*)ds, dq, L, scale);
-    return hipGetLastError();
-  }
   {
     TimingScope ts("attn_bwd_delta", stream);
     e = delta_launch(o, d_o, delta, L, stream);
@@ -1086,6 +1108,9 @@ hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const
                            const float* d_o, const float* lse, float* dq, float* dk, float* dv,
                            float* delta, float* ds, const View& L, bool vec, float scale,
                            hipStream_t stream) {
+  if (WHA_DKV_DMA && ds != nullptr && vec && dma_head_dim(L.D))
+    return L.D == 64 ? bwd_dma_t<false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream)
+                     : bwd_dma_t<true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream);
 #define WHA_BWD(DP)                                                                                 \
   return vec ? bwd_fused_t<DP, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream) \
              : bwd_fused_t<DP, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream)

@@ -185,7 +185,7 @@ constexpr float kLazyMax = 8.f;
 #ifndef WHA_FWD_WPE
 #define WHA_FWD_WPE __attribute__((amdgpu_waves_per_eu(3)))
 #endif
-template <bool UNUSED = false>
+template <bool PADQ>
 __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const float* __restrict__ Q,
                                                                      const float* __restrict__ K,
                                                                      const float* __restrict__ V,
@@ -217,10 +217,13 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
   // (lane%16) ^ (row & 11); byte offsets from the sub-tile's first row
   int rrow[2];
   uint32_t roff[2];
+  bool pad[2];  // PADQ: this lane's quad lies past the head dim (fetched from g_zero_quad)
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     rrow[u] = 4 * (2 * wave + u) + (lane >> 4);
-    roff[u] = (uint32_t)(rrow[u] * L.st + 4 * ((lane & 15) ^ (rrow[u] & 11))) * 4u;
+    const int c = (lane & 15) ^ (rrow[u] & 11);
+    pad[u] = PADQ && 4 * c >= L.D;
+    roff[u] = (uint32_t)(rrow[u] * L.st + 4 * c) * 4u;
   }
   auto fetch = [&](int st, float* Kd, float* Vd) {
     const int k0 = st * BSUB;
@@ -234,8 +237,11 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      dma_quad(reinterpret_cast<const float*>(ks + off[u]), Kd + 256 * (2 * wave + u));
-      dma_quad(reinterpret_cast<const float*>(vs + off[u]), Vd + 256 * (2 * wave + u));
+      const float* kp = reinterpret_cast<const float*>(ks + off[u]);
+      const float* vp = reinterpret_cast<const float*>(vs + off[u]);
+      if (PADQ && pad[u]) kp = vp = g_zero_quad;
+      dma_quad(kp, Kd + 256 * (2 * wave + u));
+      dma_quad(vp, Vd + 256 * (2 * wave + u));
     }
   };
 
@@ -376,19 +382,22 @@ static hipError_t launch_fwd_t(const float* q, const float* k, const float* v, f
 
 hipError_t launch_attn_fwd(const float* q, const float* k, const float* v, float* o, float* lse,
                            const View& L, bool vec, float scale, hipStream_t stream) {
+  if (WHA_FWD_DMA && vec && dma_head_dim(L.D)) {
+    const int n_qt = (L.T + 63) / 64;
+    const float scale_log2 = (float)((double)scale * 1.4426950408889634);
+    const dim3 grid((unsigned)((n_qt + 1) / 2 * L.B * L.H));
+    TimingScope ts("attn_fwd", stream);
+    if (L.D == 64)
+      hipLaunchKernelGGL((attn_fwd_dma_kernel<false>), grid, dim3(256), 0, stream, q, k, v, o, lse, L, scale_log2);
+    else
+      hipLaunchKernelGGL((attn_fwd_dma_kernel<true>), grid, dim3(256), 0, stream, q, k, v, o, lse, L, scale_log2);
+    return hipGetLastError();
+  }
   switch (padded_dim(L.D)) {
     case 48:
       return vec ? launch_fwd_t<48, 4, true>(q, k, v, o, lse, L, scale, stream)
                  : launch_fwd_t<48, 4, false>(q, k, v, o, lse, L, scale, stream);
     case 64:
-      if (vec && L.D == 64 && WHA_FWD_DMA) {
-        const int n_qt = (L.T + 63) / 64;
-        const float scale_log2 = (float)((double)scale * 1.4426950408889634);
-        TimingScope ts("attn_fwd", stream);
-        hipLaunchKernelGGL((attn_fwd_dma_kernel<>), dim3((unsigned)((n_qt + 1) / 2 * L.B * L.H)), dim3(256), 0,
-                           stream, q, k, v, o, lse, L, scale_log2);
-        return hipGetLastError();
-      }
       return vec ? launch_fwd_t<64, 4, true>(q, k, v, o, lse, L, scale, stream)
                  : launch_fwd_t<64, 4, false>(q, k, v, o, lse, L, scale, stream);
     case 128:

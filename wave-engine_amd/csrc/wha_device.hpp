@@ -257,6 +257,11 @@ __device__ __forceinline__ void prio_by_remaining(int remaining, int total) {
 #endif
 }
 
+// 16 zero bytes in device memory: the DMA source of LDS quads past the head
+// dimension when a head dim below 64 runs on the 64-wide kernels (the pad
+// must hold exact zeros: a finite operand times a zero pad, never times data)
+static __device__ __align__(16) float g_zero_quad[4];
+
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
