@@ -529,18 +529,22 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
 // key-tile x query-tile products for every block), so equal blocks fill the
 // CUs to the end instead of leaving a tail of short blocks;
 // grid = B*H*ceil(n_kt/2).
+// three blocks per CU at head dim 64, two at 128 (LDS and VGPR budgets)
 #ifndef WHA_DMA_WPE
-#define WHA_DMA_WPE __attribute__((amdgpu_waves_per_eu(3)))
+#define WHA_DMA_WPE(DP) __attribute__((amdgpu_waves_per_eu((DP) == 64 ? 3 : 2)))
 #endif
-template <bool DS_OUT, bool PADQ>
-__global__ __launch_bounds__(256) WHA_DMA_WPE void attn_bwd_dkv_dma_kernel(
+template <int DP, bool DS_OUT, bool PADQ>
+__global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ stats, float* __restrict__ dK,
     float* __restrict__ dV, float* __restrict__ DS, View L, float scale, float scale_log2) {
-  constexpr int DP = 64, DG = 16, NDT = 4;
-  constexpr int BSUB = 32;         // queries per sub-tile
-  constexpr int TILE = BSUB * DP;  // floats per operand sub-tile
-  static_assert(Lds<DP, true>::SWZ, "the DMA layout is the swizzled 64-float row");
+  constexpr int DG = DP / 4, NDT = DP / 16;
+  constexpr int QPR = DP / 4;            // quads per row
+  constexpr int BSUB = 32;               // queries per sub-tile
+  constexpr int TILE = BSUB * DP;        // floats per operand sub-tile
+  constexpr int NF = BSUB * QPR / 256;   // DMA instructions per wave per operand
+  using LT = Lds<DP, true>;
+  static_assert(LT::SWZ, "the DMA layout is the swizzled unpadded row");
   __shared__ __align__(16) float Qs0[TILE], Qs1[TILE];
   __shared__ __align__(16) float Os0[TILE], Os1[TILE];
   __shared__ __align__(16) float St0[2 * BSUB], St1[2 * BSUB];
@@ -561,37 +565,40 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE void attn_bwd_dkv_dma_kernel(
   const int wave = tid >> 6, lane = tid & 63;
   const int lq = lane & 15, g = lane >> 4;
 
-  // This lane's fetch: wave w fills LDS quads 64(2w+u) .. +63 of both operands
-  // (u = 0, 1): row r = 4(2w+u) + lane/16 of the sub-tile, position lane%16,
-  // which holds logical quad (lane%16) ^ (r & 11).  Byte offsets from the
-  // sub-tile's first row; the last sub-tile clamps rows to T-1.
-  int rrow[2];
-  uint32_t roff[2];
-  bool pad[2];  // PADQ: this lane's quad lies past the head dim (fetched from g_zero_quad)
+  // This lane's fetch: wave w fills LDS quads 64(NF*w+u) .. +63 of both
+  // operands (u < NF): quad p = 64(NF*w+u) + lane is row p / QPR of the
+  // sub-tile, position p % QPR, which holds logical quad (p % QPR) ^ swz(row).
+  // Byte offsets from the sub-tile's first row; the last sub-tile clamps rows
+  // to T-1.
+  int rrow[NF], rcol[NF];
+  uint32_t roff[NF];
+  bool pad[NF];  // PADQ: this lane's quad lies past the head dim (fetched from g_zero_quad)
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    rrow[u] = 4 * (2 * wave + u) + (lane >> 4);
-    const int c = (lane & 15) ^ (rrow[u] & 11);
-    pad[u] = PADQ && 4 * c >= L.D;
-    roff[u] = (uint32_t)(rrow[u] * L.st + 4 * c) * 4u;
+  for (int u = 0; u < NF; ++u) {
+    const int p = 64 * (NF * wave + u) + lane;
+    rrow[u] = p / QPR;
+    rcol[u] = (p % QPR) ^ LT::swz(rrow[u]);
+    pad[u] = PADQ && 4 * rcol[u] >= L.D;
+    roff[u] = (uint32_t)(rrow[u] * L.st + 4 * rcol[u]) * 4u;
   }
   auto fetch = [&](int st, float* Qd, float* Od, float* Sd) {
     const int q0 = st * BSUB;
     const char* qs = qg + st * sub_bytes;
     const char* os = og + st * sub_bytes;
-    uint32_t off[2] = {roff[0], roff[1]};
+    uint32_t off[NF];
+#pragma unroll
+    for (int u = 0; u < NF; ++u) off[u] = roff[u];
     if (q0 + BSUB > L.T) {  // last sub-tile: rows past T read row T-1
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-        off[u] = (uint32_t)((min(q0 + rrow[u], L.T - 1) - q0) * L.st + 4 * ((lane & 15) ^ (rrow[u] & 11))) * 4u;
+      for (int u = 0; u < NF; ++u) off[u] = (uint32_t)((min(q0 + rrow[u], L.T - 1) - q0) * L.st + 4 * rcol[u]) * 4u;
     }
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < NF; ++u) {
       const float* qp = reinterpret_cast<const float*>(qs + off[u]);
       const float* op = reinterpret_cast<const float*>(os + off[u]);
       if (PADQ && pad[u]) qp = op = g_zero_quad;
-      dma_quad(qp, Qd + 256 * (2 * wave + u));
-      dma_quad(op, Od + 256 * (2 * wave + u));
+      dma_quad(qp, Qd + 256 * (NF * wave + u));
+      dma_quad(op, Od + 256 * (NF * wave + u));
     }
     if (wave == 0) dma_dword(stg + st * 64 + lane, Sd);
   };
@@ -634,8 +641,8 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE void attn_bwd_dkv_dma_kernel(
         dp[mt] = *reinterpret_cast<const floatx4*>(&Sts[BSUB + 16 * mt + 4 * g]);
 #pragma unroll
         for (int j = 0; j < DG / 4; ++j) {
-          const float4 a = lds_read_quad<DP, true>(Qs, 16 * mt + lq, 4 * g + j);
-          const float4 c = lds_read_quad<DP, true>(Os, 16 * mt + lq, 4 * g + j);
+          const float4 a = lds_read_quad<DP, true>(Qs, 16 * mt + lq, (DG / 4) * g + j);
+          const float4 c = lds_read_quad<DP, true>(Os, 16 * mt + lq, (DG / 4) * g + j);
           s[mt] = mfma4(a.x, kf[4 * j + 0], s[mt]);
           s[mt] = mfma4(a.y, kf[4 * j + 1], s[mt]);
           s[mt] = mfma4(a.z, kf[4 * j + 2], s[mt]);
@@ -714,8 +721,8 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE void attn_bwd_dkv_dma_kernel(
       step(st, Qs0, Os0, St0, Qs1, Os1, St1);
       if (st + 1 < n_st) step(st + 1, Qs1, Os1, St1, Qs0, Os0, St0);
     }
-    store_row_frag<DP, true>(dK + base, krow, L.T, L.D, L.st, g, dkacc, scale);
-    store_row_frag<DP, true>(dV + base, krow, L.T, L.D, L.st, g, dvacc, 1.f);
+    store_row_frag_split<DP>(dK + base, krow, L.T, L.D, L.st, g, dkacc, scale);
+    store_row_frag_split<DP>(dV + base, krow, L.T, L.D, L.st, g, dvacc, 1.f);
   }
 }
 
@@ -734,15 +741,15 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE void attn_bwd_dkv_dma_kernel(
 //     that are never stored.
 // A block handles query tiles p and n_qt-1-p (n_qt+1 key tiles of work for
 // every block); grid = B*H*ceil(n_qt/2).
-#ifndef WHA_DQ_WPE
-#define WHA_DQ_WPE
-#endif
-template <bool PADQ>
-__global__ __launch_bounds__(256) WHA_DQ_WPE void attn_bwd_dq_dma_kernel(const float* __restrict__ K,
+template <int DP, bool PADQ>
+__global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __restrict__ K,
                                                               const float* __restrict__ DS,
                                                               float* __restrict__ dQ, View L, float scale) {
-  constexpr int DP = 64, NDT = 4, BN = 64;
+  constexpr int NDT = DP / 16, BN = 64;
+  constexpr int QPR = DP / 4;            // quads per row
   constexpr int TILE = BN * DP;
+  constexpr int NF = BN * QPR / 256;     // DMA instructions per wave per tile
+  using LT = Lds<DP, true>;
   __shared__ __align__(16) float Ks0[TILE], Ks1[TILE];
 
   const int BH = L.B * L.H;
@@ -758,35 +765,36 @@ __global__ __launch_bounds__(256) WHA_DQ_WPE void attn_bwd_dq_dma_kernel(const f
   const int wave = tid >> 6, lane = tid & 63;
   const int lq = lane & 15, g = lane >> 4;
 
-  // this lane's part of a K tile fetch: wave w fills LDS quads 64(4w+u) .. +63
-  // (u = 0..3): row 4(4w+u) + lane/16, position lane%16 <- logical quad
-  // (lane%16) ^ (row & 11); byte offsets from the tile's first row
-  uint32_t koff[4];
-  bool pad[4];  // PADQ: this lane's quad lies past the head dim (fetched from g_zero_quad)
+  // this lane's part of a K tile fetch: wave w fills LDS quads 64(NF*w+u) ..
+  // +63 (u < NF): quad p = 64(NF*w+u) + lane is row p / QPR, position p % QPR
+  // <- logical quad (p % QPR) ^ swz(row); byte offsets from the tile's first row
+  int krow_[NF], kcol[NF];
+  uint32_t koff[NF];
+  bool pad[NF];  // PADQ: this lane's quad lies past the head dim (fetched from g_zero_quad)
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int r = 4 * (4 * wave + u) + (lane >> 4);
-    const int c = (lane & 15) ^ (r & 11);
-    pad[u] = PADQ && 4 * c >= L.D;
-    koff[u] = (uint32_t)(r * L.st + 4 * c) * 4u;
+  for (int u = 0; u < NF; ++u) {
+    const int p = 64 * (NF * wave + u) + lane;
+    krow_[u] = p / QPR;
+    kcol[u] = (p % QPR) ^ LT::swz(krow_[u]);
+    pad[u] = PADQ && 4 * kcol[u] >= L.D;
+    koff[u] = (uint32_t)(krow_[u] * L.st + 4 * kcol[u]) * 4u;
   }
   auto fetch = [&](int kt, float* Kd) {
     const char* ks = kg + kt * tile_bytes;
     if ((kt + 1) * BN > L.T) {  // last tile: rows past T read row T-1
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int r = 4 * (4 * wave + u) + (lane >> 4);
-        const uint32_t off = (uint32_t)((min(kt * BN + r, L.T - 1) - kt * BN) * L.st + 4 * ((lane & 15) ^ (r & 11))) * 4u;
+      for (int u = 0; u < NF; ++u) {
+        const uint32_t off = (uint32_t)((min(kt * BN + krow_[u], L.T - 1) - kt * BN) * L.st + 4 * kcol[u]) * 4u;
         const float* kp = reinterpret_cast<const float*>(ks + off);
         if (PADQ && pad[u]) kp = g_zero_quad;
-        dma_quad(kp, Kd + 256 * (4 * wave + u));
+        dma_quad(kp, Kd + 256 * (NF * wave + u));
       }
     } else {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < NF; ++u) {
         const float* kp = reinterpret_cast<const float*>(ks + koff[u]);
         if (PADQ && pad[u]) kp = g_zero_quad;
-        dma_quad(kp, Kd + 256 * (4 * wave + u));
+        dma_quad(kp, Kd + 256 * (NF * wave + u));
       }
     }
   };
@@ -859,13 +867,14 @@ __global__ __launch_bounds__(256) WHA_DQ_WPE void attn_bwd_dq_dma_kernel(const f
       step(kt, Ks0, Ks1, dA, dB);
       if (kt + 1 < n_kt) step(kt + 1, Ks1, Ks0, dB, dA);
     }
-    store_row_frag<DP, true>(dQ + base, qrow, L.T, L.D, L.st, g, acc, scale);
+    store_row_frag_split<DP>(dQ + base, qrow, L.T, L.D, L.st, g, acc, scale);
   }
 }
 
 // Query-stationary dQ from stored dS: dQ^T[d][q] += K^T[d][key] dS^T[key][q] over
 // the causal 64-key tiles; K tiles staged through LDS (A operand, d = NDT*m + dt
-// on MFMA rows), dS read from the workspace with 128-bit loads straight into the
+// on MFMA rows; the swizzled layout at head dim 64, where it keeps that d
+// layout), dS read from the workspace with 128-bit loads straight into the
 // B operand (k-step (c, e) <-> key 16c + 4g + e), one tile ahead.
 template <int DP, int NW, bool VEC>
 __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_ds_kernel(const float* __restrict__ K,
@@ -874,7 +883,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_ds_kernel(const float* __
   constexpr int NT = NW * 64;
   constexpr int BM = NW * 16;
   constexpr int BN = 64;
-  constexpr int LD = Lds<DP, true>::PITCH;
+  constexpr int LD = Lds<DP, DP == 64>::PITCH;
   constexpr int NDT = DP / 16;
   __shared__ __align__(16) float Ks[BN * LD];
 
@@ -918,7 +927,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_ds_kernel(const float* __
 
   for (int kt = 0; kt < n_kt; ++kt) {
     __syncthreads();
-    ks.template store_tile<true>(Ks, tid);
+    ks.template store_tile<DP == 64>(Ks, tid);
     __syncthreads();
     if (kt + 1 < n_kt) {
       ks.load(K + base, (kt + 1) * BN, L.T, L.D, L.st, tid);
@@ -935,8 +944,8 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_ds_kernel(const float* __
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float ka[NDT], kb[NDT];
-          lds_read_seg<DP, NDT, true>(Ks, 16 * c + 4 * g + e, lq, ka);
-          lds_read_seg<DP, NDT, true>(Ks, 16 * (c + 1) + 4 * g + e, lq, kb);
+          lds_read_seg<DP, NDT, DP == 64>(Ks, 16 * c + 4 * g + e, lq, ka);
+          lds_read_seg<DP, NDT, DP == 64>(Ks, 16 * (c + 1) + 4 * g + e, lq, kb);
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt) {
             acc[dt] = mfma4(ka[dt], d0[e], acc[dt]);
@@ -958,7 +967,7 @@ namespace {
 // Head dims dma_head_dim() accepts, 128-bit operands, dS buffer present: row
 // statistics in 32-row blocks, the direct-to-LDS key-stationary kernel (dK,
 // dV, dS), then dQ from dS.
-template <bool PADQ>
+template <int DP, bool PADQ>
 hipError_t bwd_dma_t(const float* q, const float* k, const float* v, const float* o, const float* d_o,
                      const float* lse, float* dq, float* dk, float* dv, float* stats, float* ds, const View& L,
                      float scale, hipStream_t stream) {
@@ -976,13 +985,13 @@ hipError_t bwd_dma_t(const float* q, const float* k, const float* v, const float
   if (e != hipSuccess) return e;
   {
     TimingScope ts("attn_bwd_dkv", stream);
-    hipLaunchKernelGGL((attn_bwd_dkv_dma_kernel<true, PADQ>), grid, dim3(256), 0, stream, q, k, v, d_o,
+    hipLaunchKernelGGL((attn_bwd_dkv_dma_kernel<DP, true, PADQ>), grid, dim3(256), 0, stream, q, k, v, d_o,
                        (const float*)stats, dk, dv, ds, L, scale, sl2);
     e = hipGetLastError();
   }
   if (e != hipSuccess) return e;
   TimingScope ts("attn_bwd_dq", stream);
-  hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<PADQ>), grid, dim3(256), 0, stream, k, (const float*)ds, dq, L, scale);
+  hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<DP, PADQ>), grid, dim3(256), 0, stream, k, (const float*)ds, dq, L, scale);
   return hipGetLastError();
 }
 
@@ -1108,9 +1117,12 @@ hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const
                            const float* d_o, const float* lse, float* dq, float* dk, float* dv,
                            float* delta, float* ds, const View& L, bool vec, float scale,
                            hipStream_t stream) {
-  if (WHA_DKV_DMA && ds != nullptr && vec && dma_head_dim(L.D))
-    return L.D == 64 ? bwd_dma_t<false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream)
-                     : bwd_dma_t<true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream);
+  if (WHA_DKV_DMA && ds != nullptr && vec && dma_head_dim(L.D)) {
+    if (L.D == 64) return bwd_dma_t<64, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream);
+    if (L.D < 64) return bwd_dma_t<64, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream);
+    if (L.D == 128) return bwd_dma_t<128, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream);
+    return bwd_dma_t<128, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream);
+  }
 #define WHA_BWD(DP)                                                                                 \
   return vec ? bwd_fused_t<DP, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream) \
              : bwd_fused_t<DP, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream)

@@ -165,7 +165,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
     LSE[(int64_t)bh * L.T + qrow] = (m_i + log2f(l_sum)) * kLn2;
 }
 
-// Forward for head dim 64 with 128-bit-aligned operands, arranged like the
+// Forward for head dims 52..64 and 68..128 (128-bit-aligned operands), arranged like the
 // backward's direct-to-LDS kernels because on gfx950 every VALU instruction
 // costs MFMA issue time:
 //   - 32-key sub-tiles of K and V go from global memory straight into LDS
@@ -185,16 +185,21 @@ constexpr float kLazyMax = 8.f;
 #ifndef WHA_FWD_WPE
 #define WHA_FWD_WPE __attribute__((amdgpu_waves_per_eu(3)))
 #endif
-template <bool PADQ>
+template <int DP, bool PADQ>
 __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const float* __restrict__ Q,
                                                                      const float* __restrict__ K,
                                                                      const float* __restrict__ V,
                                                                      float* __restrict__ O,
                                                                      float* __restrict__ LSE, View L,
                                                                      float scale_log2) {
-  constexpr int DP = 64, DG = 16, NDT = 4;
-  constexpr int BSUB = 32;         // keys per sub-tile
-  constexpr int TILE = BSUB * DP;  // floats per operand sub-tile
+  constexpr int DG = DP / 4, NDT = DP / 16;
+  constexpr int QPR = DP / 4;            // quads per row
+  constexpr int BSUB = 2048 / DP;        // keys per sub-tile (8 KB per operand)
+  constexpr int NKT = BSUB / 16;         // 16-key groups per sub-tile
+  constexpr int TILE = BSUB * DP;        // floats per operand sub-tile
+  constexpr int NF = BSUB * QPR / 256;   // DMA instructions per wave per operand
+  using LT = Lds<DP, true>;
+  static_assert(NF == 2 && LT::SWZ, "sub-tiles of 512 quads in the swizzled unpadded layout");
   __shared__ __align__(16) float Ks0[TILE], Ks1[TILE];
   __shared__ __align__(16) float Vs0[TILE], Vs1[TILE];
 
@@ -213,17 +218,18 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
   const int lq = lane & 15, g = lane >> 4;
 
   // this lane's fetch: wave w fills LDS quads 64(2w+u) .. +63 of K and V
-  // (u = 0, 1): row 4(2w+u) + lane/16, position lane%16 <- logical quad
-  // (lane%16) ^ (row & 11); byte offsets from the sub-tile's first row
-  int rrow[2];
+  // (u = 0, 1): quad p = 64(2w+u) + lane is row p / QPR, position p % QPR <-
+  // logical quad (p % QPR) ^ swz(row); byte offsets from the sub-tile's first row
+  int rrow[2], rcol[2];
   uint32_t roff[2];
   bool pad[2];  // PADQ: this lane's quad lies past the head dim (fetched from g_zero_quad)
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    rrow[u] = 4 * (2 * wave + u) + (lane >> 4);
-    const int c = (lane & 15) ^ (rrow[u] & 11);
-    pad[u] = PADQ && 4 * c >= L.D;
-    roff[u] = (uint32_t)(rrow[u] * L.st + 4 * c) * 4u;
+    const int p = 64 * (2 * wave + u) + lane;
+    rrow[u] = p / QPR;
+    rcol[u] = (p % QPR) ^ LT::swz(rrow[u]);
+    pad[u] = PADQ && 4 * rcol[u] >= L.D;
+    roff[u] = (uint32_t)(rrow[u] * L.st + 4 * rcol[u]) * 4u;
   }
   auto fetch = [&](int st, float* Kd, float* Vd) {
     const int k0 = st * BSUB;
@@ -233,7 +239,7 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
     if (k0 + BSUB > L.T) {  // last sub-tile: rows past T read row T-1
 #pragma unroll
       for (int u = 0; u < 2; ++u)
-        off[u] = (uint32_t)((min(k0 + rrow[u], L.T - 1) - k0) * L.st + 4 * ((lane & 15) ^ (rrow[u] & 11))) * 4u;
+        off[u] = (uint32_t)((min(k0 + rrow[u], L.T - 1) - k0) * L.st + 4 * rcol[u]) * 4u;
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -271,13 +277,13 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
     auto compute = [&](auto masked, int k0, const float* Ks, const float* Vs) {
       constexpr bool MASKED = decltype(masked)::value;
       // S^T[key][query] in log2 units: MFMA rows are keys 16mt + lq, columns the wave's queries
-      floatx4 s[2];
+      floatx4 s[NKT];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
+      for (int mt = 0; mt < NKT; ++mt) {
         WHA_FENCE();
 #pragma unroll
         for (int j = 0; j < DG / 4; ++j) {
-          const float4 a = lds_read_quad<DP, true>(Ks, 16 * mt + lq, 4 * g + j);
+          const float4 a = lds_read_quad<DP, true>(Ks, 16 * mt + lq, (DG / 4) * g + j);
           s[mt] = mfma4(a.x, qf[4 * j + 0], j == 0 ? neg_m : s[mt]);
           s[mt] = mfma4(a.y, qf[4 * j + 1], s[mt]);
           s[mt] = mfma4(a.z, qf[4 * j + 2], s[mt]);
@@ -288,14 +294,18 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
       // lane element (mt,i): key k0 + 16mt + 4g + i of query qrow, as s - m_i
       if (MASKED) {
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
+        for (int mt = 0; mt < NKT; ++mt) {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
             s[mt][i] = (k0 + 16 * mt + 4 * g + i > key_last) ? -INFINITY : s[mt][i];
         }
       }
-      // largest shifted score of the query (its 8 keys here, then the 4 lane groups)
-      float mx = vmax3(vmax3(s[0][0], s[0][1], s[0][2]), vmax3(s[0][3], s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3]));
+      // largest shifted score of the query (its keys here, then the 4 lane groups)
+      float mx;
+      if constexpr (NKT == 2)
+        mx = vmax3(vmax3(s[0][0], s[0][1], s[0][2]), vmax3(s[0][3], s[1][0], s[1][1]), vmax2(s[1][2], s[1][3]));
+      else
+        mx = vmax3(vmax2(s[0][0], s[0][1]), s[0][2], s[0][3]);
       mx = pair_max32(pair_max16(mx));
       if (fresh) {
         // first sub-tile: the running max is this one's (k0 <= every query here,
@@ -304,7 +314,7 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
         fresh = false;
         m_i = mx;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) s[mt] -= mx;
+        for (int mt = 0; mt < NKT; ++mt) s[mt] -= mx;
         neg_m = floatx4{-m_i, -m_i, -m_i, -m_i};
       } else if (__builtin_amdgcn_ballot_w64(mx > kLazyMax) != 0) {
         // a real branch (not if-converted): rescale to the new max
@@ -316,19 +326,22 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
         for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
         m_i += d;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) s[mt] -= d;
+        for (int mt = 0; mt < NKT; ++mt) s[mt] -= d;
         neg_m = floatx4{-m_i, -m_i, -m_i, -m_i};
       }
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
+      for (int mt = 0; mt < NKT; ++mt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) s[mt][i] = fast_exp2(s[mt][i]);
       }
-      l_i += ((s[0][0] + s[0][1]) + (s[0][2] + s[0][3])) + ((s[1][0] + s[1][1]) + (s[1][2] + s[1][3]));
+      if constexpr (NKT == 2)
+        l_i += ((s[0][0] + s[0][1]) + (s[0][2] + s[0][3])) + ((s[1][0] + s[1][1]) + (s[1][2] + s[1][3]));
+      else
+        l_i += (s[0][0] + s[0][1]) + (s[0][2] + s[0][3]);
 
-      // O^T[d][query] += V^T[d][key] P^T[key][query] (d = NDT*m + dt on MFMA rows)
+      // O^T[d][query] += V^T[d][key] P^T[key][query] (MFMA rows: the d layout of lds_read_seg)
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
+      for (int mt = 0; mt < NKT; ++mt) {
         WHA_FENCE();
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -362,7 +375,7 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
     }
 
     const float l_sum = pair_sum32(pair_sum16(l_i));
-    store_row_frag<DP, true>(O + base, qrow, L.T, L.D, L.st, g, oacc, 1.f / l_sum);
+    store_row_frag_split<DP>(O + base, qrow, L.T, L.D, L.st, g, oacc, 1.f / l_sum);
     if (LSE != nullptr && g == 0 && qrow < L.T) LSE[(int64_t)bh * L.T + qrow] = (m_i + log2f(l_sum)) * kLn2;
   }
 }
@@ -388,9 +401,13 @@ hipError_t launch_attn_fwd(const float* q, const float* k, const float* v, float
     const dim3 grid((unsigned)((n_qt + 1) / 2 * L.B * L.H));
     TimingScope ts("attn_fwd", stream);
     if (L.D == 64)
-      hipLaunchKernelGGL((attn_fwd_dma_kernel<false>), grid, dim3(256), 0, stream, q, k, v, o, lse, L, scale_log2);
+      hipLaunchKernelGGL((attn_fwd_dma_kernel<64, false>), grid, dim3(256), 0, stream, q, k, v, o, lse, L, scale_log2);
+    else if (L.D < 64)
+      hipLaunchKernelGGL((attn_fwd_dma_kernel<64, true>), grid, dim3(256), 0, stream, q, k, v, o, lse, L, scale_log2);
+    else if (L.D == 128)
+      hipLaunchKernelGGL((attn_fwd_dma_kernel<128, false>), grid, dim3(256), 0, stream, q, k, v, o, lse, L, scale_log2);
     else
-      hipLaunchKernelGGL((attn_fwd_dma_kernel<true>), grid, dim3(256), 0, stream, q, k, v, o, lse, L, scale_log2);
+      hipLaunchKernelGGL((attn_fwd_dma_kernel<128, true>), grid, dim3(256), 0, stream, q, k, v, o, lse, L, scale_log2);
     return hipGetLastError();
   }
   switch (padded_dim(L.D)) {

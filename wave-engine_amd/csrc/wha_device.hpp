@@ -114,16 +114,20 @@ __device__ __forceinline__ float pair_sum32(float x) {
 // probe: a padded pitch such as DP+4 leaves both read patterns 2-way
 // conflicted).  For DP = 64 rows are unpadded and quad c of row r is stored at
 // quad c ^ (r & 11), which keeps all three patterns conflict-free for every
-// lane grouping consistent with the probe.  Kernels opt in (ALLOW_SWZ): the
+// lane grouping consistent with the probe; DP = 128 uses the XOR in swz().  Kernels opt in (ALLOW_SWZ): the
 // XOR costs per-lane address registers, which only pays where LDS traffic
 // matters more than VGPRs.  Other DP, and kernels that do not opt in, keep a
 // 4-float pad.
 template <int DP, bool ALLOW_SWZ = false>
 struct Lds {
-  static constexpr bool SWZ = WHA_LDS_SWZ && ALLOW_SWZ && DP == 64;
+  static constexpr bool SWZ = WHA_LDS_SWZ && ALLOW_SWZ && (DP == 64 || DP == 128);
   static constexpr int PITCH = SWZ ? DP : DP + WHA_LDS_PAD;
+  // XOR applied to the quad index of row r (128-float rows: rows by lane read
+  // quads 8g + j, and the contractions over rows read quads lq and lq + 16 --
+  // see lds_read_seg -- which r & 11 does not keep apart)
+  __device__ __forceinline__ static int swz(int r) { return DP == 64 ? (r & 11) : ((r & 3) | ((r >> 1) & 4)); }
   // float offset of quad c of row r
-  __device__ __forceinline__ static int at(int r, int c) { return r * PITCH + 4 * (SWZ ? (c ^ (r & 11)) : c); }
+  __device__ __forceinline__ static int at(int r, int c) { return r * PITCH + 4 * (SWZ ? (c ^ swz(r)) : c); }
   // float offset of head-dim entry d of row r (a quad-aligned group of N <= 4
   // entries starting at d stays contiguous)
   __device__ __forceinline__ static int at_d(int r, int d) { return SWZ ? at(r, d >> 2) + (d & 3) : r * PITCH + d; }
@@ -200,7 +204,10 @@ struct TileStage {
   }
 };
 
-// Reads the N head-dim entries [N*lq, N*lq + N) of row r of an Lds<DP, SW> tile.
+// Reads N head-dim entries of row r of an Lds<DP, SW> tile for lane lq: the
+// entries [N*lq, N*lq + N) (padded tiles, and swizzled 64-wide tiles where
+// N = 4), or for swizzled 128-wide tiles quads lq and lq + 16 (d = 4lq..4lq+3
+// and 64+4lq..64+4lq+3), the split layout store_row_frag_split writes back.
 template <int DP, int N, bool SW = false>
 __device__ __forceinline__ void lds_read_seg(const float* tile, int r, int lq, float* out) {
   using LT = Lds<DP, SW>;
@@ -210,8 +217,19 @@ __device__ __forceinline__ void lds_read_seg(const float* tile, int r, int lq, f
     out[1] = v.y;
     out[2] = v.z;
     out[3] = v.w;
+  } else if (LT::SWZ && N == 8) {
+    const float4 v = *reinterpret_cast<const float4*>(tile + LT::at(r, lq));
+    const float4 w = *reinterpret_cast<const float4*>(tile + LT::at(r, lq + 16));
+    out[0] = v.x;
+    out[1] = v.y;
+    out[2] = v.z;
+    out[3] = v.w;
+    out[4] = w.x;
+    out[5] = w.y;
+    out[6] = w.z;
+    out[7] = w.w;
   } else {
-    static_assert(!LT::SWZ || N == 4, "swizzled tiles are read in whole quads");
+    static_assert(!LT::SWZ || N == 4 || N == 8, "swizzled tiles are read in whole quads");
     const float* p = tile + r * LT::PITCH + N * lq;
     if (N % 4 == 0) {
 #pragma unroll
@@ -347,6 +365,32 @@ __device__ __forceinline__ void store_row_frag(float* __restrict__ base, int row
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
         if (c0 + dt < D) dst[c0 + dt] = acc[dt][i] * mul;
+    }
+  }
+}
+
+// The contraction-over-rows accumulators of a kernel that reads its A operand
+// with lds_read_seg<DP, NDT, true> (swizzled tiles): for DP = 64 the layout of
+// store_row_frag; for DP = 128 d-tile dt < 4 holds d = 4m + dt and dt >= 4
+// holds d = 64 + 4m + dt - 4 (m = MFMA row), so lane (lq, g) stores quads
+// 4g+i and 16+4g+i of row `row`.  128-bit stores, columns >= D skipped.
+template <int DP>
+__device__ __forceinline__ void store_row_frag_split(float* __restrict__ base, int row, int T, int D, int64_t st,
+                                                     int g, const floatx4* acc, float mul) {
+  if (DP == 64) {
+    store_row_frag<DP, true>(base, row, T, D, st, g, acc, mul);
+    return;
+  }
+  if (row >= T) return;
+  float* dst = base + (int64_t)row * st;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = 64 * h + 4 * (4 * g + i);
+      if (c < D)
+        *reinterpret_cast<float4*>(dst + c) = make_float4(acc[4 * h + 0][i] * mul, acc[4 * h + 1][i] * mul,
+                                                          acc[4 * h + 2][i] * mul, acc[4 * h + 3][i] * mul);
     }
   }
 }

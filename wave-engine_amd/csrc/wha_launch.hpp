@@ -23,12 +23,13 @@ inline int padded_dim(int D) {
   return 0;
 }
 
-// Head dims the 64-wide direct-to-LDS kernels serve (with 128-bit operands):
-// 64, and 52..60 with the LDS quads past D fetched as zeros (those pad to 64 in
-// the register-staged kernels too).  48 keeps its exact 48-wide kernels: padded
-// to 64 here it needs a third more MFMA work, which cancels the gain (measured
-// on the 384-dim config: 0.167 vs 0.164 ms per step).
-inline bool dma_head_dim(int D) { return D % 4 == 0 && D > 48 && D <= 64; }
+// Head dims the direct-to-LDS kernels serve (with 128-bit operands): 64 and
+// 128, and 52..60 / 68..124 on the 64- / 128-wide kernels with the LDS quads
+// past D fetched as zeros (those pad the same way in the register-staged
+// kernels).  48 keeps its exact 48-wide kernels: padded to 64 here it needs a
+// third more MFMA work, which cancels the gain (measured on the 384-dim
+// config: 0.167 vs 0.164 ms per step).
+inline bool dma_head_dim(int D) { return D % 4 == 0 && D > 48 && D <= 128; }
 
 // Optional per-kernel HIP-event timing (implemented in wha_api.hip).
 struct TimingScope {
