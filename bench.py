@@ -1,10 +1,14 @@
 """Benchmark: causal attention fwd+bwd on one MI355X (BASELINE.json metric).
 
-A step is one fused forward (wha_attn_fwd) plus one fused backward
-(wha_attn_bwd) over the whole headline batch -- 768-dim config: B=8 sequences,
-H=12 heads, T=1024, head_dim 64, fp32 -- with Q, K, V, dO drawn from the seeded
-generator (seed 42) and already resident in HBM.  Outputs and the backward
+A step is one training forward (wha_attn_fwd_keep: the fused forward, which
+also keeps its raw scores for the backward) plus one fused backward
+(wha_attn_bwd_kept: reads those scores instead of recomputing Q K^T) over the
+whole headline batch -- 768-dim config: B=8 sequences, H=12 heads, T=1024,
+head_dim 64, fp32 -- with Q, K, V, dO drawn from the seeded generator (seed 42)
+and already resident in HBM.  Outputs, the score buffer and the backward
 workspace are preallocated, so the timed region holds only kernel launches.
+Head dims the kept pair does not cover (42, 48) run wha_attn_fwd / wha_attn_bwd.
+--recompute times the wha_attn_fwd / wha_attn_bwd pair instead.
 
 Prints one JSON line: value = tokens/s (B*T per step), plus TFLOP/s on the
 credited FLOPs (12*B*H*D*P, P = T(T+1)/2), a roofline object for the dominant
@@ -103,7 +107,8 @@ def run_attention(args, cfg, pkg, torch):
     o = torch.empty_like(tq)
     lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
     dq, dk, dv = (torch.empty_like(tq) for _ in range(3))
-    plan = pkg.AttnPlan(tq, tk, tv, o, lse, tdo, dq, dk, dv)  # pointers and layouts bound once
+    # pointers and layouts bound once; the forward keeps its scores for the backward unless --recompute
+    plan = pkg.AttnPlan(tq, tk, tv, o, lse, tdo, dq, dk, dv, keep_scores=not args.recompute)
 
     def step():
         plan.fwd()
@@ -173,7 +178,8 @@ def run_attention(args, cfg, pkg, torch):
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic (seeded xorshift64 + Box-Muller, seed 42)",
         "config": {"workload": cfg["name"], "batch": B, "heads": H, "seq_len": T, "head_dim": D,
-                   "layout": "[B,H,T,D] contiguous", "causal": True, "parallelism": "none (1 GPU)"},
+                   "layout": "[B,H,T,D] contiguous", "causal": True, "parallelism": "none (1 GPU)",
+                   "backward": "scores kept by the forward" if plan.keeps_scores else "S recomputed"},
         "tflops": flops["total"] / (ms_per_step * 1e-3) / 1e12,
         "pct_fp32_mfma_peak": 100.0 * flops["total"] / (ms_per_step * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
         "kernel_ms": {n: round(kern[n]["avg_ms"], 5) for n in kern},
@@ -480,16 +486,17 @@ def run_layer(args, cfg, pkg, torch):
     dq4, dk4, dv4 = heads(d_qkv, 0), heads(d_qkv, 1), heads(d_qkv, 2)
     L = pkg.layout_of(q)
     wsa = torch.empty(pkg.attn_bwd_workspace_bytes(L) // 4 + 64, device=dev)
+    sc = None if args.recompute else pkg.attn_scores_buffer(L, dev)  # the core keeps its scores
     wsl = torch.empty(max(int(pkg.lib().wha_linear_bwd_dw_workspace_size(M, n, E)) for n in (E, 3 * E)) // 4 + 64,
                       device=dev)
 
     def step():
         pkg.linear_fwd(x, wa, ba, out=qkv)
-        pkg.attn_fwd(q, k, v, out=o4, lse=lse)
+        pkg.attn_fwd(q, k, v, out=o4, lse=lse, scores=sc)
         pkg.linear_fwd(obuf[:, :E], wp, bp, out=out)
         pkg.linear_bwd_dx(dy, wp, out=dobuf[:, :E])
         pkg.linear_bwd_dw(dy, obuf[:, :E], workspace=wsl)
-        pkg.attn_bwd(q, k, v, o4, do4, lse, workspace=wsa, dq=dq4, dk=dk4, dv=dv4)
+        pkg.attn_bwd(q, k, v, o4, do4, lse, workspace=wsa, dq=dq4, dk=dk4, dv=dv4, scores=sc)
         pkg.linear_bwd_dx(d_qkv, wa, out=dx)
         pkg.linear_bwd_dw(d_qkv, x, workspace=wsl)
 
@@ -630,6 +637,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="768", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--recompute", action="store_true",
+                    help="time wha_attn_fwd + wha_attn_bwd (S recomputed in the backward) instead of the "
+                         "kept-scores pair")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="first run a plain device copy (y = 2*x, torch elementwise kernel) of this many "
                          "MiB five times, as the known-size reference for rocprofv3 byte counters")

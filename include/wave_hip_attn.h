@@ -92,6 +92,29 @@ int wha_attn_bwd(const float* q, const float* k, const float* v,
                  float* dk, float* dv, void* workspace, size_t workspace_bytes,
                  const wha_layout* layout, float scale, void* stream);
 
+/* Training pair that keeps the forward's scores for the backward, as the
+ * reference's forward keeps its attention weights and hands them to
+ * attention_backward (src/common/compute.rs:391-399 -> :286-314,
+ * src/cpu/backward.rs:330).  wha_attn_fwd_keep is wha_attn_fwd that also
+ * writes the raw scores q_t.k_j*scale*log2(e) of the causal half into scores;
+ * wha_attn_bwd_kept is wha_attn_bwd that reads them instead of recomputing
+ * q k^T (same workspace as wha_attn_bwd).  scores: wha_attn_scores_size bytes
+ * of device memory, 16-byte aligned, opaque (its layout is internal), valid
+ * until the next wha_attn_fwd_keep into it.  When wha_attn_scores_size is 0
+ * (head dims outside 52..128 or not a multiple of 4, strides not multiples of
+ * 4 floats, or a score buffer above 8 GiB) scores may be NULL and the pair
+ * behaves exactly as wha_attn_fwd / wha_attn_bwd.  Otherwise every tensor
+ * must be 16-byte aligned (WHA_ERR_INVALID if not). */
+size_t wha_attn_scores_size(const wha_layout* layout);
+int wha_attn_fwd_keep(const float* q, const float* k, const float* v, float* o,
+                      float* lse, float* scores, const wha_layout* layout,
+                      float scale, void* stream);
+int wha_attn_bwd_kept(const float* q, const float* k, const float* v,
+                      const float* o, const float* d_o, const float* lse,
+                      const float* scores, float* dq, float* dk, float* dv,
+                      void* workspace, size_t workspace_bytes,
+                      const wha_layout* layout, float scale, void* stream);
+
 /* Bytes of device workspace wha_attn_bwd_from_probs needs. */
 size_t wha_attn_bwd_from_probs_workspace_size(const wha_layout* layout);
 

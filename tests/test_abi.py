@@ -192,3 +192,34 @@ def test_wave_kv_entry_points_validate(pkg):
                                  None) == WHA_ERR_INVALID
     assert b"capacity" in L.wha_last_error()
     assert L.wha_wave_kv_decode_workspace_size(ctypes.byref(sh), 0) == 0
+
+
+def test_scores_size_and_kept_pair_validation(pkg):
+    """wha_attn_scores_size: the causal half in 64-key column blocks (rows
+    64kt..Tp-1 of block kt) for the covered layouts, 0 elsewhere; the kept pair
+    rejects a missing or misaligned scores buffer before touching the device."""
+    L = pkg.lib()
+    B, H, T = 8, 12, 1024
+    rows = sum(T - 64 * kt for kt in range(T // 64))
+    assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(B, H, T, 64))) == B * H * rows * 64 * 4
+    assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_seq(B, T, 12, 768))) == B * H * rows * 64 * 4
+    for D in (100, 128, 52):
+        assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(2, 2, 100, D))) > 0
+    for D in (48, 42, 16, 50):
+        assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(2, 2, 100, D))) == 0
+    odd = pkg.layout_bhtd(2, 2, 100, 64)
+    odd.stride_t = 66
+    assert L.wha_attn_scores_size(ctypes.byref(odd)) == 0
+    assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(0, 1, 1, 64))) == 0
+
+    lay = pkg.layout_bhtd(1, 1, 64, 64)
+    p = ctypes.c_void_p(0x100000)
+    rc = L.wha_attn_fwd_keep(p, p, p, p, p, None, ctypes.byref(lay), 0.125, None)
+    assert rc == WHA_ERR_INVALID and b"scores" in L.wha_last_error()
+    rc = L.wha_attn_fwd_keep(ctypes.c_void_p(0x100004), p, p, p, p, p, ctypes.byref(lay), 0.125, None)
+    assert rc == WHA_ERR_INVALID and b"aligned" in L.wha_last_error()
+    rc = L.wha_attn_bwd_kept(*([p] * 6), None, p, p, p, None, 0, ctypes.byref(lay), 0.125, None)
+    assert rc == WHA_ERR_INVALID and b"scores" in L.wha_last_error()
+    null = ctypes.c_void_p(0)
+    rc = L.wha_attn_bwd_kept(*([null] * 10), None, 0, ctypes.byref(lay), 0.125, None)
+    assert rc == WHA_ERR_INVALID and b"non-NULL" in L.wha_last_error()

@@ -1,0 +1,98 @@
+"""GPU parity of the kept-scores training pair (wha_attn_fwd_keep, then
+wha_attn_bwd_kept reading the forward's scores instead of recomputing Q K^T)
+against the CPU oracle (src/common/compute.rs:377-409, src/cpu/backward.rs:313-363),
+at the same bar as the fused pair: max-abs <= 1e-4 and relative L2 <= 1e-5 for
+O, dQ, dK and dV against the f32 oracle.  Shapes the kept pair does not cover
+(wha_attn_scores_size = 0) must behave exactly as wha_attn_fwd / wha_attn_bwd.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_parity, errors
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+    return torch, torch.device("cuda:0")
+
+
+def run_pair(pkg, torch, dev, q, k, v, do, keep):
+    tq, tk, tv, tdo = (torch.from_numpy(np.ascontiguousarray(a)).to(dev) for a in (q, k, v, do))
+    L = pkg.layout_of(tq)
+    sc = pkg.attn_scores_buffer(L, dev) if keep else None
+    if keep and sc is not None:
+        sc.fill_(float("nan"))  # entries the forward does not write must never be used unmasked
+    o, lse = pkg.attn_fwd(tq, tk, tv, scores=sc)
+    dq, dk, dv = pkg.attn_bwd(tq, tk, tv, o, tdo, lse, scores=sc)
+    torch.cuda.synchronize()
+    return [x.cpu().numpy() for x in (o, lse, dq, dk, dv)], sc is not None
+
+
+SHAPES = [(1, 1, 1, 64), (1, 2, 17, 64), (2, 2, 100, 64), (3, 1, 48, 64), (2, 3, 130, 64),
+          (1, 1, 257, 128), (1, 2, 129, 100), (2, 2, 97, 56), (1, 3, 40, 52), (1, 2, 65, 124),
+          (2, 3, 63, 48), (1, 2, 65, 42), (1, 4, 200, 8)]
+
+
+@pytest.mark.parametrize("B,H,T,D", SHAPES)
+def test_kept_pair_small_shapes(pkg, torch_dev, B, H, T, D):
+    torch, dev = torch_dev
+    print(f"case kept B={B} H={H} T={T} D={D}", flush=True)
+    q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=2000 + T + D)
+    got, kept = run_pair(pkg, torch, dev, q, k, v, do, keep=True)
+    covered = pkg.attn_scores_bytes(pkg.layout_bhtd(B, H, T, D)) > 0
+    assert kept == covered
+    r32 = oracle.fwd_bwd_bhtd(q, k, v, do, "f32")
+    r64 = oracle.fwd_bwd_bhtd(q, k, v, do, "f64")
+    for i, n in enumerate(("O", "dQ", "dK", "dV")):
+        g = got[[0, 2, 3, 4][i]]
+        ma, rl = assert_parity(f"kept B{B}H{H}T{T}D{D} {n}", g, r32[i])
+        print(f"  {n}: vs f32 max_abs={ma:.2e} rel_l2={rl:.2e} | vs f64 {errors(g, r64[i])[1]:.2e}", flush=True)
+    assert np.abs(got[1] - r64[4]).max() < 2e-5
+    # the recompute pair on the same inputs: same softmax, scores rounded in another order
+    ref, _ = run_pair(pkg, torch, dev, q, k, v, do, keep=False)
+    assert np.array_equal(got[0], ref[0]) and np.array_equal(got[1], ref[1])  # same forward kernel
+    for a, b in zip(got[2:], ref[2:]):
+        assert errors(a, b)[1] < 1e-6
+
+
+def test_kept_pair_headline_config(pkg, torch_dev):
+    """768-dim config at full size (seed 42) against the threaded f32 oracle,
+    through AttnPlan (the bench's launch path), two steps in a row."""
+    torch, dev = torch_dev
+    B, H, T, D = 8, 12, 1024, 64
+    print("case kept headline", flush=True)
+    q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=42)
+    tq, tk, tv, tdo = (torch.from_numpy(a).to(dev) for a in (q, k, v, do))
+    o = torch.empty_like(tq)
+    lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
+    dq, dk, dv = (torch.empty_like(tq) for _ in range(3))
+    plan = pkg.AttnPlan(tq, tk, tv, o, lse, tdo, dq, dk, dv)
+    assert plan.keeps_scores
+    for _ in range(2):
+        plan.fwd()
+        plan.bwd()
+    torch.cuda.synchronize()
+    out, rq, rk, rv = oracle.batch_fwd_bwd_f32_threaded(
+        *(oracle.bhtd_to_seq(a) for a in (q, k, v, do)), H, nthreads=16)
+    for n, g, r in (("O", o, out), ("dQ", dq, rq), ("dK", dk, rk), ("dV", dv, rv)):
+        ma, rl = assert_parity(f"kept headline {n}", g.cpu().numpy(), oracle.seq_to_bhtd(r, H))
+        print(f"  {n}: max_abs={ma:.2e} rel_l2={rl:.2e}", flush=True)
+
+
+def test_kept_pair_4096_slice(pkg, torch_dev):
+    """4096 preset (D = 128, T = 2048) on one (b,h) slice against the oracle."""
+    torch, dev = torch_dev
+    print("case kept 4096 slice", flush=True)
+    q, k, v, do = pkg.synth_inputs(1, 2, 2048, 128, seed=42)
+    got, kept = run_pair(pkg, torch, dev, q, k, v, do, keep=True)
+    assert kept
+    sl = lambda a: a[:, 1:2]
+    out, rq, rk, rv = oracle.batch_fwd_bwd_f32_threaded(
+        *(oracle.bhtd_to_seq(sl(a)) for a in (q, k, v, do)), 1, nthreads=1)
+    for n, g, r in (("O", got[0], out), ("dQ", got[2], rq), ("dK", got[3], rk), ("dV", got[4], rv)):
+        assert_parity(f"kept 4096 {n}", sl(g), oracle.seq_to_bhtd(r, 1))

@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "wha_last_error", "wha_version",
     "wha_attn_fwd", "wha_attn_bwd_workspace_size", "wha_attn_bwd",
     "wha_attn_bwd_from_probs_workspace_size", "wha_attn_bwd_from_probs",
+    "wha_attn_scores_size", "wha_attn_fwd_keep", "wha_attn_bwd_kept",
     "wha_decode_workspace_size", "wha_decode_fwd", "wha_attn_probs_rows",
     "wha_wave_fwd", "wha_wave_bwd_workspace_size", "wha_wave_bwd", "wha_wave_probs_rows",
     "wha_wave_kv_prefill_workspace_size", "wha_wave_kv_prefill", "wha_wave_kv_decode_workspace_size",
@@ -133,6 +134,10 @@ def lib():
         L.wha_attn_bwd_from_probs_workspace_size.argtypes = [lp]
         L.wha_attn_bwd_from_probs_workspace_size.restype = sz
         L.wha_attn_bwd_from_probs.argtypes = [vp] * 8 + [vp, sz, lp, ctypes.c_float, vp]
+        L.wha_attn_scores_size.argtypes = [lp]
+        L.wha_attn_scores_size.restype = sz
+        L.wha_attn_fwd_keep.argtypes = [vp] * 6 + [lp, ctypes.c_float, vp]
+        L.wha_attn_bwd_kept.argtypes = [vp] * 10 + [vp, sz, lp, ctypes.c_float, vp]
         L.wha_decode_workspace_size.argtypes = [lp]
         L.wha_decode_workspace_size.restype = sz
         L.wha_decode_fwd.argtypes = [vp] * 5 + [vp, sz, lp, ctypes.c_float, vp]
@@ -233,9 +238,24 @@ def default_scale(D: int) -> float:
     return float(np.float32(1.0) / np.sqrt(np.float32(D)))
 
 
-def attn_fwd(q, k, v, scale=None, want_lse=True, out=None, lse=None):
+def attn_scores_bytes(L: WaveLayout) -> int:
+    """Bytes of the scores buffer a training forward keeps for its backward
+    (wha_attn_scores_size; 0 where the layout's kernels cannot keep them)."""
+    return int(lib().wha_attn_scores_size(ctypes.byref(L)))
+
+
+def attn_scores_buffer(L: WaveLayout, device):
+    """A scores buffer for attn_fwd(..., scores=) / attn_bwd(..., scores=), or
+    None where attn_scores_bytes(L) is 0 (nothing to keep)."""
+    n = attn_scores_bytes(L)
+    return _torch().empty(n // 4, dtype=_torch().float32, device=device) if n else None
+
+
+def attn_fwd(q, k, v, scale=None, want_lse=True, out=None, lse=None, scores=None):
     """Fused causal forward on [B,H,T,D] views.  Returns (o, lse) with lse
-    [B,H,T] (natural-log row log-sum-exp), or o alone when want_lse=False."""
+    [B,H,T] (natural-log row log-sum-exp), or o alone when want_lse=False.
+    scores (attn_scores_buffer): also keep the raw scores for attn_bwd(...,
+    scores=) (wha_attn_fwd_keep)."""
     torch = _torch()
     L = layout_of(q)
     _same_layout(L, k, v)
@@ -245,14 +265,20 @@ def attn_fwd(q, k, v, scale=None, want_lse=True, out=None, lse=None):
     if want_lse and lse is None:
         lse = torch.empty((L.B, L.H, L.T), dtype=torch.float32, device=q.device)
     s = default_scale(L.D) if scale is None else float(scale)
-    _check("wha_attn_fwd", lib().wha_attn_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(out),
-                                              _ptr(lse) if want_lse else None,
-                                              ctypes.byref(L), s, _stream_ptr(q)))
+    if scores is not None:
+        _check("wha_attn_fwd_keep", lib().wha_attn_fwd_keep(_ptr(q), _ptr(k), _ptr(v), _ptr(out),
+                                                            _ptr(lse) if want_lse else None, _ptr(scores),
+                                                            ctypes.byref(L), s, _stream_ptr(q)))
+    else:
+        _check("wha_attn_fwd", lib().wha_attn_fwd(_ptr(q), _ptr(k), _ptr(v), _ptr(out),
+                                                  _ptr(lse) if want_lse else None,
+                                                  ctypes.byref(L), s, _stream_ptr(q)))
     return (out, lse) if want_lse else out
 
 
-def attn_bwd(q, k, v, o, do, lse, scale=None, workspace=None, dq=None, dk=None, dv=None):
-    """Fused causal backward (P recomputed from lse).  Returns (dq, dk, dv)."""
+def attn_bwd(q, k, v, o, do, lse, scale=None, workspace=None, dq=None, dk=None, dv=None, scores=None):
+    """Fused causal backward (P recomputed from lse; with scores, from the
+    scores attn_fwd kept: wha_attn_bwd_kept).  Returns (dq, dk, dv)."""
     torch = _torch()
     L = layout_of(q)
     _same_layout(L, k, v, o, do)
@@ -262,9 +288,14 @@ def attn_bwd(q, k, v, o, do, lse, scale=None, workspace=None, dq=None, dk=None, 
     _same_layout(L, dq, dk, dv)
     s = default_scale(L.D) if scale is None else float(scale)
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    _check("wha_attn_bwd", lib().wha_attn_bwd(
-        _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse.contiguous()), _ptr(dq), _ptr(dk), _ptr(dv),
-        _ptr(workspace), ws_bytes, ctypes.byref(L), s, _stream_ptr(q)))
+    if scores is not None:
+        _check("wha_attn_bwd_kept", lib().wha_attn_bwd_kept(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse.contiguous()), _ptr(scores), _ptr(dq),
+            _ptr(dk), _ptr(dv), _ptr(workspace), ws_bytes, ctypes.byref(L), s, _stream_ptr(q)))
+    else:
+        _check("wha_attn_bwd", lib().wha_attn_bwd(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse.contiguous()), _ptr(dq), _ptr(dk), _ptr(dv),
+            _ptr(workspace), ws_bytes, ctypes.byref(L), s, _stream_ptr(q)))
     return dq, dk, dv
 
 
@@ -393,9 +424,12 @@ class AttnPlan:
     """Launches bound once to a fixed set of [B,H,T,D] tensors: layouts, pointers,
     scale, workspace and stream are validated and marshalled at construction, so
     fwd() and bwd() are one C call each (for training loops and benchmarks where
-    per-call Python checks would cost as much as the kernels)."""
+    per-call Python checks would cost as much as the kernels).  A plan with
+    backward tensors keeps the forward's scores for its backward
+    (wha_attn_fwd_keep / wha_attn_bwd_kept) unless keep_scores=False."""
 
-    def __init__(self, q, k, v, o, lse, do=None, dq=None, dk=None, dv=None, workspace=None, scale=None):
+    def __init__(self, q, k, v, o, lse, do=None, dq=None, dk=None, dv=None, workspace=None, scale=None,
+                 keep_scores=True):
         torch = _torch()
         L = layout_of(q)
         _same_layout(L, k, v, o)
@@ -407,6 +441,10 @@ class AttnPlan:
         st = _stream_ptr(q)
         self._fwd_args = (_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), ctypes.byref(L), s, st)
         self._bwd_args = None
+        self._f = lib().wha_attn_fwd
+        self._b = lib().wha_attn_bwd
+        self._fname, self._bname = "wha_attn_fwd", "wha_attn_bwd"
+        scores = attn_scores_buffer(L, q.device) if (do is not None and keep_scores) else None
         if do is not None:
             _same_layout(L, do, dq, dk, dv)
             need = attn_bwd_workspace_bytes(L)
@@ -416,20 +454,27 @@ class AttnPlan:
             ws_bytes = workspace.numel() * workspace.element_size()
             self._bwd_args = (_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse), _ptr(dq), _ptr(dk),
                               _ptr(dv), _ptr(workspace), ctypes.c_size_t(ws_bytes), ctypes.byref(L), s, st)
-        self._f = lib().wha_attn_fwd
-        self._b = lib().wha_attn_bwd
+        if scores is not None:
+            self._keep.append(scores)
+            a = self._fwd_args
+            self._fwd_args = a[:5] + (_ptr(scores),) + a[5:]
+            a = self._bwd_args
+            self._bwd_args = a[:6] + (_ptr(scores),) + a[6:]
+            self._f, self._b = lib().wha_attn_fwd_keep, lib().wha_attn_bwd_kept
+            self._fname, self._bname = "wha_attn_fwd_keep", "wha_attn_bwd_kept"
+        self.keeps_scores = scores is not None
 
     def fwd(self):
         rc = self._f(*self._fwd_args)
         if rc:
-            _check("wha_attn_fwd", rc)
+            _check(self._fname, rc)
 
     def bwd(self):
         if self._bwd_args is None:
             raise ValueError("this plan was built without backward tensors")
         rc = self._b(*self._bwd_args)
         if rc:
-            _check("wha_attn_bwd", rc)
+            _check(self._bname, rc)
 
 
 # ------------------------------------------------------------------ timing

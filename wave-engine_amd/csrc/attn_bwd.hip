@@ -529,15 +529,20 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
 // key-tile x query-tile products for every block), so equal blocks fill the
 // CUs to the end instead of leaving a tail of short blocks;
 // grid = B*H*ceil(n_kt/2).
+// SAVED: S comes from the forward's kept scores SC (attn_fwd_dma_kernel with
+// SAVE, same layout as DS) instead of Q K^T: a lane's 8 scores of the next
+// sub-tile are loaded while the current one is consumed (two register sets,
+// alternating with the unrolled loop), and K is not needed at all.
 // three blocks per CU at head dim 64, two at 128 (LDS and VGPR budgets)
 #ifndef WHA_DMA_WPE
 #define WHA_DMA_WPE(DP) __attribute__((amdgpu_waves_per_eu((DP) == 64 ? 3 : 2)))
 #endif
-template <int DP, bool DS_OUT, bool PADQ>
+template <int DP, bool DS_OUT, bool PADQ, bool SAVED>
 __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ stats, float* __restrict__ dK,
-    float* __restrict__ dV, float* __restrict__ DS, View L, float scale, float scale_log2) {
+    float* __restrict__ dV, float* __restrict__ DS, const float* __restrict__ SC, View L, float scale,
+    float scale_log2) {
   constexpr int DG = DP / 4, NDT = DP / 16;
   constexpr int QPR = DP / 4;            // quads per row
   constexpr int BSUB = 32;               // queries per sub-tile
@@ -613,8 +618,8 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
     const int kt = pass == 0 ? pair : n_kt - 1 - pair;
     const int k0w = kt * 64 + wave * 16;
     const int krow = k0w + lq;
-    float kf[DG], vf[DG];
-    load_row_frag<DP, true>(K + base, krow, L.T, L.D, L.st, g, scale_log2, kf);
+    float kf[SAVED ? 1 : DG], vf[DG];
+    if constexpr (!SAVED) load_row_frag<DP, true>(K + base, krow, L.T, L.D, L.st, g, scale_log2, kf);
     load_row_frag<DP, true>(V + base, krow, L.T, L.D, L.st, g, 1.f, vf);
     floatx4 dkacc[NDT], dvacc[NDT];
 #pragma unroll
@@ -623,14 +628,23 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
       dvacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
     const int q_end = krow < L.T ? L.T : 0;  // valid queries: krow <= q < q_end
-    float* dsw = DS_OUT ? DS + ((int64_t)bh * ds_rows(L.T) + ds_block_row(kt, L.T) - (int64_t)64 * kt) * 64 +
-                              wave * 16 + lq
-                        : nullptr;
+    const int64_t kcol = ((int64_t)bh * ds_rows(L.T) + ds_block_row(kt, L.T) - (int64_t)64 * kt) * 64 + wave * 16 + lq;
+    float* dsw = DS_OUT ? DS + kcol : nullptr;
+    // SAVED: a lane's scores of sub-tile st (rows 32st+16mt+4g+i, this lane's key)
+    auto load_sc = [&](int st, float (&dst)[8]) {
+      const float* src = SC + kcol + (int64_t)(st * BSUB + 4 * g) * 64;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[4 * mt + i] = src[(16 * mt + i) * 64];
+      }
+    };
 
     // one sub-tile's contractions; MASKED: the sub-tile touches the diagonal or
     // the end of the sequence (a separate copy, so the common case carries no
     // compare or select)
-    auto compute = [&](auto masked, int qb, const float* Qs, const float* Os, const float* Sts) {
+    auto compute = [&](auto masked, int qb, const float* Qs, const float* Os, const float* Sts,
+                       const float (&sc)[8]) {
       constexpr bool MASKED = decltype(masked)::value;
       // S (log2 units) and dP, started from -LSE*log2(e) and -Delta of their rows
       floatx4 s[2], dp[2];
@@ -641,12 +655,14 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
         dp[mt] = *reinterpret_cast<const floatx4*>(&Sts[BSUB + 16 * mt + 4 * g]);
 #pragma unroll
         for (int j = 0; j < DG / 4; ++j) {
-          const float4 a = lds_read_quad<DP, true>(Qs, 16 * mt + lq, (DG / 4) * g + j);
+          if constexpr (!SAVED) {
+            const float4 a = lds_read_quad<DP, true>(Qs, 16 * mt + lq, (DG / 4) * g + j);
+            s[mt] = mfma4(a.x, kf[4 * j + 0], s[mt]);
+            s[mt] = mfma4(a.y, kf[4 * j + 1], s[mt]);
+            s[mt] = mfma4(a.z, kf[4 * j + 2], s[mt]);
+            s[mt] = mfma4(a.w, kf[4 * j + 3], s[mt]);
+          }
           const float4 c = lds_read_quad<DP, true>(Os, 16 * mt + lq, (DG / 4) * g + j);
-          s[mt] = mfma4(a.x, kf[4 * j + 0], s[mt]);
-          s[mt] = mfma4(a.y, kf[4 * j + 1], s[mt]);
-          s[mt] = mfma4(a.z, kf[4 * j + 2], s[mt]);
-          s[mt] = mfma4(a.w, kf[4 * j + 3], s[mt]);
           dp[mt] = mfma4(c.x, vf[4 * j + 0], dp[mt]);
           dp[mt] = mfma4(c.y, vf[4 * j + 1], dp[mt]);
           dp[mt] = mfma4(c.z, vf[4 * j + 2], dp[mt]);
@@ -654,6 +670,13 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
         }
       }
       WHA_FENCE();
+      if constexpr (SAVED) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) s[mt][i] += sc[4 * mt + i];
+        }
+      }
       // lane element (mt,i): query qb+16mt+4g+i, key krow
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
@@ -701,25 +724,30 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
 
     // one sub-tile: wait for its loads, start the next one's, then consume it
     auto step = [&](int st, const float* Qs, const float* Os, const float* Sts, float* Qn, float* On,
-                    float* Sn) {
+                    float* Sn, const float (&sc)[8], float (&sc_next)[8]) {
       wait_vmem();
       __syncthreads();  // sub-tile st is in LDS; every wave is done with sub-tile st-1
       prio_by_remaining(left--, work);
-      if (st + 1 < n_st) fetch(st + 1, Qn, On, Sn);
+      if (st + 1 < n_st) {
+        fetch(st + 1, Qn, On, Sn);
+        if constexpr (SAVED) load_sc(st + 1, sc_next);
+      }
       const int qb = st * BSUB;
       if (qb + BSUB - 1 < k0w) return;  // every row precedes every key of the wave
       if (qb >= k0w + 15 && qb + BSUB <= L.T && k0w + 16 <= L.T)
-        compute(std::false_type{}, qb, Qs, Os, Sts);
+        compute(std::false_type{}, qb, Qs, Os, Sts, sc);
       else
-        compute(std::true_type{}, qb, Qs, Os, Sts);
+        compute(std::true_type{}, qb, Qs, Os, Sts, sc);
     };
 
     const int st0 = 2 * kt;
+    float scA[8], scB[8];  // SAVED: scores of the even / odd sub-tiles
     __syncthreads();  // the previous key tile's last sub-tile has been read by every wave
     fetch(st0, Qs0, Os0, St0);
+    if constexpr (SAVED) load_sc(st0, scA);
     for (int st = st0; st < n_st; st += 2) {
-      step(st, Qs0, Os0, St0, Qs1, Os1, St1);
-      if (st + 1 < n_st) step(st + 1, Qs1, Os1, St1, Qs0, Os0, St0);
+      step(st, Qs0, Os0, St0, Qs1, Os1, St1, scA, scB);
+      if (st + 1 < n_st) step(st + 1, Qs1, Os1, St1, Qs0, Os0, St0, scB, scA);
     }
     store_row_frag_split<DP>(dK + base, krow, L.T, L.D, L.st, g, dkacc, scale);
     store_row_frag_split<DP>(dV + base, krow, L.T, L.D, L.st, g, dvacc, 1.f);
@@ -970,7 +998,7 @@ namespace {
 template <int DP, bool PADQ>
 hipError_t bwd_dma_t(const float* q, const float* k, const float* v, const float* o, const float* d_o,
                      const float* lse, float* dq, float* dk, float* dv, float* stats, float* ds, const View& L,
-                     float scale, hipStream_t stream) {
+                     float scale, hipStream_t stream, const float* sc) {
   const float sl2 = (float)((double)scale * 1.4426950408889634);
   const int n_t64 = (L.T + 63) / 64;
   const dim3 grid((unsigned)((n_t64 + 1) / 2 * L.B * L.H));
@@ -985,8 +1013,12 @@ hipError_t bwd_dma_t(const float* q, const float* k, const float* v, const float
   if (e != hipSuccess) return e;
   {
     TimingScope ts("attn_bwd_dkv", stream);
-    hipLaunchKernelGGL((attn_bwd_dkv_dma_kernel<DP, true, PADQ>), grid, dim3(256), 0, stream, q, k, v, d_o,
-                       (const float*)stats, dk, dv, ds, L, scale, sl2);
+    if (sc != nullptr)
+      hipLaunchKernelGGL((attn_bwd_dkv_dma_kernel<DP, true, PADQ, true>), grid, dim3(256), 0, stream, q, k, v, d_o,
+                         (const float*)stats, dk, dv, ds, sc, L, scale, sl2);
+    else
+      hipLaunchKernelGGL((attn_bwd_dkv_dma_kernel<DP, true, PADQ, false>), grid, dim3(256), 0, stream, q, k, v,
+                         d_o, (const float*)stats, dk, dv, ds, sc, L, scale, sl2);
     e = hipGetLastError();
   }
   if (e != hipSuccess) return e;
@@ -1116,12 +1148,13 @@ hipError_t launch_dq_from_ds(const float* k, const float* ds, float* dq, const V
 hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const float* o,
                            const float* d_o, const float* lse, float* dq, float* dk, float* dv,
                            float* delta, float* ds, const View& L, bool vec, float scale,
-                           hipStream_t stream) {
+                           hipStream_t stream, const float* sc) {
+  if (sc != nullptr && (ds == nullptr || !WHA_DKV_DMA || !scores_kept(L, vec))) return hipErrorInvalidValue;
   if (WHA_DKV_DMA && ds != nullptr && vec && dma_head_dim(L.D)) {
-    if (L.D == 64) return bwd_dma_t<64, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream);
-    if (L.D < 64) return bwd_dma_t<64, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream);
-    if (L.D == 128) return bwd_dma_t<128, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream);
-    return bwd_dma_t<128, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream);
+    if (L.D == 64) return bwd_dma_t<64, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
+    if (L.D < 64) return bwd_dma_t<64, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
+    if (L.D == 128) return bwd_dma_t<128, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
+    return bwd_dma_t<128, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
   }
 #define WHA_BWD(DP)                                                                                 \
   return vec ? bwd_fused_t<DP, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream) \

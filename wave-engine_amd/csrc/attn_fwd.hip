@@ -181,16 +181,24 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
 //     overflow.  The result is the same softmax, rounded differently.
 // A block handles query tiles p and n_qt-1-p (n_qt+1 key tiles of work for
 // every block); grid = B*H*ceil(n_qt/2).
+// SAVE: also keep the raw scores q.k*scale*log2(e) of every sub-tile it
+// computes in SC (the layout of the backward's dS workspace, ds_block_row), the
+// way the reference's forward hands its attention weights to the backward
+// (src/common/compute.rs:391-399 -> :286-314): the key-stationary backward then
+// reads them instead of recomputing Q K^T.  Entries after the diagonal hold
+// whatever the key tile gave (the backward masks them); rows past T are
+// written too (the layout pads every block to a multiple of 64 rows).
 constexpr float kLazyMax = 8.f;
 #ifndef WHA_FWD_WPE
 #define WHA_FWD_WPE __attribute__((amdgpu_waves_per_eu(3)))
 #endif
-template <int DP, bool PADQ>
+template <int DP, bool PADQ, bool SAVE>
 __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const float* __restrict__ Q,
                                                                      const float* __restrict__ K,
                                                                      const float* __restrict__ V,
                                                                      float* __restrict__ O,
-                                                                     float* __restrict__ LSE, View L,
+                                                                     float* __restrict__ LSE,
+                                                                     float* __restrict__ SC, View L,
                                                                      float scale_log2) {
   constexpr int DG = DP / 4, NDT = DP / 16;
   constexpr int QPR = DP / 4;            // quads per row
@@ -273,6 +281,8 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
     for (int dt = 0; dt < NDT; ++dt) oacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
     const int n_sub = (min(L.T, (qt + 1) * 64) + BSUB - 1) / BSUB;
     const int key_last = min(qrow, L.T - 1);  // keys above it are masked
+    // SAVE: this lane's row of the score layout, less 64 rows per column block
+    float* sc_row = SAVE ? SC + ((int64_t)bh * ds_rows(L.T) + qrow) * 64 + 4 * g : nullptr;
 
     auto compute = [&](auto masked, int k0, const float* Ks, const float* Vs) {
       constexpr bool MASKED = decltype(masked)::value;
@@ -292,6 +302,12 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
       }
       WHA_FENCE();
       // lane element (mt,i): key k0 + 16mt + 4g + i of query qrow, as s - m_i
+      if constexpr (SAVE) {
+        const int kt = k0 >> 6;
+        float* dst = sc_row + (ds_block_row(kt, L.T) - (int64_t)64 * kt) * 64 + (k0 & 63);
+#pragma unroll
+        for (int mt = 0; mt < NKT; ++mt) *reinterpret_cast<floatx4*>(dst + 16 * mt) = s[mt] - neg_m;
+      }
       if (MASKED) {
 #pragma unroll
         for (int mt = 0; mt < NKT; ++mt) {
@@ -393,21 +409,36 @@ static hipError_t launch_fwd_t(const float* q, const float* k, const float* v, f
   return hipGetLastError();
 }
 
+namespace {
+template <int DP, bool PADQ>
+void fwd_dma_t(const float* q, const float* k, const float* v, float* o, float* lse, float* sc, const View& L,
+               float scale_log2, hipStream_t stream) {
+  const int n_qt = (L.T + 63) / 64;
+  const dim3 grid((unsigned)((n_qt + 1) / 2 * L.B * L.H));
+  if (sc != nullptr)
+    hipLaunchKernelGGL((attn_fwd_dma_kernel<DP, PADQ, true>), grid, dim3(256), 0, stream, q, k, v, o, lse, sc, L,
+                       scale_log2);
+  else
+    hipLaunchKernelGGL((attn_fwd_dma_kernel<DP, PADQ, false>), grid, dim3(256), 0, stream, q, k, v, o, lse, sc, L,
+                       scale_log2);
+}
+}  // namespace
+
+bool scores_kept(const View& L, bool vec) { return WHA_FWD_DMA && vec && dma_head_dim(L.D); }
+
 hipError_t launch_attn_fwd(const float* q, const float* k, const float* v, float* o, float* lse,
-                           const View& L, bool vec, float scale, hipStream_t stream) {
+                           const View& L, bool vec, float scale, hipStream_t stream, float* scores) {
   if (WHA_FWD_DMA && vec && dma_head_dim(L.D)) {
-    const int n_qt = (L.T + 63) / 64;
     const float scale_log2 = (float)((double)scale * 1.4426950408889634);
-    const dim3 grid((unsigned)((n_qt + 1) / 2 * L.B * L.H));
     TimingScope ts("attn_fwd", stream);
     if (L.D == 64)
-      hipLaunchKernelGGL((attn_fwd_dma_kernel<64, false>), grid, dim3(256), 0, stream, q, k, v, o, lse, L, scale_log2);
+      fwd_dma_t<64, false>(q, k, v, o, lse, scores, L, scale_log2, stream);
     else if (L.D < 64)
-      hipLaunchKernelGGL((attn_fwd_dma_kernel<64, true>), grid, dim3(256), 0, stream, q, k, v, o, lse, L, scale_log2);
+      fwd_dma_t<64, true>(q, k, v, o, lse, scores, L, scale_log2, stream);
     else if (L.D == 128)
-      hipLaunchKernelGGL((attn_fwd_dma_kernel<128, false>), grid, dim3(256), 0, stream, q, k, v, o, lse, L, scale_log2);
+      fwd_dma_t<128, false>(q, k, v, o, lse, scores, L, scale_log2, stream);
     else
-      hipLaunchKernelGGL((attn_fwd_dma_kernel<128, true>), grid, dim3(256), 0, stream, q, k, v, o, lse, L, scale_log2);
+      fwd_dma_t<128, true>(q, k, v, o, lse, scores, L, scale_log2, stream);
     return hipGetLastError();
   }
   switch (padded_dim(L.D)) {

@@ -351,6 +351,71 @@ int wha_attn_bwd(const float* q, const float* k, const float* v, const float* o,
   return WHA_OK;
 }
 
+// The kept-scores pair: the forward writes the raw scores of the causal half
+// (the dS layout, ds_bytes) and the backward's dK/dV kernel reads them instead
+// of recomputing Q K^T.  Covered layouts: the direct-to-LDS head dims with
+// 16-byte-aligned strides and a dS buffer within kMaxDsBytes; elsewhere the
+// size is 0 and the pair behaves as wha_attn_fwd / wha_attn_bwd.
+size_t wha_attn_scores_size(const wha_layout* layout) {
+  if (!layout || layout->B <= 0 || layout->H <= 0 || layout->T <= 0 || layout->D <= 0) return 0;
+  wha::View V{layout->B, layout->H, layout->T, layout->D, layout->stride_b, layout->stride_h, layout->stride_t};
+  const bool strides16 = V.sb % 4 == 0 && V.sh % 4 == 0 && V.st % 4 == 0;
+  if (!strides16 || !wha::scores_kept(V, true)) return 0;
+  return ds_bytes(layout);
+}
+
+int wha_attn_fwd_keep(const float* q, const float* k, const float* v, float* o, float* lse, float* scores,
+                      const wha_layout* layout, float scale, void* stream) {
+  static const char* fn = "wha_attn_fwd_keep";
+  wha::View V;
+  int rc = check_layout(layout, &V, fn);
+  if (rc) return rc;
+  if ((rc = check_scale(scale, fn))) return rc;
+  if (!q || !k || !v || !o) return fail(WHA_ERR_INVALID, "%s: q, k, v and o must be non-NULL", fn);
+  const bool keep = wha_attn_scores_size(layout) > 0;
+  const bool vec = vec_ok(V, {q, k, v, o});
+  if (keep) {
+    if (!scores) return fail(WHA_ERR_INVALID, "%s: scores must be non-NULL (wha_attn_scores_size > 0)", fn);
+    if (!vec || (reinterpret_cast<uintptr_t>(scores) & 15))
+      return fail(WHA_ERR_INVALID, "%s: q, k, v, o and scores must be 16-byte aligned to keep scores", fn);
+  }
+  hipError_t e = wha::launch_attn_fwd(q, k, v, o, lse, V, vec, scale, static_cast<hipStream_t>(stream),
+                                      keep ? scores : nullptr);
+  if (e != hipSuccess) return hip_fail(e, "wha_attn_fwd_keep launch");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+int wha_attn_bwd_kept(const float* q, const float* k, const float* v, const float* o, const float* d_o,
+                      const float* lse, const float* scores, float* dq, float* dk, float* dv, void* workspace,
+                      size_t workspace_bytes, const wha_layout* layout, float scale, void* stream) {
+  static const char* fn = "wha_attn_bwd_kept";
+  wha::View V;
+  int rc = check_layout(layout, &V, fn);
+  if (rc) return rc;
+  if ((rc = check_scale(scale, fn))) return rc;
+  if (!q || !k || !v || !o || !d_o || !lse || !dq || !dk || !dv)
+    return fail(WHA_ERR_INVALID, "%s: every tensor pointer must be non-NULL", fn);
+  const bool keep = wha_attn_scores_size(layout) > 0;
+  const bool vec = vec_ok(V, {q, k, v, o, d_o, dq, dk, dv});
+  if (keep) {
+    if (!scores) return fail(WHA_ERR_INVALID, "%s: scores must be non-NULL (wha_attn_scores_size > 0)", fn);
+    if (!vec) return fail(WHA_ERR_INVALID, "%s: tensors must be 16-byte aligned to use kept scores", fn);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  if ((rc = resolve_workspace(workspace, workspace_bytes, wha_attn_bwd_workspace_size(layout), s, fn, &ws)))
+    return rc;
+  float* delta = static_cast<float*>(ws);
+  const size_t dsb = ds_bytes(layout);
+  float* ds = dsb ? reinterpret_cast<float*>(static_cast<char*>(ws) + stats_bytes(layout)) : nullptr;
+  hipError_t e =
+      wha::launch_attn_bwd(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, V, vec, scale, s, keep ? scores : nullptr);
+  if (e != hipSuccess) return hip_fail(e, "wha_attn_bwd_kept launch");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
 size_t wha_attn_bwd_from_probs_workspace_size(const wha_layout* layout) {
   if (!layout || layout->B <= 0 || layout->H <= 0 || layout->T <= 0) return 0;
   return delta_bytes(layout) + ds_bytes(layout);

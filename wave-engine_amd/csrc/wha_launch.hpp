@@ -39,8 +39,15 @@ struct TimingScope {
   hipStream_t stream;
 };
 
+// Fused forward.  scores != nullptr (only where scores_kept(L, vec)): also
+// writes the raw scores q.k*scale*log2(e) of the causal half into it, in the
+// layout of the dS buffer (bwd_ds_floats(L) floats).
 hipError_t launch_attn_fwd(const float* q, const float* k, const float* v, float* o, float* lse,
-                           const View& L, bool vec, float scale, hipStream_t stream);
+                           const View& L, bool vec, float scale, hipStream_t stream, float* scores = nullptr);
+
+// Whether the forward can keep its scores for this layout (the direct-to-LDS
+// kernels: 16-byte-aligned operands, dma_head_dim(D)).
+bool scores_kept(const View& L, bool vec);
 
 // Floats of the dS buffer the fused backward uses (the causal half of the
 // score matrix in 64-key column blocks, fp32).
@@ -55,10 +62,12 @@ size_t bwd_stats_floats(const View& L);
 // (ds == nullptr) a query-stationary dQ kernel that recomputes S and dP and the
 // key-stationary dK/dV kernel.  Both deterministic.  delta: bwd_stats_floats(L)
 // floats of scratch.
+// scores != nullptr: the forward's kept scores (launch_attn_fwd; requires ds
+// and scores_kept(L, vec)), read by the dK/dV kernel instead of recomputing S.
 hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const float* o,
                            const float* d_o, const float* lse, float* dq, float* dk, float* dv,
                            float* delta, float* ds, const View& L, bool vec, float scale,
-                           hipStream_t stream);
+                           hipStream_t stream, const float* scores = nullptr);
 
 // Backward from given probabilities att [B][H][T][T].  delta: [B*H*T] scratch;
 // ds: bwd_ds_floats(L) scratch for the dS tiles, or nullptr to recompute dP in
