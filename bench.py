@@ -7,7 +7,7 @@ whole headline batch -- 768-dim config: B=8 sequences, H=12 heads, T=1024,
 head_dim 64, fp32 -- with Q, K, V, dO drawn from the seeded generator (seed 42)
 and already resident in HBM.  Outputs, the score buffer and the backward
 workspace are preallocated, so the timed region holds only kernel launches.
-Head dims the kept pair does not cover (42, 48) run wha_attn_fwd / wha_attn_bwd.
+Head dims the kept pair does not cover (42) run wha_attn_fwd / wha_attn_bwd.
 --recompute times the wha_attn_fwd / wha_attn_bwd pair instead.
 
 Prints one JSON line: value = tokens/s (B*T per step), plus TFLOP/s on the

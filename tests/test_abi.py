@@ -203,9 +203,9 @@ def test_scores_size_and_kept_pair_validation(pkg):
     rows = sum(T - 64 * kt for kt in range(T // 64))
     assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(B, H, T, 64))) == B * H * rows * 64 * 4
     assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_seq(B, T, 12, 768))) == B * H * rows * 64 * 4
-    for D in (100, 128, 52):
+    for D in (100, 128, 52, 48):
         assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(2, 2, 100, D))) > 0
-    for D in (48, 42, 16, 50):
+    for D in (44, 42, 16, 50):
         assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(2, 2, 100, D))) == 0
     odd = pkg.layout_bhtd(2, 2, 100, 64)
     odd.stride_t = 66

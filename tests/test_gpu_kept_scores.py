@@ -55,8 +55,9 @@ def test_kept_pair_small_shapes(pkg, torch_dev, B, H, T, D):
     assert np.abs(got[1] - r64[4]).max() < 2e-5
     # the recompute pair on the same inputs: same softmax, scores rounded in another order
     ref, _ = run_pair(pkg, torch, dev, q, k, v, do, keep=False)
-    assert np.array_equal(got[0], ref[0]) and np.array_equal(got[1], ref[1])  # same forward kernel
-    for a, b in zip(got[2:], ref[2:]):
+    if D != 48:  # the same forward kernel (head dim 48 keeps on the 64-wide one, else the exact 48-wide)
+        assert np.array_equal(got[0], ref[0]) and np.array_equal(got[1], ref[1])
+    for a, b in zip(got, ref):
         assert errors(a, b)[1] < 1e-6
 
 
@@ -81,6 +82,22 @@ def test_kept_pair_headline_config(pkg, torch_dev):
         *(oracle.bhtd_to_seq(a) for a in (q, k, v, do)), H, nthreads=16)
     for n, g, r in (("O", o, out), ("dQ", dq, rq), ("dK", dk, rk), ("dV", dv, rv)):
         ma, rl = assert_parity(f"kept headline {n}", g.cpu().numpy(), oracle.seq_to_bhtd(r, H))
+        print(f"  {n}: max_abs={ma:.2e} rel_l2={rl:.2e}", flush=True)
+
+
+def test_kept_pair_384_config(pkg, torch_dev):
+    """384-dim config (D = 48, kept pair on the 64-wide kernels with zero pad
+    quads) at full size, seed 42, against the threaded f32 oracle."""
+    torch, dev = torch_dev
+    B, H, T, D = 16, 8, 512, 48
+    print("case kept 384-dim", flush=True)
+    q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=42)
+    got, kept = run_pair(pkg, torch, dev, q, k, v, do, keep=True)
+    assert kept
+    out, rq, rk, rv = oracle.batch_fwd_bwd_f32_threaded(
+        *(oracle.bhtd_to_seq(a) for a in (q, k, v, do)), H, nthreads=16)
+    for n, g, r in (("O", got[0], out), ("dQ", got[2], rq), ("dK", got[3], rk), ("dV", got[4], rv)):
+        ma, rl = assert_parity(f"kept 384 {n}", g, oracle.seq_to_bhtd(r, H))
         print(f"  {n}: max_abs={ma:.2e} rel_l2={rl:.2e}", flush=True)
 
 

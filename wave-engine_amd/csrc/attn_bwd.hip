@@ -1150,7 +1150,7 @@ hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const
                            float* delta, float* ds, const View& L, bool vec, float scale,
                            hipStream_t stream, const float* sc) {
   if (sc != nullptr && (ds == nullptr || !WHA_DKV_DMA || !scores_kept(L, vec))) return hipErrorInvalidValue;
-  if (WHA_DKV_DMA && ds != nullptr && vec && dma_head_dim(L.D)) {
+  if (WHA_DKV_DMA && ds != nullptr && vec && (sc != nullptr ? kept_head_dim(L.D) : dma_head_dim(L.D))) {
     if (L.D == 64) return bwd_dma_t<64, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
     if (L.D < 64) return bwd_dma_t<64, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
     if (L.D == 128) return bwd_dma_t<128, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);

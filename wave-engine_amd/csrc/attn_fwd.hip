@@ -424,11 +424,12 @@ void fwd_dma_t(const float* q, const float* k, const float* v, float* o, float* 
 }
 }  // namespace
 
-bool scores_kept(const View& L, bool vec) { return WHA_FWD_DMA && vec && dma_head_dim(L.D); }
+bool scores_kept(const View& L, bool vec) { return WHA_FWD_DMA && vec && kept_head_dim(L.D); }
 
 hipError_t launch_attn_fwd(const float* q, const float* k, const float* v, float* o, float* lse,
                            const View& L, bool vec, float scale, hipStream_t stream, float* scores) {
-  if (WHA_FWD_DMA && vec && dma_head_dim(L.D)) {
+  if (scores != nullptr && !scores_kept(L, vec)) return hipErrorInvalidValue;
+  if (WHA_FWD_DMA && vec && (scores != nullptr ? kept_head_dim(L.D) : dma_head_dim(L.D))) {
     const float scale_log2 = (float)((double)scale * 1.4426950408889634);
     TimingScope ts("attn_fwd", stream);
     if (L.D == 64)

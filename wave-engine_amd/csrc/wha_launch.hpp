@@ -31,6 +31,12 @@ inline int padded_dim(int D) {
 // config: 0.167 vs 0.164 ms per step).
 inline bool dma_head_dim(int D) { return D % 4 == 0 && D > 48 && D <= 128; }
 
+// Head dims of the kept-scores pair: the above and 48 (padded to 64).  With the
+// scores kept the padded dK/dV kernel skips the Q K^T recompute, which makes
+// the pair faster than the exact 48-wide kernels (384-dim config: 0.154 vs
+// 0.164 ms per step).
+inline bool kept_head_dim(int D) { return D % 4 == 0 && D >= 48 && D <= 128; }
+
 // Optional per-kernel HIP-event timing (implemented in wha_api.hip).
 struct TimingScope {
   TimingScope(const char* name, hipStream_t stream);
