@@ -113,3 +113,34 @@ def test_kept_pair_4096_slice(pkg, torch_dev):
         *(oracle.bhtd_to_seq(sl(a)) for a in (q, k, v, do)), 1, nthreads=1)
     for n, g, r in (("O", got[0], out), ("dQ", got[2], rq), ("dK", got[3], rk), ("dV", got[4], rv)):
         assert_parity(f"kept 4096 {n}", sl(g), oracle.seq_to_bhtd(r, 1))
+
+
+def test_kept_pair_fused_qkv_layout_is_bit_identical(pkg, torch_dev):
+    """The kept pair on q, k, v read in place from one fused c_attn output
+    [B][T][3E] (the reference layout, stride_t = 3E; src/common/compute.rs:368-375)
+    and dq, dk, dv written into one [B][T][3E] gradient buffer gives the same bits
+    as on contiguous [B,H,T,D] tensors."""
+    torch, dev = torch_dev
+    for (B, H, T, D) in ((2, 12, 300, 64), (1, 4, 130, 48), (1, 2, 200, 128)):
+        print(f"case kept fused-qkv B={B} H={H} T={T} D={D}", flush=True)
+        E = H * D
+        q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=6)
+        base, kept = run_pair(pkg, torch, dev, q, k, v, do, keep=True)
+        assert kept
+        qkv = torch.from_numpy(np.concatenate([oracle.bhtd_to_seq(a) for a in (q, k, v)], axis=-1)).to(dev)
+        heads = lambda buf, c, w: buf.view(B, T, w)[:, :, c * E:(c + 1) * E].view(B, T, H, D).permute(0, 2, 1, 3)
+        tq, tk, tv = (heads(qkv, c, 3 * E) for c in range(3))
+        # o and dO share q's layout (one wha_layout per call): 3E-wide buffers, first E columns
+        dobuf = torch.zeros(B, T, 3 * E, device=dev)
+        dobuf[:, :, :E] = torch.from_numpy(oracle.bhtd_to_seq(do)).to(dev)
+        tdo = heads(dobuf, 0, 3 * E)
+        o = heads(torch.empty(B, T, 3 * E, device=dev), 0, 3 * E)
+        grads = torch.empty(B, T, 3 * E, device=dev)
+        dq, dk, dv = (heads(grads, c, 3 * E) for c in range(3))
+        sc = pkg.attn_scores_buffer(pkg.layout_of(tq), dev)
+        _, lse = pkg.attn_fwd(tq, tk, tv, out=o, scores=sc)
+        pkg.attn_bwd(tq, tk, tv, o, tdo, lse, dq=dq, dk=dk, dv=dv, scores=sc)
+        torch.cuda.synchronize()
+        got = [x.contiguous().cpu().numpy() for x in (o, lse, dq, dk, dv)]
+        for a, b_ in zip(got, base):
+            np.testing.assert_array_equal(a, b_)
