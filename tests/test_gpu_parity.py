@@ -191,7 +191,7 @@ def test_from_probs_matches_reference_contract(pkg, torch_dev):
     Q K^T; masked entries (j > t) hold garbage that must never be read."""
     torch, dev = torch_dev
     rng = np.random.default_rng(0)
-    for (B, H, T, D) in ((2, 3, 100, 64), (1, 4, 96, 42), (1, 2, 257, 128)):
+    for (B, H, T, D) in ((2, 3, 100, 64), (1, 4, 96, 42), (1, 2, 257, 128), (1, 2, 130, 56), (1, 1, 70, 100)):
         print(f"case from_probs B={B} H={H} T={T} D={D}", flush=True)
         q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=11)
         qs, ks, vs, dos = (oracle.bhtd_to_seq(a) for a in (q, k, v, do))

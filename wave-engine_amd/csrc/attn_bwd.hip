@@ -134,6 +134,21 @@ __global__ __launch_bounds__(256) void attn_bwd_stats_kernel(const float* __rest
 
 size_t bwd_stats_floats(const View& L) { return (size_t)L.B * L.H * ((L.T + 31) / 32 * 32) * 2; }
 
+// Stats blocks of the from-probabilities path (attn_bwd_dkv_dma_kernel with
+// PROBS): block j of a (b,h) gets 0 in the -LSE half (P is given, no LSE) and
+// -Delta_t for t = 32j..32j+31 (0 past T), Delta from the [B][H][T] pass.
+__global__ __launch_bounds__(256) void attn_bwd_probs_stats_kernel(const float* __restrict__ delta,
+                                                                   float* __restrict__ stats, View L) {
+  const int Tb = (L.T + 31) / 32 * 32;
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= (int64_t)L.B * L.H * Tb) return;
+  const int t = (int)(r % Tb);
+  const int64_t bh = r / Tb;
+  float* blk = stats + (bh * (Tb / 32) + t / 32) * 64 + (t % 32);
+  blk[0] = 0.f;
+  blk[32] = t < L.T ? -delta[bh * L.T + t] : 0.f;
+}
+
 namespace {
 bool delta_vec(const float* o, const float* d_o, const View& L) {
   return ((reinterpret_cast<uintptr_t>(o) | reinterpret_cast<uintptr_t>(d_o)) & 15) == 0 && L.D % 4 == 0 &&
@@ -533,11 +548,16 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
 // SAVE, same layout as DS) instead of Q K^T: a lane's 8 scores of the next
 // sub-tile are loaded while the current one is consumed (two register sets,
 // alternating with the unrolled loop), and K is not needed at all.
+// PROBS (with SAVED): SC is the caller's att [B][H][T][T] and P is read as
+// given (the reference's attention_backward contract, src/cpu/backward.rs:330):
+// no exponential, rows and columns clamped into the tensor (those entries are
+// masked), entries after the diagonal never used unmasked; the stats blocks
+// then hold only -Delta (attn_bwd_probs_stats_kernel).
 // three blocks per CU at head dim 64, two at 128 (LDS and VGPR budgets)
 #ifndef WHA_DMA_WPE
 #define WHA_DMA_WPE(DP) __attribute__((amdgpu_waves_per_eu((DP) == 64 ? 3 : 2)))
 #endif
-template <int DP, bool DS_OUT, bool PADQ, bool SAVED>
+template <int DP, bool DS_OUT, bool PADQ, bool SAVED, bool PROBS = false>
 __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ stats, float* __restrict__ dK,
@@ -632,11 +652,21 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
     float* dsw = DS_OUT ? DS + kcol : nullptr;
     // SAVED: a lane's scores of sub-tile st (rows 32st+16mt+4g+i, this lane's key)
     auto load_sc = [&](int st, float (&dst)[8]) {
-      const float* src = SC + kcol + (int64_t)(st * BSUB + 4 * g) * 64;
+      if constexpr (PROBS) {
+        const float* src = SC + (int64_t)bh * L.T * L.T + min(krow, L.T - 1);
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
+        for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dst[4 * mt + i] = src[(16 * mt + i) * 64];
+          for (int i = 0; i < 4; ++i)
+            dst[4 * mt + i] = src[(int64_t)min(st * BSUB + 16 * mt + 4 * g + i, L.T - 1) * L.T];
+        }
+      } else {
+        const float* src = SC + kcol + (int64_t)(st * BSUB + 4 * g) * 64;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dst[4 * mt + i] = src[(16 * mt + i) * 64];
+        }
       }
     };
 
@@ -674,7 +704,7 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) s[mt][i] += sc[4 * mt + i];
+          for (int i = 0; i < 4; ++i) s[mt][i] = PROBS ? sc[4 * mt + i] : s[mt][i] + sc[4 * mt + i];
         }
       }
       // lane element (mt,i): query qb+16mt+4g+i, key krow
@@ -682,7 +712,7 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
       for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p = fast_exp2(s[mt][i]);
+          const float p = PROBS ? s[mt][i] : fast_exp2(s[mt][i]);
           if (MASKED) {
             const int q = qb + 16 * mt + 4 * g + i;
             const bool valid = (q >= krow) & (q < q_end);
@@ -1168,12 +1198,59 @@ hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const
 #undef WHA_BWD
 }
 
+namespace {
+// Head dims dma_head_dim() accepts, 128-bit operands, dS buffer present: the
+// Delta pass (dP and sum_j att dP), its values packed into stats blocks, the
+// direct-to-LDS key-stationary kernel reading P from att (dK, dV, dS), then
+// dQ from dS.
+template <int DP, bool PADQ, bool AV>
+hipError_t bwd_probs_dma_t(const float* d_o, const float* q, const float* k, const float* v, const float* att,
+                           float* dq, float* dk, float* dv, float* delta, float* stats, float* ds, const View& L,
+                           float scale, hipStream_t stream) {
+  const int n_t64 = (L.T + 63) / 64;
+  hipError_t e;
+  {
+    TimingScope ts("attn_bwd_probs_delta", stream);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<DP, 4, true, kDeltaFromProbs, AV>), dim3((unsigned)(n_t64 * L.B * L.H)),
+                       dim3(256), 0, stream, q, k, v, d_o, (const float*)nullptr, delta, att, (float*)nullptr, L,
+                       scale, 0.f);
+    const int64_t n = (int64_t)L.B * L.H * ((L.T + 31) / 32 * 32);
+    hipLaunchKernelGGL(attn_bwd_probs_stats_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       (const float*)delta, stats, L);
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) return e;
+  const dim3 grid((unsigned)((n_t64 + 1) / 2 * L.B * L.H));
+  {
+    TimingScope ts("attn_bwd_probs_dkv", stream);
+    hipLaunchKernelGGL((attn_bwd_dkv_dma_kernel<DP, true, PADQ, true, true>), grid, dim3(256), 0, stream, q, k, v,
+                       d_o, (const float*)stats, dk, dv, ds, att, L, scale, 0.f);
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) return e;
+  TimingScope ts("attn_bwd_probs_dq", stream);
+  hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<DP, PADQ>), grid, dim3(256), 0, stream, k, (const float*)ds, dq, L,
+                     scale);
+  return hipGetLastError();
+}
+}  // namespace
+
 hipError_t launch_attn_bwd_probs(const float* d_o, const float* q, const float* k, const float* v,
-                                 const float* att, float* dq, float* dk, float* dv, float* delta,
+                                 const float* att, float* dq, float* dk, float* dv, float* delta, float* stats,
                                  float* ds, const View& L, bool vec, float scale, hipStream_t stream) {
   // 128-bit att loads need every row start 16-byte aligned (the non-VEC build
   // keeps scalar loads: it only serves unaligned operands)
   const bool av = vec && L.T % 4 == 0 && (reinterpret_cast<uintptr_t>(att) & 15) == 0;
+  if (WHA_DKV_DMA && vec && ds != nullptr && stats != nullptr && dma_head_dim(L.D)) {
+#define WHA_BWDP_DMA(DP, PADQ)                                                                                \
+  return av ? bwd_probs_dma_t<DP, PADQ, true>(d_o, q, k, v, att, dq, dk, dv, delta, stats, ds, L, scale, stream) \
+            : bwd_probs_dma_t<DP, PADQ, false>(d_o, q, k, v, att, dq, dk, dv, delta, stats, ds, L, scale, stream)
+    if (L.D == 64) WHA_BWDP_DMA(64, false);
+    if (L.D < 64) WHA_BWDP_DMA(64, true);
+    if (L.D == 128) WHA_BWDP_DMA(128, false);
+    WHA_BWDP_DMA(128, true);
+#undef WHA_BWDP_DMA
+  }
 #define WHA_BWDP(DP)                                                                                           \
   return !vec ? bwd_probs_t<DP, false, false>(d_o, q, k, v, att, dq, dk, dv, delta, ds, L, scale, stream)    \
          : av ? bwd_probs_t<DP, true, true>(d_o, q, k, v, att, dq, dk, dv, delta, ds, L, scale, stream)      \

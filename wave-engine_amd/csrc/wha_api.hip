@@ -418,7 +418,7 @@ int wha_attn_bwd_kept(const float* q, const float* k, const float* v, const floa
 
 size_t wha_attn_bwd_from_probs_workspace_size(const wha_layout* layout) {
   if (!layout || layout->B <= 0 || layout->H <= 0 || layout->T <= 0) return 0;
-  return delta_bytes(layout) + ds_bytes(layout);
+  return delta_bytes(layout) + stats_bytes(layout) + ds_bytes(layout);
 }
 
 int wha_attn_bwd_from_probs(const float* d_pre_proj, const float* q, const float* k, const float* v,
@@ -439,9 +439,11 @@ int wha_attn_bwd_from_probs(const float* d_pre_proj, const float* q, const float
     return rc;
   const bool vec = vec_ok(V, {d_pre_proj, q, k, v, dq, dk, dv});
   const size_t dsb = ds_bytes(layout);
-  float* ds = dsb ? reinterpret_cast<float*>(static_cast<char*>(ws) + delta_bytes(layout)) : nullptr;
+  float* stats = reinterpret_cast<float*>(static_cast<char*>(ws) + delta_bytes(layout));
+  float* ds = dsb ? reinterpret_cast<float*>(static_cast<char*>(ws) + delta_bytes(layout) + stats_bytes(layout))
+                  : nullptr;
   hipError_t e = wha::launch_attn_bwd_probs(d_pre_proj, q, k, v, att, dq, dk, dv, static_cast<float*>(ws),
-                                            ds, V, vec, scale, s);
+                                            stats, ds, V, vec, scale, s);
   if (e != hipSuccess) return hip_fail(e, "wha_attn_bwd_from_probs launch");
   g_err[0] = 0;
   return WHA_OK;
@@ -1067,7 +1069,7 @@ int wha_host_attention_backward(const float* d_pre_proj, const float* q, const f
     e = hipMemcpyAsync(d_att, att, (size_t)n_head * T * T * sizeof(float), hipMemcpyHostToDevice, s);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync H2D");
   const float scale = 1.0f / sqrtf((float)(E / n_head));  // src/cpu/backward.rs:326
-  e = wha::launch_attn_bwd_probs(d_do, d_q, d_k, d_v, d_att, d_dq, d_dk, d_dv, d_delta, nullptr, V,
+  e = wha::launch_attn_bwd_probs(d_do, d_q, d_k, d_v, d_att, d_dq, d_dk, d_dv, d_delta, nullptr, nullptr, V,
                                  vec_ok(V, {d_do, d_q, d_k, d_v, d_dq, d_dk, d_dv}), scale, s);
   if (e != hipSuccess) return hip_fail(e, "attention backward launch");
   float* outs[3] = {dq, dk, dv};

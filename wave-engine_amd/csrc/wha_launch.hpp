@@ -76,10 +76,11 @@ hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const
                            hipStream_t stream, const float* scores = nullptr);
 
 // Backward from given probabilities att [B][H][T][T].  delta: [B*H*T] scratch;
+// stats: bwd_stats_floats(L) scratch (the direct-to-LDS path's -Delta blocks);
 // ds: bwd_ds_floats(L) scratch for the dS tiles, or nullptr to recompute dP in
 // a query-stationary dQ pass instead.
 hipError_t launch_attn_bwd_probs(const float* d_o, const float* q, const float* k, const float* v,
-                                 const float* att, float* dq, float* dk, float* dv, float* delta,
+                                 const float* att, float* dq, float* dk, float* dv, float* delta, float* stats,
                                  float* ds, const View& L, bool vec, float scale, hipStream_t stream);
 
 // Split-K decode.  Workspace layout and size: decode_workspace_floats().
