@@ -134,21 +134,6 @@ __global__ __launch_bounds__(256) void attn_bwd_stats_kernel(const float* __rest
 
 size_t bwd_stats_floats(const View& L) { return (size_t)L.B * L.H * ((L.T + 31) / 32 * 32) * 2; }
 
-// Stats blocks of the from-probabilities path (attn_bwd_dkv_dma_kernel with
-// PROBS): block j of a (b,h) gets 0 in the -LSE half (P is given, no LSE) and
-// -Delta_t for t = 32j..32j+31 (0 past T), Delta from the [B][H][T] pass.
-__global__ __launch_bounds__(256) void attn_bwd_probs_stats_kernel(const float* __restrict__ delta,
-                                                                   float* __restrict__ stats, View L) {
-  const int Tb = (L.T + 31) / 32 * 32;
-  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (r >= (int64_t)L.B * L.H * Tb) return;
-  const int t = (int)(r % Tb);
-  const int64_t bh = r / Tb;
-  float* blk = stats + (bh * (Tb / 32) + t / 32) * 64 + (t % 32);
-  blk[0] = 0.f;
-  blk[32] = t < L.T ? -delta[bh * L.T + t] : 0.f;
-}
-
 namespace {
 bool delta_vec(const float* o, const float* d_o, const View& L) {
   return ((reinterpret_cast<uintptr_t>(o) | reinterpret_cast<uintptr_t>(d_o)) & 15) == 0 && L.D % 4 == 0 &&
@@ -552,7 +537,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
 // given (the reference's attention_backward contract, src/cpu/backward.rs:330):
 // no exponential, rows and columns clamped into the tensor (those entries are
 // masked), entries after the diagonal never used unmasked; the stats blocks
-// then hold only -Delta (attn_bwd_probs_stats_kernel).
+// then hold only -Delta (the Delta pass, launch_probs_delta_dma).
 // three blocks per CU at head dim 64, two at 128 (LDS and VGPR budgets)
 #ifndef WHA_DMA_WPE
 #define WHA_DMA_WPE(DP) __attribute__((amdgpu_waves_per_eu((DP) == 64 ? 3 : 2)))
@@ -1200,9 +1185,9 @@ hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const
 
 namespace {
 // Head dims dma_head_dim() accepts, 128-bit operands, dS buffer present: the
-// Delta pass (dP and sum_j att dP), its values packed into stats blocks, the
-// direct-to-LDS key-stationary kernel reading P from att (dK, dV, dS), then
-// dQ from dS.
+// Delta pass (dP and sum_j att dP, on the forward's tiles) writing the stats
+// blocks, the direct-to-LDS key-stationary kernel reading P from att (dK, dV,
+// dS), then dQ from dS.
 template <int DP, bool PADQ, bool AV>
 hipError_t bwd_probs_dma_t(const float* d_o, const float* q, const float* k, const float* v, const float* att,
                            float* dq, float* dk, float* dv, float* delta, float* stats, float* ds, const View& L,
@@ -1211,13 +1196,7 @@ hipError_t bwd_probs_dma_t(const float* d_o, const float* q, const float* k, con
   hipError_t e;
   {
     TimingScope ts("attn_bwd_probs_delta", stream);
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<DP, 4, true, kDeltaFromProbs, AV>), dim3((unsigned)(n_t64 * L.B * L.H)),
-                       dim3(256), 0, stream, q, k, v, d_o, (const float*)nullptr, delta, att, (float*)nullptr, L,
-                       scale, 0.f);
-    const int64_t n = (int64_t)L.B * L.H * ((L.T + 31) / 32 * 32);
-    hipLaunchKernelGGL(attn_bwd_probs_stats_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
-                       (const float*)delta, stats, L);
-    e = hipGetLastError();
+    e = launch_probs_delta_dma(d_o, v, att, stats, L, AV, stream);
   }
   if (e != hipSuccess) return e;
   const dim3 grid((unsigned)((n_t64 + 1) / 2 * L.B * L.H));

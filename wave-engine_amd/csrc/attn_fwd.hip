@@ -188,18 +188,25 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
 // reads them instead of recomputing Q K^T.  Entries after the diagonal hold
 // whatever the key tile gave (the backward masks them); rows past T are
 // written too (the layout pads every block to a multiple of 64 rows).
+// DELTA: the Delta pass of the from-probabilities backward on the same tiles:
+// Q is dO, K is V (scale 1), so the score contraction forms dP^T; each lane
+// takes sum_j att[q][j] dP[q][j] over its keys (att given, read one sub-tile
+// ahead as 16-byte loads along the row, masked entries selected away), and the
+// row's -Delta goes into the stats blocks of attn_bwd_dkv_dma_kernel (LSE
+// argument; 0 in the -LSE half and past T).  No softmax, no V operand, no O.
 constexpr float kLazyMax = 8.f;
 #ifndef WHA_FWD_WPE
 #define WHA_FWD_WPE __attribute__((amdgpu_waves_per_eu(3)))
 #endif
-template <int DP, bool PADQ, bool SAVE>
+template <int DP, bool PADQ, bool SAVE, bool DELTA = false, bool AV = false>
 __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const float* __restrict__ Q,
                                                                      const float* __restrict__ K,
                                                                      const float* __restrict__ V,
                                                                      float* __restrict__ O,
                                                                      float* __restrict__ LSE,
                                                                      float* __restrict__ SC, View L,
-                                                                     float scale_log2) {
+                                                                     float scale_log2,
+                                                                     const float* __restrict__ ATT = nullptr) {
   constexpr int DG = DP / 4, NDT = DP / 16;
   constexpr int QPR = DP / 4;            // quads per row
   constexpr int BSUB = 2048 / DP;        // keys per sub-tile (8 KB per operand)
@@ -255,7 +262,7 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
       const float* vp = reinterpret_cast<const float*>(vs + off[u]);
       if (PADQ && pad[u]) kp = vp = g_zero_quad;
       dma_quad(kp, Kd + 256 * (2 * wave + u));
-      dma_quad(vp, Vd + 256 * (2 * wave + u));
+      if constexpr (!DELTA) dma_quad(vp, Vd + 256 * (2 * wave + u));
     }
   };
 
@@ -283,8 +290,24 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
     const int key_last = min(qrow, L.T - 1);  // keys above it are masked
     // SAVE: this lane's row of the score layout, less 64 rows per column block
     float* sc_row = SAVE ? SC + ((int64_t)bh * ds_rows(L.T) + qrow) * 64 + 4 * g : nullptr;
+    // DELTA: this lane's att row (clamped into the tensor; rows past T are never stored)
+    const float* att_row = DELTA ? ATT + ((int64_t)bh * L.T + min(qrow, L.T - 1)) * L.T : nullptr;
+    float d_acc = 0.f;
+    floatx4 atA[NKT], atB[NKT];  // DELTA: att of the even / odd sub-tiles
+    auto load_att = [&](int st, floatx4 (&dst)[NKT]) {
+#pragma unroll
+      for (int mt = 0; mt < NKT; ++mt) {
+        const int c = st * BSUB + 16 * mt + 4 * g;  // keys c..c+3, clamped into the row (masked past it)
+        if constexpr (AV) {
+          dst[mt] = *reinterpret_cast<const floatx4*>(att_row + min(c, L.T - 4));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dst[mt][i] = att_row[min(c + i, L.T - 1)];
+        }
+      }
+    };
 
-    auto compute = [&](auto masked, int k0, const float* Ks, const float* Vs) {
+    auto compute = [&](auto masked, int k0, const float* Ks, const float* Vs, const floatx4 (&at)[NKT]) {
       constexpr bool MASKED = decltype(masked)::value;
       // S^T[key][query] in log2 units: MFMA rows are keys 16mt + lq, columns the wave's queries
       floatx4 s[NKT];
@@ -301,6 +324,18 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
         }
       }
       WHA_FENCE();
+      if constexpr (DELTA) {
+        // lane element (mt,i): dP of key k0 + 16mt + 4g + i and query qrow
+#pragma unroll
+        for (int mt = 0; mt < NKT; ++mt) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float t = at[mt][i] * s[mt][i];
+            d_acc += (MASKED && k0 + 16 * mt + 4 * g + i > key_last) ? 0.f : t;
+          }
+        }
+        return;
+      }
       // lane element (mt,i): key k0 + 16mt + 4g + i of query qrow, as s - m_i
       if constexpr (SAVE) {
         const int kt = k0 >> 6;
@@ -370,24 +405,41 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
     };
 
     // one sub-tile: wait for its loads, start the next one's, then consume it
-    auto step = [&](int st, const float* Ks, const float* Vs, float* Kn, float* Vn) {
+    auto step = [&](int st, const float* Ks, const float* Vs, float* Kn, float* Vn, const floatx4 (&at)[NKT],
+                    floatx4 (&at_next)[NKT]) {
       wait_vmem();
       __syncthreads();  // sub-tile st is in LDS; every wave is done with sub-tile st-1
       prio_by_remaining(left--, work);
-      if (st + 1 < n_sub) fetch(st + 1, Kn, Vn);
+      if (st + 1 < n_sub) {
+        fetch(st + 1, Kn, Vn);
+        if constexpr (DELTA) load_att(st + 1, at_next);
+      }
       const int k0 = st * BSUB;
       if (k0 > q0 + 15) return;  // every key follows every query of the wave
       if (k0 + BSUB - 1 <= q0 && k0 + BSUB <= L.T)
-        compute(std::false_type{}, k0, Ks, Vs);
+        compute(std::false_type{}, k0, Ks, Vs, at);
       else
-        compute(std::true_type{}, k0, Ks, Vs);
+        compute(std::true_type{}, k0, Ks, Vs, at);
     };
 
     __syncthreads();  // the previous pass's last sub-tile has been read by every wave
     fetch(0, Ks0, Vs0);
+    if constexpr (DELTA) load_att(0, atA);
     for (int st = 0; st < n_sub; st += 2) {
-      step(st, Ks0, Vs0, Ks1, Vs1);
-      if (st + 1 < n_sub) step(st + 1, Ks1, Vs1, Ks0, Vs0);
+      step(st, Ks0, Vs0, Ks1, Vs1, atA, atB);
+      if (st + 1 < n_sub) step(st + 1, Ks1, Vs1, Ks0, Vs0, atB, atA);
+    }
+
+    if constexpr (DELTA) {
+      // -Delta of the row into its stats block (rows past T within the block get 0)
+      const float delta = pair_sum32(pair_sum16(d_acc));
+      const int Tb = (L.T + 31) / 32 * 32;
+      if (g == 0 && qrow < Tb) {
+        float* blk = LSE + ((int64_t)bh * (Tb / 32) + qrow / 32) * 64 + qrow % 32;
+        blk[0] = 0.f;
+        blk[32] = qrow < L.T ? -delta : 0.f;
+      }
+      continue;
     }
 
     const float l_sum = pair_sum32(pair_sum16(l_i));
@@ -425,6 +477,35 @@ void fwd_dma_t(const float* q, const float* k, const float* v, float* o, float* 
 }  // namespace
 
 bool scores_kept(const View& L, bool vec) { return WHA_FWD_DMA && vec && kept_head_dim(L.D); }
+
+namespace {
+template <int DP, bool PADQ, bool AV>
+void probs_delta_t(const float* d_o, const float* v, const float* att, float* stats, const View& L,
+                   hipStream_t stream) {
+  const int n_qt = (L.T + 63) / 64;
+  const dim3 grid((unsigned)((n_qt + 1) / 2 * L.B * L.H));
+  hipLaunchKernelGGL((attn_fwd_dma_kernel<DP, PADQ, false, true, AV>), grid, dim3(256), 0, stream, d_o, v, v,
+                     (float*)nullptr, stats, (float*)nullptr, L, 1.f, att);
+}
+}  // namespace
+
+hipError_t launch_probs_delta_dma(const float* d_o, const float* v, const float* att, float* stats, const View& L,
+                                  bool av, hipStream_t stream) {
+  if (!dma_head_dim(L.D)) return hipErrorInvalidValue;
+#define WHA_PD(DP, PADQ)                                                 \
+  (av ? probs_delta_t<DP, PADQ, true>(d_o, v, att, stats, L, stream)   \
+      : probs_delta_t<DP, PADQ, false>(d_o, v, att, stats, L, stream))
+  if (L.D == 64)
+    WHA_PD(64, false);
+  else if (L.D < 64)
+    WHA_PD(64, true);
+  else if (L.D == 128)
+    WHA_PD(128, false);
+  else
+    WHA_PD(128, true);
+#undef WHA_PD
+  return hipGetLastError();
+}
 
 hipError_t launch_attn_fwd(const float* q, const float* k, const float* v, float* o, float* lse,
                            const View& L, bool vec, float scale, hipStream_t stream, float* scores) {

@@ -51,6 +51,13 @@ struct TimingScope {
 hipError_t launch_attn_fwd(const float* q, const float* k, const float* v, float* o, float* lse,
                            const View& L, bool vec, float scale, hipStream_t stream, float* scores = nullptr);
 
+// Delta pass of the from-probabilities backward on the forward's direct-to-LDS
+// tiles (dma_head_dim(D), 128-bit operands): stats <- the -Delta blocks of
+// attn_bwd_dkv_dma_kernel, Delta_t = sum_j att[t][j] (dO_t . V_j).  av: T % 4
+// == 0 and att 16-byte aligned (128-bit att loads).
+hipError_t launch_probs_delta_dma(const float* d_o, const float* v, const float* att, float* stats, const View& L,
+                                  bool av, hipStream_t stream);
+
 // Whether the forward can keep its scores for this layout (the direct-to-LDS
 // kernels: 16-byte-aligned operands, dma_head_dim(D)).
 bool scores_kept(const View& L, bool vec);
