@@ -466,27 +466,36 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
 
 namespace {
 
-// Output tile: the largest of 128 x 128, 64 x 128 that gives at least two
+// Output tile: the largest of 128 x 128, 64 x 128 that gives at least four
 // blocks per CU; 64-column tiles when N <= 64, and for N <= 256 when 64 x 128
-// tiles would leave CUs without a second block (same padding, twice the blocks).
+// tiles would leave CUs with fewer (same padding, twice the blocks).  Split-K
+// then aims for 1024 blocks.  Both thresholds were swept on the layer and wave
+// steps (tile 256/512/1024 blocks x split 512/1024/2048: 1024/1024 best, layer
+// 1.465 vs 1.501 ms at 512/512, wave 0.865 vs 0.877 ms).
 constexpr int kCUs = 256;
+#ifndef WHA_GEMM_TILE_BLOCKS
+#define WHA_GEMM_TILE_BLOCKS (4 * kCUs)
+#endif
+#ifndef WHA_GEMM_SPLIT_BLOCKS
+#define WHA_GEMM_SPLIT_BLOCKS 1024
+#endif
 struct GemmTile {
   int bm, bn;
 };
 GemmTile gemm_tile(int M, int N, int batch) {
   auto blocks = [&](int bm, int bn) { return (int64_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
-  if (N <= 64) return {blocks(128, 64) >= 2 * kCUs ? 128 : 64, 64};
-  if (blocks(128, kGBN) >= 2 * kCUs) return {128, kGBN};
-  if (blocks(64, kGBN) >= 2 * kCUs || N > 256) return {64, kGBN};
+  if (N <= 64) return {blocks(128, 64) >= WHA_GEMM_TILE_BLOCKS ? 128 : 64, 64};
+  if (blocks(128, kGBN) >= WHA_GEMM_TILE_BLOCKS) return {128, kGBN};
+  if (blocks(64, kGBN) >= WHA_GEMM_TILE_BLOCKS || N > 256) return {64, kGBN};
   return {64, 64};
 }
 
-// Split-K factor: aim for >= 512 blocks while keeping >= min_k k per split.
+// Split-K factor: aim for >= WHA_GEMM_SPLIT_BLOCKS blocks while keeping >= min_k k per split.
 int gemm_splits(int M, int N, int K, int batch, int min_k = 256) {
   const GemmTile t = gemm_tile(M, N, batch);
   const int tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) * batch;
   int splits = 1;
-  while (tiles * splits < 512 && (K / (splits * 2)) >= min_k) splits *= 2;
+  while (tiles * splits < WHA_GEMM_SPLIT_BLOCKS && (K / (splits * 2)) >= min_k) splits *= 2;
   return splits;
 }
 
