@@ -1,26 +1,39 @@
 """Benchmark: causal attention fwd+bwd on one MI355X (BASELINE.json metric).
 
-A step is one training forward (wha_attn_fwd_keep: the fused forward, which
-also keeps its raw scores for the backward) plus one fused backward
-(wha_attn_bwd_kept: reads those scores instead of recomputing Q K^T) over the
-whole headline batch -- 768-dim config: B=8 sequences, H=12 heads, T=1024,
+A step is one fused forward (wha_attn_fwd: online softmax, the T x T score
+matrix is never materialised; writes O and the row log-sum-exp) plus one fused
+backward (wha_attn_bwd: P recomputed on chip from the saved LSE) over the whole
+headline batch -- 768-dim config: B=8 sequences, H=12 heads, T=1024,
 head_dim 64, fp32 -- with Q, K, V, dO drawn from the seeded generator (seed 42)
-and already resident in HBM.  Outputs, the score buffer and the backward
-workspace are preallocated, so the timed region holds only kernel launches.
-Head dims the kept pair does not cover (42) run wha_attn_fwd / wha_attn_bwd.
---recompute times the wha_attn_fwd / wha_attn_bwd pair instead.
+and already resident in HBM.  Outputs and the backward workspace are
+preallocated, so the timed region holds only kernel launches.
 
-Prints one JSON line: value = tokens/s (B*T per step), plus TFLOP/s on the
-credited FLOPs (12*B*H*D*P, P = T(T+1)/2), a roofline object for the dominant
-kernel (algorithmic FLOPs per launch / its average HIP-event duration), and the
-CPU baseline (the reference-order f32 oracle, one thread per sequence).
+Before any timed region the step is repeated for at least --settle seconds
+(after the --warmup steps) so the GPU clocks have ramped; the line states that
+time as warmup_s.  The headline `value` and `ms_per_step` come from exactly
+--steps un-instrumented steps between two synchronisations.  Per-kernel
+durations (kernel_ms, roofline) come from a separate region of the same
+--steps steps with HIP events the library records on the launch stream around
+each kernel.
 
-    python bench.py [--steps K] [--warmup W] [--config 768|384|168|4096|decode|wave|wavedecode|layer]
+Beside the headline the same JSON line carries:
+  kept_scores  the training pair that keeps the forward's scores for the
+               backward (wha_attn_fwd_keep / wha_attn_bwd_kept), same batch;
+  configs      GPU-only results for every other BASELINE config (168-dim,
+               384-dim, 4096 preset: both pairs; 768 decode: HBM GB/s);
+  parity       max-abs / relative-L2 of the headline outputs against the CPU
+               f32 oracle run as the CPU baseline (same seeded inputs);
+  cpu_baseline the reference-order f32 oracle, one thread per sequence.
 
---config wave measures the wave (harmonic coherence) attention layer the
-reference trains with, forward and full backward with its projections;
---config layer the dot-product attention layer with its c_attn / c_proj
-projections (ComputeBackend::attention) forward and backward.
+    python bench.py [--steps K] [--warmup W] [--config 768|384|168|4096|decode|wave|wavedecode|layer|probs]
+                    [--kept] [--no-suite] [--no-cpu-baseline]
+
+--config other than 768 prints that workload's line alone (used to profile one
+workload).  --kept makes the kept-scores pair the one a single-config line
+times.  --config wave measures the wave (harmonic coherence) attention layer
+the reference trains with; --config layer the dot-product attention layer with
+its c_attn / c_proj projections (ComputeBackend::attention) forward and
+backward; --config probs the exact-contract backward (att given).
 """
 from __future__ import annotations
 
@@ -55,6 +68,7 @@ CONFIGS = {
 }
 
 METRIC = "causal attn fwd+bwd tokens/s & TFLOP/s (% fp32 MFMA peak), 768-dim seq1024"
+ATTN_KERNELS = ("attn_fwd", "attn_bwd_delta", "attn_bwd_dq", "attn_bwd_dkv")
 
 
 def credited_flops(B, H, T, D):
@@ -66,12 +80,62 @@ def credited_flops(B, H, T, D):
             "total": 12 * B * H * D * P}
 
 
+def settle(step, args, torch, min_s=None):
+    """--warmup untimed steps, then more steps until at least min_s seconds
+    (default --settle) have passed since the first, so that the GPU clocks
+    have ramped before a timed region.  Returns (seconds, steps)."""
+    min_s = args.settle if min_s is None else min_s
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    for _ in range(args.warmup):
+        step()
+        n += 1
+    torch.cuda.synchronize()
+    while time.perf_counter() - t0 < min_s:
+        for _ in range(4):
+            step()
+        n += 4
+        torch.cuda.synchronize()
+    return time.perf_counter() - t0, n
+
+
+def timed_kernels(step, steps, names, pkg, torch):
+    """Run `steps` steps with the library's HIP events around each kernel;
+    returns {name: {"avg_ms", "launches"}} and the wall time per step (ms)."""
+    torch.cuda.synchronize()
+    pkg.timing_reset()
+    pkg.timing_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps * 1e3
+    pkg.timing_enable(False)
+    kern = {}
+    for name in names:
+        ms, n = pkg.timing_read(name)
+        kern[name] = {"avg_ms": ms / max(n, 1), "total_ms": ms / steps, "launches": n}
+    pkg.timing_reset()
+    return kern, wall
+
+
+def timed_plain(step, steps, torch):
+    """Exactly `steps` un-instrumented steps between two synchronisations (ms per step)."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps * 1e3
+
+
 def cpu_baseline(cfg, seed=42, max_threads=None, min_seconds=10.0):
     """Reference-order f32 oracle (test infrastructure, the CPU baseline only):
     forward core + backward from att, one thread per sequence as the reference's
     training loop runs one thread per batch element.  The sample (one sequence
-    per thread) is repeated until at least min_seconds of CPU work have run."""
-    import numpy as np
+    per thread) is repeated until at least min_seconds of CPU work have run.
+    Returns (baseline dict, (out, dq, dk, dv) of the sample in [n][H][T][D])."""
     import oracle
     B, H, T, D = cfg["B"], cfg["H"], cfg["T"], cfg["D"]
     ncpu = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
@@ -82,7 +146,7 @@ def cpu_baseline(cfg, seed=42, max_threads=None, min_seconds=10.0):
     reps = 0
     t0 = time.perf_counter()
     while True:
-        oracle.batch_fwd_bwd_f32_threaded(qs, ks, vs, dos, H, nthreads=nthreads)
+        outs = oracle.batch_fwd_bwd_f32_threaded(qs, ks, vs, dos, H, nthreads=nthreads)
         reps += 1
         if time.perf_counter() - t0 >= min_seconds:
             break
@@ -92,63 +156,74 @@ def cpu_baseline(cfg, seed=42, max_threads=None, min_seconds=10.0):
     t1 = time.perf_counter()
     oracle.batch_fwd_bwd_f32_threaded(qs[:1], ks[:1], vs[:1], dos[:1], H, nthreads=1)
     one = time.perf_counter() - t1
-    return {"value": nseq * T / dt, "unit": "tokens/s", "cores": nthreads, "kind": "port",
+    base = {"value": nseq * T / dt, "unit": "tokens/s", "cores": nthreads, "kind": "port",
             "sample": f"{nseq} of the {B} sequences ({nseq}x{T} tokens, {H} heads, D={D}), fwd+bwd, "
                       f"one thread per sequence, repeated {reps}x; host has {ncpu} cores",
             "seconds_per_rep": dt, "tflops": flops / dt / 1e12, "nproc": ncpu,
             "one_thread_seconds_per_sequence": one}
+    return base, tuple(oracle.seq_to_bhtd(a, H) for a in outs)
 
 
-def run_attention(args, cfg, pkg, torch):
+def parity_of(got, want):
+    """max-abs and relative-L2 error of device outputs against CPU arrays."""
+    import numpy as np
+    res = {}
+    for name, g, w in zip(("O", "dQ", "dK", "dV"), got, want):
+        g = g[:w.shape[0]].detach().cpu().numpy().astype(np.float64)
+        w = w.astype(np.float64)
+        res[name] = {"max_abs": float(np.abs(g - w).max()),
+                     "rel_l2": float(np.linalg.norm(g - w) / max(np.linalg.norm(w), 1e-30))}
+    return res
+
+
+def attn_pair(args, cfg, pkg, torch, keep, inputs=None, settle_s=None):
+    """Times one pair (keep=False: wha_attn_fwd + wha_attn_bwd; keep=True:
+    wha_attn_fwd_keep + wha_attn_bwd_kept) on one config.  Returns the result
+    dict and the outputs (o, dq, dk, dv) of the last step."""
     B, H, T, D = cfg["B"], cfg["H"], cfg["T"], cfg["D"]
     dev = torch.device("cuda:0")
-    q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=42)
-    tq, tk, tv, tdo = (torch.from_numpy(a).to(dev) for a in (q, k, v, do))
+    if inputs is None:
+        inputs = tuple(torch.from_numpy(a).to(dev) for a in pkg.synth_inputs(B, H, T, D, seed=42))
+    tq, tk, tv, tdo = inputs
     o = torch.empty_like(tq)
     lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
     dq, dk, dv = (torch.empty_like(tq) for _ in range(3))
-    # pointers and layouts bound once; the forward keeps its scores for the backward unless --recompute
-    plan = pkg.AttnPlan(tq, tk, tv, o, lse, tdo, dq, dk, dv, keep_scores=not args.recompute)
+    # pointers and layouts bound once, so a step is two C calls
+    plan = pkg.AttnPlan(tq, tk, tv, o, lse, tdo, dq, dk, dv, keep_scores=keep)
 
     def step():
         plan.fwd()
         plan.bwd()
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm_s, warm_n = settle(step, args, torch, settle_s)
+    kern, ms_events = timed_kernels(step, args.steps, ATTN_KERNELS, pkg, torch)
+    ms = timed_plain(step, args.steps, torch)
+    flops = credited_flops(B, H, T, D)
+    dom = max(("attn_fwd", "attn_bwd_dq", "attn_bwd_dkv"), key=lambda n: kern[n]["avg_ms"])
+    achieved = flops[dom] / (kern[dom]["avg_ms"] * 1e-3) / 1e12
+    variant = "kept" if plan.keeps_scores else "recompute"
+    res = {
+        "pair": ("wha_attn_fwd_keep + wha_attn_bwd_kept" if plan.keeps_scores
+                 else "wha_attn_fwd + wha_attn_bwd"),
+        "backward": "scores kept by the forward" if plan.keeps_scores else "P recomputed from the saved LSE",
+        "ms_per_step": ms, "tokens_per_s": B * T / (ms * 1e-3),
+        "tflops": flops["total"] / (ms * 1e-3) / 1e12,
+        "pct_fp32_mfma_peak": 100.0 * flops["total"] / (ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
+        "kernel_ms": {n: round(kern[n]["avg_ms"], 5) for n in kern},
+        "ms_per_step_with_events": ms_events,
+        "warmup_s": round(warm_s, 3), "warmup_steps": warm_n,
+        "roofline": {"kernel": dom, "bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS,
+                     "traffic": load_traffic(f"{dom}[{variant}]", cfg),
+                     "algorithmic_flops_per_launch": flops[dom], "avg_launch_ms": kern[dom]["avg_ms"]},
+    }
+    return res, (o, dq, dk, dv), plan
 
-    # timed region: wall clock and HIP events on the launch stream around each kernel
-    pkg.timing_reset()
-    pkg.timing_enable(True)
+
+def step_medians(plan, steps, torch):
+    """Per-step forward and backward durations (events on the launch stream), medians in ms."""
     stream = torch.cuda.current_stream()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0.record(stream)
-    for _ in range(args.steps):
-        step()
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    pkg.timing_enable(False)
-    kern = {}
-    for name in ("attn_fwd", "attn_bwd_delta", "attn_bwd_dq", "attn_bwd_dkv"):
-        ms, n = pkg.timing_read(name)
-        kern[name] = {"avg_ms": ms / max(n, 1), "launches": n}
-    pkg.timing_reset()
-
-    # a second region without the per-kernel events, for the headline number
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    wall_plain = time.perf_counter() - t0
-
-    # fwd and bwd separately, per step (events on the launch stream), medians
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
-            torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    evs = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(steps)]
     torch.cuda.synchronize()
     for e0, e1, e2 in evs:
         e0.record(stream)
@@ -157,43 +232,92 @@ def run_attention(args, cfg, pkg, torch):
         plan.bwd()
         e2.record(stream)
     torch.cuda.synchronize()
-    fwd_each = sorted(e0.elapsed_time(e1) for e0, e1, _ in evs)
-    bwd_each = sorted(e1.elapsed_time(e2) for _, e1, e2 in evs)
-    median = lambda xs: xs[len(xs) // 2] if len(xs) % 2 else 0.5 * (xs[len(xs) // 2 - 1] + xs[len(xs) // 2])
 
-    ms_per_step = wall_plain / args.steps * 1e3
-    flops = credited_flops(B, H, T, D)
-    tokens = B * T
-    dom = max(("attn_fwd", "attn_bwd_dq", "attn_bwd_dkv"), key=lambda n: kern[n]["avg_ms"])
-    achieved = flops[dom] / (kern[dom]["avg_ms"] * 1e-3) / 1e12
-    traffic = load_traffic(dom, cfg)
-    fwd_ms = kern["attn_fwd"]["avg_ms"]
-    bwd_ms = kern["attn_bwd_delta"]["avg_ms"] + kern["attn_bwd_dq"]["avg_ms"] + kern["attn_bwd_dkv"]["avg_ms"]
+    def median(xs):
+        xs = sorted(xs)
+        return xs[len(xs) // 2] if len(xs) % 2 else 0.5 * (xs[len(xs) // 2 - 1] + xs[len(xs) // 2])
+
+    return median(e0.elapsed_time(e1) for e0, e1, _ in evs), median(e1.elapsed_time(e2) for _, e1, e2 in evs)
+
+
+def run_attention(args, cfg, pkg, torch):
+    """The headline line: the recompute pair (north-star design) on `cfg`, the
+    kept pair beside it; with the suite, every other BASELINE config."""
+    B, H, T, D = cfg["B"], cfg["H"], cfg["T"], cfg["D"]
+    dev = torch.device("cuda:0")
+    inputs = tuple(torch.from_numpy(a).to(dev) for a in pkg.synth_inputs(B, H, T, D, seed=42))
+    head, outs, plan = attn_pair(args, cfg, pkg, torch, keep=args.kept, inputs=inputs)
+    fwd_med, bwd_med = step_medians(plan, args.steps, torch)
+    ms = head["ms_per_step"]
+    k = head["kernel_ms"]
     res = {
         "metric": METRIC,
-        "value": tokens / (ms_per_step * 1e-3),
+        "value": head["tokens_per_s"],
         "unit": "tokens/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
+        "ms_per_step": ms,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic (seeded xorshift64 + Box-Muller, seed 42)",
         "config": {"workload": cfg["name"], "batch": B, "heads": H, "seq_len": T, "head_dim": D,
                    "layout": "[B,H,T,D] contiguous", "causal": True, "parallelism": "none (1 GPU)",
-                   "backward": "scores kept by the forward" if plan.keeps_scores else "S recomputed"},
-        "tflops": flops["total"] / (ms_per_step * 1e-3) / 1e12,
-        "pct_fp32_mfma_peak": 100.0 * flops["total"] / (ms_per_step * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
-        "kernel_ms": {n: round(kern[n]["avg_ms"], 5) for n in kern},
-        "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "ms_per_step_with_events": wall / args.steps * 1e3,
-        "fwd_ms_median": median(fwd_each), "bwd_ms_median": median(bwd_each),
-        "roofline": {"kernel": dom, "bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS, "traffic": traffic,
-                     "algorithmic_flops_per_launch": flops[dom],
-                     "avg_launch_ms": kern[dom]["avg_ms"]},
+                   "pair": head["pair"], "backward": head["backward"]},
+        "tflops": head["tflops"],
+        "pct_fp32_mfma_peak": head["pct_fp32_mfma_peak"],
+        "warmup_s": head["warmup_s"], "warmup_steps": head["warmup_steps"],
+        "kernel_ms": k,
+        "fwd_ms": k["attn_fwd"], "bwd_ms": k["attn_bwd_delta"] + k["attn_bwd_dq"] + k["attn_bwd_dkv"],
+        "ms_per_step_with_events": head["ms_per_step_with_events"],
+        "fwd_ms_median": fwd_med, "bwd_ms_median": bwd_med,
+        "roofline": head["roofline"],
     }
+    del plan
+    if not args.kept:
+        kept, kouts, _ = attn_pair(args, cfg, pkg, torch, keep=True, inputs=inputs, settle_s=0.5)
+        res["kept_scores"] = {n: kept[n] for n in ("pair", "ms_per_step", "tokens_per_s", "tflops",
+                                                   "pct_fp32_mfma_peak", "kernel_ms", "roofline")}
+        res["_outs_kept"] = kouts
+    res["_outs"] = outs
+    if args.suite and cfg is CONFIGS["768"]:
+        res["configs"] = {}
+        for key in ("168", "384", "4096"):
+            c = CONFIGS[key]
+            sub = {"workload": c["name"], "B": c["B"], "H": c["H"], "T": c["T"], "D": c["D"]}
+            for keep in (False, True):
+                r, _, p = attn_pair(args, c, pkg, torch, keep=keep, settle_s=0.5)
+                if keep and not p.keeps_scores:
+                    sub["kept"] = "same kernels as the recompute pair (this head dim keeps no scores)"
+                    continue
+                sub["kept" if keep else "recompute"] = {
+                    n: r[n] for n in ("ms_per_step", "tokens_per_s", "tflops", "pct_fp32_mfma_peak",
+                                      "kernel_ms", "roofline")}
+                del p
+            res["configs"][key] = sub
+            torch.cuda.empty_cache()
+        res["configs"]["decode"] = run_decode(args, CONFIGS["decode"], pkg, torch, sub=True)
+        torch.cuda.empty_cache()
     return res
 
 
-def run_decode(args, cfg, pkg, torch):
+def hbm_read_ceiling(torch, gib=4):
+    """Read-only stream rate: torch's sum over a `gib` GiB fp32 tensor (GB/s),
+    the practical ceiling for kernels that only read (the decode split)."""
+    x = torch.ones(gib * (1 << 28), dtype=torch.float32, device="cuda:0")
+    for _ in range(3):
+        x.sum()
+    torch.cuda.synchronize()
+    n = 10
+    t0 = time.perf_counter()
+    for _ in range(n):
+        x.sum()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / n
+    nbytes = x.numel() * 4
+    del x
+    torch.cuda.empty_cache()
+    return nbytes / dt / 1e9
+
+
+def run_decode(args, cfg, pkg, torch, sub=False):
     B, H, T, D = cfg["B"], cfg["H"], cfg["T"], cfg["D"]
     dev = torch.device("cuda:0")
     import numpy as np
@@ -202,30 +326,36 @@ def run_decode(args, cfg, pkg, torch):
     q = torch.from_numpy(g.normal(B * H * D, sd).reshape(B, H, D)).to(dev)
     kc = torch.from_numpy(g.normal(B * H * T * D, sd).reshape(B, H, T, D)).to(dev)
     vc = torch.from_numpy(g.normal(B * H * T * D, sd).reshape(B, H, T, D)).to(dev)
-    for _ in range(args.warmup):
-        pkg.decode_fwd(q, kc, vc)
-    torch.cuda.synchronize()
-    pkg.timing_reset()
-    pkg.timing_enable(True)
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        pkg.decode_fwd(q, kc, vc)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    pkg.timing_enable(False)
-    ms_split, n = pkg.timing_read("decode_split")
-    ms_merge, _ = pkg.timing_read("decode_merge")
+    ws = torch.empty(int(pkg.lib().wha_decode_workspace_size(ctypes.byref(pkg.layout_of(kc)))) // 4 + 64,
+                     device=dev)
+
+    def step():
+        pkg.decode_fwd(q, kc, vc, workspace=ws)
+
+    warm_s, warm_n = settle(step, args, torch, 0.5 if sub else None)
+    kern, _ = timed_kernels(step, args.steps, ("decode_split", "decode_merge"), pkg, torch)
+    ms = timed_plain(step, args.steps, torch)
     bytes_kv = 2 * B * H * T * D * 4
-    achieved = bytes_kv / (ms_split / n * 1e-3) / 1e9
-    ms = wall / args.steps * 1e3
-    return {"metric": "decode HBM GB/s (K+V bytes / time), 768-dim decode Tkv 8192", "value": bytes_kv / (ms * 1e-3) / 1e9,
-            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
-            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-            "data": "synthetic", "config": {"workload": cfg["name"], "batch": B, "heads": H, "kv_len": T,
-                                            "head_dim": D},
-            "kernel_ms": {"decode_split": ms_split / n, "decode_merge": ms_merge / n},
-            "roofline": {"kernel": "decode_split", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic("decode_split", cfg)}}
+    split = kern["decode_split"]["avg_ms"]
+    achieved = bytes_kv / (split * 1e-3) / 1e9
+    res = {"metric": "decode HBM GB/s (K+V bytes / time), 768-dim decode Tkv 8192",
+           "value": bytes_kv / (ms * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": ms,
+           "config": {"workload": cfg["name"], "batch": B, "heads": H, "kv_len": T, "head_dim": D},
+           "kernel_ms": {n: round(kern[n]["avg_ms"], 5) for n in kern},
+           "warmup_s": round(warm_s, 3),
+           "roofline": {"kernel": "decode_split", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                        "traffic": load_traffic("decode_split", cfg), "algorithmic_bytes_per_launch": bytes_kv,
+                        "avg_launch_ms": split}}
+    del q, kc, vc, ws
+    torch.cuda.empty_cache()
+    res["hbm_read_ceiling_gbs"] = hbm_read_ceiling(torch)
+    res["frac_of_read_ceiling"] = achieved / res["hbm_read_ceiling_gbs"]
+    if sub:
+        return res
+    res.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+                "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic"})
+    return res
 
 
 def run_probs(args, cfg, pkg, torch):
@@ -251,9 +381,7 @@ def run_probs(args, cfg, pkg, torch):
         pkg.attn_fwd(q, k, v, out=o, lse=lse_o)
         pkg.attn_bwd_from_probs(do, q, k, v, att, workspace=ws)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm_s, _ = settle(step, args, torch)
     names = ("attn_fwd", "attn_bwd_probs_delta", "attn_bwd_probs_dq", "attn_bwd_probs_dkv")
     pkg.timing_reset()
     pkg.timing_enable(True)
@@ -282,7 +410,7 @@ def run_probs(args, cfg, pkg, torch):
     flops = credited_flops(B, H, T, D)["total"]
     return {"metric": "causal attn fwd + exact-contract bwd (att given) tokens/s, 768-dim seq1024",
             "value": B * T / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-            "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+            "warmup": args.warmup, "warmup_s": round(warm_s, 3), "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded xorshift64 + Box-Muller, seed 42)",
             "config": {"workload": cfg["name"], "batch": B, "heads": H, "seq_len": T, "head_dim": D,
                        "parallelism": "none (1 GPU)"},
@@ -332,9 +460,7 @@ def run_wave(args, cfg, pkg, torch):
         _, _, cache = pkg.wave_attention_forward(W, x, out=out)
         pkg.wave_attention_backward_full(W, cache, dy, workspace=ws)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm_s, _ = settle(step, args, torch)
     names = ("wave_feat", "wave_fwd", "wave_bwd_delta", "wave_bwd_dkv", "wave_bwd_dq", "wave_feat_bwd",
              "wave_harmonic", "linear_fwd", "linear_bwd_dx", "linear_bwd_dw")
     pkg.timing_reset()
@@ -363,7 +489,7 @@ def run_wave(args, cfg, pkg, torch):
     return {
         "metric": "wave attention layer fwd+bwd tokens/s & TFLOP/s, 768-dim seq1024",
         "value": B * T / (ms_per_step * 1e-3), "unit": "tokens/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "warmup_s": round(warm_s, 3), "ms_per_step": ms_per_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded xorshift64 + Box-Muller, seed 42), random-init weights",
         "config": {"workload": cfg["name"], "batch": B, "heads": H, "seq_len": T, "head_dim": D,
@@ -405,9 +531,7 @@ def run_wave_decode(args, cfg, pkg, torch):
         cache.lengths = [L] * B
         return pkg.forward_one_attention(W, xn, cache, workspace=ws)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm_s, _ = settle(step, args, torch)
     pkg.timing_reset()
     pkg.timing_enable(True)
     for _ in range(args.steps):
@@ -435,7 +559,7 @@ def run_wave_decode(args, cfg, pkg, torch):
     alg_bytes = B * H * L * 12 + n_valid * D * 4
     achieved = alg_bytes / (kern["wave_kv_split"]["avg_ms"] * 1e-3) / 1e9
     return {"metric": "wave-attention KV-cache decode tokens/s (one new token per sequence), 768-dim, 8192 cached",
-            "value": B / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "value": B / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "warmup_s": round(warm_s, 3),
             "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
             "data": "synthetic prompts (seeded), random-init weights",
             "config": {"workload": cfg["name"], "batch": B, "heads": H, "cached": L, "head_dim": D,
@@ -500,9 +624,7 @@ def run_layer(args, cfg, pkg, torch):
         pkg.linear_bwd_dx(d_qkv, wa, out=dx)
         pkg.linear_bwd_dw(d_qkv, x, workspace=wsl)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm_s, _ = settle(step, args, torch)
     names = ("linear_fwd", "linear_bwd_dx", "linear_bwd_dw", "attn_fwd", "attn_bwd_delta",
              "attn_bwd_dkv", "attn_bwd_dq")
     pkg.timing_reset()
@@ -529,7 +651,7 @@ def run_layer(args, cfg, pkg, torch):
     return {
         "metric": "attention layer (c_attn + causal core + c_proj) fwd+bwd tokens/s & TFLOP/s, 768-dim seq1024",
         "value": M / (ms_per_step * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "warmup_s": round(warm_s, 3), "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded xorshift64 + Box-Muller, seed 42)",
         "config": {"workload": cfg["name"], "batch": B, "heads": H, "seq_len": T, "head_dim": D,
                    "parallelism": "none (1 GPU)"},
@@ -635,11 +757,17 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--settle", type=float, default=2.0,
+                    help="seconds the step is repeated (after --warmup steps) before the first timed region")
     ap.add_argument("--config", default="768", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-suite", dest="suite", action="store_false",
+                    help="768 only: leave out the other BASELINE configs")
+    ap.add_argument("--kept", action="store_true",
+                    help="time the kept-scores pair (wha_attn_fwd_keep + wha_attn_bwd_kept) as the line's "
+                         "main pair instead of the recompute pair")
     ap.add_argument("--recompute", action="store_true",
-                    help="time wha_attn_fwd + wha_attn_bwd (S recomputed in the backward) instead of the "
-                         "kept-scores pair")
+                    help="--config layer: the core runs the recompute pair instead of keeping its scores")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="first run a plain device copy (y = 2*x, torch elementwise kernel) of this many "
                          "MiB five times, as the known-size reference for rocprofv3 byte counters")
@@ -676,11 +804,24 @@ def main():
         res = run_probs(args, cfg, pkg, torch)
     else:
         res = run_attention(args, cfg, pkg, torch)
+    outs = res.pop("_outs", None)
+    outs_kept = res.pop("_outs_kept", None)
     if args.config in ("decode", "wavedecode", "probs"):
         res["cpu_baseline"] = None
     elif not args.no_cpu_baseline:
-        res["cpu_baseline"] = (wave_cpu_baseline(cfg) if args.config == "wave" else
-                               layer_cpu_baseline(cfg) if args.config == "layer" else cpu_baseline(cfg))
+        if args.config == "wave":
+            res["cpu_baseline"] = wave_cpu_baseline(cfg)
+        elif args.config == "layer":
+            res["cpu_baseline"] = layer_cpu_baseline(cfg)
+        else:
+            res["cpu_baseline"], cpu_outs = cpu_baseline(cfg)
+            # the same seeded inputs on both sides: the GPU outputs of the timed
+            # steps against the CPU f32 oracle's (the parity bar is 1e-4 max-abs,
+            # 1e-5 relative L2)
+            res["parity"] = {"vs": f"CPU f32 oracle, the {cpu_outs[0].shape[0]} sequences of the CPU sample",
+                             "pair": parity_of(outs, cpu_outs)}
+            if outs_kept is not None:
+                res["parity"]["kept_scores"] = parity_of(outs_kept, cpu_outs)
     print(json.dumps(res), flush=True)
 
 

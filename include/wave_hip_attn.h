@@ -45,6 +45,10 @@ extern "C" {
  *   device layout [B,H,T,D] contiguous: stride_b=H*T*D, stride_h=T*D, stride_t=D
  *   reference per-sequence layout [T][H*D] (src/common/compute.rs:370-374,
  *   :384-386) batched as [B][T][H*D]: stride_b=T*H*D, stride_h=D, stride_t=H*D
+ * Rows of distinct (b,h,t) must not overlap (the layout also describes the
+ * outputs): taken in increasing stride order, each dimension of extent > 1
+ * must step at least over the span of the smaller ones, else WHA_ERR_INVALID
+ * (zero strides, i.e. K or V shared across heads, are rejected).
  * lse is always [B][H][T] contiguous; workspaces are opaque scratch whose
  * size the matching *_workspace_size function reports. */
 typedef struct wha_layout {
@@ -103,8 +107,11 @@ int wha_attn_bwd(const float* q, const float* k, const float* v,
  * until the next wha_attn_fwd_keep into it.  When wha_attn_scores_size is 0
  * (head dims outside 48..128 or not a multiple of 4, strides not multiples of
  * 4 floats, or a score buffer above 8 GiB) scores may be NULL and the pair
- * behaves exactly as wha_attn_fwd / wha_attn_bwd.  Otherwise every tensor
- * must be 16-byte aligned (WHA_ERR_INVALID if not). */
+ * behaves exactly as wha_attn_fwd / wha_attn_bwd.  The pair also runs as
+ * wha_attn_fwd / wha_attn_bwd when a tensor is not 16-byte aligned (the
+ * forward then leaves scores untouched, and the backward, whose check covers
+ * the same q, k, v, o, recomputes); scores itself, when used, must be non-NULL
+ * and 16-byte aligned (WHA_ERR_INVALID if not). */
 size_t wha_attn_scores_size(const wha_layout* layout);
 int wha_attn_fwd_keep(const float* q, const float* k, const float* v, float* o,
                       float* lse, float* scores, const wha_layout* layout,

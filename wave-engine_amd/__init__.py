@@ -444,7 +444,9 @@ class AttnPlan:
         self._f = lib().wha_attn_fwd
         self._b = lib().wha_attn_bwd
         self._fname, self._bname = "wha_attn_fwd", "wha_attn_bwd"
-        scores = attn_scores_buffer(L, q.device) if (do is not None and keep_scores) else None
+        # the kept pair needs 16-byte-aligned tensors (the C ABI otherwise runs the recompute pair)
+        aligned = do is not None and all(t.data_ptr() % 16 == 0 for t in (q, k, v, o, do, dq, dk, dv))
+        scores = attn_scores_buffer(L, q.device) if (aligned and keep_scores) else None
         if do is not None:
             _same_layout(L, do, dq, dk, dv)
             need = attn_bwd_workspace_bytes(L)

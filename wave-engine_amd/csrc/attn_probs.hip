@@ -8,7 +8,9 @@
 // requested rows from Q, K and the forward's row log-sum-exp:
 //   out[b][h][r][j] = exp(q_t . k_j * scale - lse[b][h][t])  for j <= t = rows[r], else 0.
 // Rows are few (monitor use), so the kernel favours simplicity: one block per
-// (row, b, h), the query row in LDS, one key per thread per pass.
+// (b*h, row) -- b*h on grid.x, whose limit (2^31 - 1) covers every layout the
+// C ABI accepts, the <= 256 rows on grid.y -- the query row in LDS, one key per
+// thread per pass.
 #include "wha_launch.hpp"
 
 namespace wha {
@@ -19,8 +21,8 @@ __global__ __launch_bounds__(256) void attn_probs_rows_kernel(const float* __res
                                                               const float* __restrict__ LSE, RowList rl,
                                                               float* __restrict__ out, View L, float scale) {
   __shared__ float qs[DP];
-  const int r = blockIdx.x;
-  const int bh = blockIdx.y;
+  const int bh = blockIdx.x;
+  const int r = blockIdx.y;
   const int b = bh / L.H, h = bh % L.H;
   const int64_t base = (int64_t)b * L.sb + (int64_t)h * L.sh;
   const int t = rl.rows[r];  // validated on the host: 0 <= t < T
@@ -42,7 +44,7 @@ __global__ __launch_bounds__(256) void attn_probs_rows_kernel(const float* __res
 
 hipError_t launch_attn_probs_rows(const float* q, const float* k, const float* lse, const RowList& rl, float* out,
                                   const View& L, float scale, hipStream_t stream) {
-  const dim3 grid((unsigned)rl.n, (unsigned)(L.B * L.H));
+  const dim3 grid((unsigned)(L.B * L.H), (unsigned)rl.n);
   TimingScope ts("attn_probs_rows", stream);
   switch (padded_dim(L.D)) {
     case 48:

@@ -552,7 +552,8 @@ __global__ __launch_bounds__(256) void wave_harmonic_kernel(const float* __restr
   }
 }
 
-// Rows of att_weights_all on demand (attn.rs:240): one block per (row, b*h),
+// Rows of att_weights_all on demand (attn.rs:240): one block per (b*h, row)
+// (b*h on grid.x, rows on grid.y),
 // the query's features in LDS, one key per thread per pass;
 // p = exp(score - lse) where the mask admits the key, 0 where it excludes a
 // key j <= t, -inf after the diagonal (the reference's untouched entries).
@@ -561,8 +562,8 @@ __global__ __launch_bounds__(256) void wave_probs_rows_kernel(const float* __res
                                                               const float* __restrict__ LSE, RowList rl,
                                                               float* __restrict__ out, int T, float cs) {
   __shared__ float qs[kFP];
-  const int r = blockIdx.x;
-  const int64_t bh = blockIdx.y;
+  const int64_t bh = blockIdx.x;
+  const int r = blockIdx.y;
   const int t = rl.rows[r];  // validated on the host: 0 <= t < T
   const float* Fh = F + bh * T * kFP;
   const int* Bh = BK + bh * T;
@@ -705,7 +706,7 @@ hipError_t launch_wave_feat_bwd(const float* proj, const float* feat, const floa
 hipError_t launch_wave_probs_rows(const float* feat, const int* bucket, const float* lse, const RowList& rl,
                                   float* out, int B, int H, int T, float cs, hipStream_t stream) {
   TimingScope ts("wave_probs_rows", stream);
-  hipLaunchKernelGGL(wave_probs_rows_kernel, dim3((unsigned)rl.n, (unsigned)(B * H)), dim3(256), 0, stream, feat,
+  hipLaunchKernelGGL(wave_probs_rows_kernel, dim3((unsigned)(B * H), (unsigned)rl.n), dim3(256), 0, stream, feat,
                      bucket, lse, rl, out, T, cs);
   return hipGetLastError();
 }

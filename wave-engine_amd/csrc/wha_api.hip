@@ -51,6 +51,29 @@ int check_layout(const wha_layout* L, wha::View* v, const char* fn) {
                 (long long)L->stride_b, (long long)L->stride_h, (long long)L->stride_t, L->D);
   if ((int64_t)L->B * L->H * L->T > (int64_t)1 << 31)
     return fail(WHA_ERR_UNSUPPORTED, "%s: B*H*T too large", fn);
+  // The one layout also describes the outputs (o, dq, dk, dv), so distinct
+  // (b, h, t) rows must not overlap: a zero or too-small head/batch stride
+  // would let heads overwrite each other's gradients.  Accepted: the
+  // dimensions of extent > 1, in increasing stride order, each step at least
+  // the span of the smaller ones (rows of D floats) -- this covers [B,H,T,D],
+  // [B][T][H*D] and column slices of a fused [B][T][3E] row.
+  {
+    struct Dim {
+      int64_t n, stride;
+    } dims[3] = {{L->T, L->stride_t}, {L->H, L->stride_h}, {L->B, L->stride_b}};
+    std::sort(dims, dims + 3, [](const Dim& a, const Dim& b) { return a.stride < b.stride; });
+    int64_t span = L->D;
+    for (const Dim& d : dims) {
+      if (d.n <= 1) continue;
+      if (d.stride < span)
+        return fail(WHA_ERR_INVALID,
+                    "%s: strides (b=%lld, h=%lld, t=%lld) make rows of different (b,h,t) overlap for "
+                    "B=%d, H=%d, T=%d, D=%d (outputs share the layout and must not alias)",
+                    fn, (long long)L->stride_b, (long long)L->stride_h, (long long)L->stride_t, L->B, L->H, L->T,
+                    L->D);
+      span += d.stride * (d.n - 1);
+    }
+  }
   v->B = L->B;
   v->H = L->H;
   v->T = L->T;
@@ -372,12 +395,15 @@ int wha_attn_fwd_keep(const float* q, const float* k, const float* v, float* o, 
   if (rc) return rc;
   if ((rc = check_scale(scale, fn))) return rc;
   if (!q || !k || !v || !o) return fail(WHA_ERR_INVALID, "%s: q, k, v and o must be non-NULL", fn);
-  const bool keep = wha_attn_scores_size(layout) > 0;
+  // Tensors that are not 16-byte aligned run the recompute forward (scores
+  // untouched); wha_attn_bwd_kept then falls back as well, since its check
+  // includes the same q, k, v, o.
   const bool vec = vec_ok(V, {q, k, v, o});
+  const bool keep = wha_attn_scores_size(layout) > 0 && vec;
   if (keep) {
     if (!scores) return fail(WHA_ERR_INVALID, "%s: scores must be non-NULL (wha_attn_scores_size > 0)", fn);
-    if (!vec || (reinterpret_cast<uintptr_t>(scores) & 15))
-      return fail(WHA_ERR_INVALID, "%s: q, k, v, o and scores must be 16-byte aligned to keep scores", fn);
+    if (reinterpret_cast<uintptr_t>(scores) & 15)
+      return fail(WHA_ERR_INVALID, "%s: scores must be 16-byte aligned", fn);
   }
   hipError_t e = wha::launch_attn_fwd(q, k, v, o, lse, V, vec, scale, static_cast<hipStream_t>(stream),
                                       keep ? scores : nullptr);
@@ -396,11 +422,13 @@ int wha_attn_bwd_kept(const float* q, const float* k, const float* v, const floa
   if ((rc = check_scale(scale, fn))) return rc;
   if (!q || !k || !v || !o || !d_o || !lse || !dq || !dk || !dv)
     return fail(WHA_ERR_INVALID, "%s: every tensor pointer must be non-NULL", fn);
-  const bool keep = wha_attn_scores_size(layout) > 0;
+  // Unaligned tensors: the recompute backward (the kept scores are not needed).
   const bool vec = vec_ok(V, {q, k, v, o, d_o, dq, dk, dv});
+  const bool keep = wha_attn_scores_size(layout) > 0 && vec;
   if (keep) {
     if (!scores) return fail(WHA_ERR_INVALID, "%s: scores must be non-NULL (wha_attn_scores_size > 0)", fn);
-    if (!vec) return fail(WHA_ERR_INVALID, "%s: tensors must be 16-byte aligned to use kept scores", fn);
+    if (reinterpret_cast<uintptr_t>(scores) & 15)
+      return fail(WHA_ERR_INVALID, "%s: scores must be 16-byte aligned", fn);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   void* ws = nullptr;
