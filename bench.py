@@ -283,10 +283,10 @@ def run_attention(args, cfg, pkg, torch):
             c = CONFIGS[key]
             sub = {"workload": c["name"], "B": c["B"], "H": c["H"], "T": c["T"], "D": c["D"]}
             for keep in (False, True):
-                r, _, p = attn_pair(args, c, pkg, torch, keep=keep, settle_s=0.5)
-                if keep and not p.keeps_scores:
+                if keep and pkg.attn_scores_bytes(pkg.layout_bhtd(c["B"], c["H"], c["T"], c["D"])) == 0:
                     sub["kept"] = "same kernels as the recompute pair (this head dim keeps no scores)"
                     continue
+                r, _, p = attn_pair(args, c, pkg, torch, keep=keep, settle_s=0.5)
                 sub["kept" if keep else "recompute"] = {
                     n: r[n] for n in ("ms_per_step", "tokens_per_s", "tflops", "pct_fp32_mfma_peak",
                                       "kernel_ms", "roofline")}
@@ -299,22 +299,38 @@ def run_attention(args, cfg, pkg, torch):
 
 
 def hbm_read_ceiling(torch, gib=4):
-    """Read-only stream rate: torch's sum over a `gib` GiB fp32 tensor (GB/s),
-    the practical ceiling for kernels that only read (the decode split)."""
+    """Read-only stream rate (GB/s): a calibration kernel (wave-engine_amd/
+    libwha_hbm_probe.so, 16-byte loads grid-stride, one float written per
+    thread) over a `gib` GiB buffer, best of a few grid sizes -- the practical
+    ceiling for kernels that only read, such as the decode split kernel."""
+    probe = ctypes.CDLL(str(ROOT / "wave-engine_amd" / "libwha_hbm_probe.so"))
+    probe.whp_read_stream.restype = ctypes.c_int
+    probe.whp_read_stream.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
+                                      ctypes.c_void_p]
     x = torch.ones(gib * (1 << 28), dtype=torch.float32, device="cuda:0")
-    for _ in range(3):
-        x.sum()
-    torch.cuda.synchronize()
-    n = 10
-    t0 = time.perf_counter()
-    for _ in range(n):
-        x.sum()
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / n
-    nbytes = x.numel() * 4
+    best = (0.0, 0)
+    for blocks in (1024, 2048, 4096, 8192):
+        out = torch.empty(blocks * 256, dtype=torch.float32, device="cuda:0")
+        st = torch.cuda.current_stream().cuda_stream
+
+        def run():
+            rc = probe.whp_read_stream(x.data_ptr(), x.numel() // 4, out.data_ptr(), blocks, st)
+            if rc:
+                raise RuntimeError(f"whp_read_stream failed ({rc})")
+
+        for _ in range(3):
+            run()
+        torch.cuda.synchronize()
+        n = 10
+        t0 = time.perf_counter()
+        for _ in range(n):
+            run()
+        torch.cuda.synchronize()
+        gbs = x.numel() * 4 / ((time.perf_counter() - t0) / n) / 1e9
+        best = max(best, (gbs, blocks))
     del x
     torch.cuda.empty_cache()
-    return nbytes / dt / 1e9
+    return {"gbs": best[0], "blocks": best[1], "buffer_gib": gib}
 
 
 def run_decode(args, cfg, pkg, torch, sub=False):
@@ -349,8 +365,8 @@ def run_decode(args, cfg, pkg, torch, sub=False):
                         "avg_launch_ms": split}}
     del q, kc, vc, ws
     torch.cuda.empty_cache()
-    res["hbm_read_ceiling_gbs"] = hbm_read_ceiling(torch)
-    res["frac_of_read_ceiling"] = achieved / res["hbm_read_ceiling_gbs"]
+    res["hbm_read_ceiling"] = hbm_read_ceiling(torch)
+    res["frac_of_read_ceiling"] = achieved / res["hbm_read_ceiling"]["gbs"]
     if sub:
         return res
     res.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
