@@ -153,6 +153,22 @@ int wha_decode_fwd(const float* q, const float* k_cache, const float* v_cache,
                    float* o, float* lse, void* workspace, size_t workspace_bytes,
                    const wha_layout* cache_layout, float scale, void* stream);
 
+/* wha_decode_fwd that allocates nothing, for callers that cannot call
+ * hipMalloc (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid allocation).  No counterpart in the reference: it exists for those
+ * callers only.  The split-K partials live in a static device array of
+ * 16 MiB that every GPU the library runs on holds until the process ends;
+ * layouts whose partials need more (wha_decode_workspace_size above 16 MiB,
+ * e.g. B*H = 768 at D = 64 beyond about 82 000 cached keys) return
+ * WHA_ERR_WORKSPACE before any pointer is looked at.  All calls on one GPU
+ * share that array: calls that overlap on one GPU (several streams or host
+ * threads at once) race and must be serialised by the caller.  Otherwise the
+ * same contract and results as wha_decode_fwd. */
+int wha_decode_fwd_noalloc(const float* q, const float* k_cache,
+                           const float* v_cache, float* o, float* lse,
+                           const wha_layout* cache_layout, float scale,
+                           void* stream);
+
 /* Rows of the attention probabilities on demand, for consumers of materialised
  * P: the head monitor reads the last row of every head
  * (src/monitors/attn_monitor.rs:26-80) and the softmax_rows value contract

@@ -43,6 +43,9 @@ extern "C" {
     pub fn wha_decode_fwd(q: *const f32, k_cache: *const f32, v_cache: *const f32, o: *mut f32,
                           lse: *mut f32, workspace: *mut c_void, workspace_bytes: usize,
                           cache_layout: *const WhaLayout, scale: f32, stream: *mut c_void) -> c_int;
+    pub fn wha_decode_fwd_noalloc(q: *const f32, k_cache: *const f32, v_cache: *const f32, o: *mut f32,
+                                  lse: *mut f32, cache_layout: *const WhaLayout, scale: f32,
+                                  stream: *mut c_void) -> c_int;
     pub fn wha_attn_probs_rows(q: *const f32, k: *const f32, lse: *const f32, rows: *const i32, n_rows: i32,
                                out: *mut f32, layout: *const WhaLayout, scale: f32, stream: *mut c_void) -> c_int;
     pub fn wha_linear_fwd(x: *const f32, ldx: i64, w: *const f32, b: *const f32, y: *mut f32, ldy: i64,

@@ -275,3 +275,20 @@ def test_plan_keeps_scores_only_for_aligned_tensors():
     assert "data_ptr() % 16 == 0" in src
     api = (ROOT / "wave-engine_amd" / "csrc" / "wha_api.hip").read_text()
     assert api.count("wha_attn_scores_size(layout) > 0 && vec") == 2
+
+
+def test_noalloc_decode_rejects_layouts_beyond_its_scratch(pkg):
+    """wha_decode_fwd_noalloc checks the split-K scratch size (16 MiB static
+    array) before the pointers, so NULL pointers with a too-large layout get
+    WHA_ERR_WORKSPACE and nothing reaches the device."""
+    L = pkg.lib()
+    WHA_ERR_WORKSPACE = -4
+    null = ctypes.c_void_p(0)
+    big = pkg.layout_bhtd(64, 12, 1 << 17, 64)             # 768 (b,h) x 128 splits x 66 floats
+    assert L.wha_decode_workspace_size(ctypes.byref(big)) > 16 << 20
+    rc = L.wha_decode_fwd_noalloc(null, null, null, null, None, ctypes.byref(big), 0.125, None)
+    assert rc == WHA_ERR_WORKSPACE and b"static" in L.wha_last_error(), L.wha_last_error()
+    fits = pkg.layout_bhtd(64, 12, 8192, 64)               # the decode config: 1.6 MB of partials
+    assert L.wha_decode_workspace_size(ctypes.byref(fits)) <= 16 << 20
+    rc = L.wha_decode_fwd_noalloc(null, null, null, null, None, ctypes.byref(fits), 0.125, None)
+    assert rc == WHA_ERR_INVALID and b"non-NULL" in L.wha_last_error()

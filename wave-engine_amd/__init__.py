@@ -40,7 +40,7 @@ EXPORTED_SYMBOLS = (
     "wha_attn_fwd", "wha_attn_bwd_workspace_size", "wha_attn_bwd",
     "wha_attn_bwd_from_probs_workspace_size", "wha_attn_bwd_from_probs",
     "wha_attn_scores_size", "wha_attn_fwd_keep", "wha_attn_bwd_kept",
-    "wha_decode_workspace_size", "wha_decode_fwd", "wha_attn_probs_rows",
+    "wha_decode_workspace_size", "wha_decode_fwd", "wha_decode_fwd_noalloc", "wha_attn_probs_rows",
     "wha_wave_fwd", "wha_wave_bwd_workspace_size", "wha_wave_bwd", "wha_wave_probs_rows",
     "wha_wave_kv_prefill_workspace_size", "wha_wave_kv_prefill", "wha_wave_kv_decode_workspace_size",
     "wha_wave_kv_decode", "wha_host_wave_attention_forward", "wha_host_wave_attention_backward",
@@ -141,6 +141,7 @@ def lib():
         L.wha_decode_workspace_size.argtypes = [lp]
         L.wha_decode_workspace_size.restype = sz
         L.wha_decode_fwd.argtypes = [vp] * 5 + [vp, sz, lp, ctypes.c_float, vp]
+        L.wha_decode_fwd_noalloc.argtypes = [vp] * 5 + [lp, ctypes.c_float, vp]
         i64 = ctypes.c_int64
         L.wha_linear_fwd.argtypes = [vp, i64, vp, vp, vp, i64, i64, i32, i32, vp]
         L.wha_linear_bwd_dx.argtypes = [vp, i64, vp, vp, i64, i64, i32, i32, vp]
@@ -364,6 +365,25 @@ def decode_fwd(q, k_cache, v_cache, scale=None, want_lse=False, workspace=None):
     _check("wha_decode_fwd", lib().wha_decode_fwd(
         _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(o), _ptr(lse) if want_lse else None,
         _ptr(workspace), ws_bytes, ctypes.byref(L), s, _stream_ptr(q)))
+    return (o, lse) if want_lse else o
+
+
+def decode_fwd_noalloc(q, k_cache, v_cache, scale=None, want_lse=False, out=None, lse=None):
+    """decode_fwd through wha_decode_fwd_noalloc: the split-K partials live in
+    the library's static device scratch (no allocation inside the call; calls
+    that overlap on one GPU race).  out / lse may be preallocated."""
+    torch = _torch()
+    L = layout_of(k_cache)
+    _same_layout(L, v_cache)
+    if tuple(q.shape) != (L.B, L.H, L.D) or not q.is_contiguous():
+        raise ValueError(f"q must be a contiguous [B,H,D] tensor, got {tuple(q.shape)}")
+    o = torch.empty_like(q) if out is None else out
+    if want_lse and lse is None:
+        lse = torch.empty((L.B, L.H), dtype=torch.float32, device=q.device)
+    s = default_scale(L.D) if scale is None else float(scale)
+    _check("wha_decode_fwd_noalloc", lib().wha_decode_fwd_noalloc(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(o), _ptr(lse) if want_lse else None,
+        ctypes.byref(L), s, _stream_ptr(q)))
     return (o, lse) if want_lse else o
 
 

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -524,6 +525,74 @@ int wha_decode_fwd(const float* q, const float* k_cache, const float* v_cache, f
   const bool vec = vec_ok(V, {k_cache, v_cache});
   hipError_t e = wha::launch_decode(q, k_cache, v_cache, o, lse, static_cast<float*>(ws), V, vec, scale, s);
   if (e != hipSuccess) return hip_fail(e, "wha_decode_fwd launch");
+  g_err[0] = 0;
+  return WHA_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- allocation-free decode
+// wha_decode_fwd_noalloc keeps its split-K partials in this file-scope device
+// array instead of a workspace.  Each GPU holds its own copy for the life of
+// the process; host code must use the per-device address from
+// hipGetSymbolAddress, never the array's name (a host-side stand-in).
+static constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// The current device's address of `scratch`, resolved once per device.
+int noalloc_scratch(void** out, const char* fn) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(WHA_ERR_UNSUPPORTED, "%s: device index %d is not below %d", fn, dev, kMaxDevices);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return WHA_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int wha_decode_fwd_noalloc(const float* q, const float* k_cache, const float* v_cache, float* o, float* lse,
+                           const wha_layout* cache_layout, float scale, void* stream) {
+  static const char* fn = "wha_decode_fwd_noalloc";
+  wha::View V;
+  int rc = check_layout(cache_layout, &V, fn);
+  if (rc) return rc;
+  if ((rc = check_scale(scale, fn))) return rc;
+  // the size limit is checked before the pointers, so a too-large layout is
+  // rejected whatever pointers come with it
+  const size_t need = wha_decode_workspace_size(cache_layout);
+  if (need > kNoAllocScratchBytes)
+    return fail(WHA_ERR_WORKSPACE,
+                "%s: this cache layout needs %zu bytes of split-K scratch, above the %zu bytes of the static "
+                "scratch (use wha_decode_fwd with a workspace)",
+                fn, need, kNoAllocScratchBytes);
+  if (!q || !k_cache || !v_cache || !o)
+    return fail(WHA_ERR_INVALID, "%s: q, k_cache, v_cache and o must be non-NULL", fn);
+  void* ws = nullptr;
+  if ((rc = noalloc_scratch(&ws, fn))) return rc;
+  // every partial the merge kernel reads is written by the split kernel of the
+  // same call, so nothing in the scratch needs clearing first
+  const bool vec = vec_ok(V, {k_cache, v_cache});
+  hipError_t e = wha::launch_decode(q, k_cache, v_cache, o, lse, static_cast<float*>(ws), V, vec, scale,
+                                    static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "wha_decode_fwd_noalloc launch");
   g_err[0] = 0;
   return WHA_OK;
 }
