@@ -272,7 +272,7 @@ def run_attention(args, cfg, pkg, torch):
     }
     del plan
     if not args.kept:
-        kept, kouts, _ = attn_pair(args, cfg, pkg, torch, keep=True, inputs=inputs, settle_s=0.5)
+        kept, kouts, _ = attn_pair(args, cfg, pkg, torch, keep=True, inputs=inputs, settle_s=min(0.5, args.settle))
         res["kept_scores"] = {n: kept[n] for n in ("pair", "ms_per_step", "tokens_per_s", "tflops",
                                                    "pct_fp32_mfma_peak", "kernel_ms", "roofline")}
         res["_outs_kept"] = kouts
@@ -286,7 +286,7 @@ def run_attention(args, cfg, pkg, torch):
                 if keep and pkg.attn_scores_bytes(pkg.layout_bhtd(c["B"], c["H"], c["T"], c["D"])) == 0:
                     sub["kept"] = "same kernels as the recompute pair (this head dim keeps no scores)"
                     continue
-                r, _, p = attn_pair(args, c, pkg, torch, keep=keep, settle_s=0.5)
+                r, _, p = attn_pair(args, c, pkg, torch, keep=keep, settle_s=min(0.5, args.settle))
                 sub["kept" if keep else "recompute"] = {
                     n: r[n] for n in ("ms_per_step", "tokens_per_s", "tflops", "pct_fp32_mfma_peak",
                                       "kernel_ms", "roofline")}
@@ -348,7 +348,7 @@ def run_decode(args, cfg, pkg, torch, sub=False):
     def step():
         pkg.decode_fwd(q, kc, vc, workspace=ws)
 
-    warm_s, warm_n = settle(step, args, torch, 0.5 if sub else None)
+    warm_s, warm_n = settle(step, args, torch, min(0.5, args.settle) if sub else None)
     kern, _ = timed_kernels(step, args.steps, ("decode_split", "decode_merge"), pkg, torch)
     ms = timed_plain(step, args.steps, torch)
     bytes_kv = 2 * B * H * T * D * 4

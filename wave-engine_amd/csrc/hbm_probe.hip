@@ -1,8 +1,9 @@
 // HBM read-stream calibration for the benchmark (not part of the attention
 // ABI): the practical ceiling of a kernel that only reads, against which the
 // decode split kernel (a read-only stream over the K/V cache) is compared.
-// Each thread streams 16-byte loads grid-stride over the buffer and keeps a
-// running sum, written once at the end so the loads cannot be dropped.
+// Each block streams 32 KB chunks (eight 16-byte loads in flight per thread),
+// grid-stride over the buffer, and keeps a running sum, written once per
+// thread at the end so the loads cannot be dropped.
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -13,21 +14,26 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(256) void read_stream_kernel(const f4* __restrict__ x, size_t n4,
                                                           float* __restrict__ out) {
-  const size_t stride = (size_t)gridDim.x * blockDim.x;
-  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  f4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
-  // two loads in flight per iteration
-  for (; i + stride < n4; i += 2 * stride) {
-    const f4 u = x[i];
-    const f4 v = x[i + stride];
-    a += u;
-    b += v;
+  // block-contiguous 32 KB chunks (8 loads of 16 B in flight per thread), grid-stride over chunks
+  constexpr int U = 8;
+  const size_t chunk = (size_t)U * 256;
+  f4 acc[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) acc[u] = f4{0.f, 0.f, 0.f, 0.f};
+  size_t c = (size_t)blockIdx.x * chunk;
+  for (; c + chunk <= n4; c += (size_t)gridDim.x * chunk) {
+    f4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = x[c + threadIdx.x + 256 * u];
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc[u] += v[u];
   }
-  if (i < n4) {
-    const f4 u = x[i];
-    a += u;
-  }
-  out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = (a.x + a.y) + (a.z + a.w) + (b.x + b.y) + (b.z + b.w);
+  // the tail chunk (partial), element by element
+  for (size_t i = c + threadIdx.x; c < n4 && i < n4 && i < c + chunk; i += 256) acc[0] += x[i];
+  f4 t = acc[0];
+#pragma unroll
+  for (int u = 1; u < U; ++u) t += acc[u];
+  out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = (t.x + t.y) + (t.z + t.w);
 }
 
 }  // namespace
