@@ -438,13 +438,27 @@ def run_probs(args, cfg, pkg, torch):
                          "avg_launch_ms": avg[dom]}}
 
 
-def wave_credited_flops(B, H, T, D, C):
+def wave_admitted_pairs(bucket, torch):
+    """(admitted, causal) pair counts of the wave mask over bucket [B,H,T]
+    (int32, device): key k <= q is admitted when its bucket is within one of
+    the query's mod 8, or k = q - 1 (src/common/attn.rs:189-224)."""
+    bk = bucket.long()
+    T = bk.shape[-1]
+    cum = torch.nn.functional.one_hot(bk, 8).cumsum(dim=2)          # keys k <= q per bucket
+    near = sum(cum.gather(3, ((bk + d) % 8).unsqueeze(-1)).squeeze(-1) for d in (-1, 0, 1))
+    prev_far = (((bk[..., :-1] - bk[..., 1:] + 1) & 7) > 2)          # k = q-1 outside the bucket window
+    admitted = int(near.sum().item()) + int(prev_far.sum().item())
+    return admitted, bk.shape[0] * bk.shape[1] * (T * (T + 1) // 2)
+
+
+def wave_credited_flops(B, H, T, D, C, admitted=None):
     """FLOPs of one wave-attention layer step (wave_attention_forward +
-    wave_attention_backward_full).  Core terms count every causal pair (what the
-    kernels execute; the bucket mask admits about 3/8 of them) with the
-    (2 + C)-wide feature dot product, not its 32-wide zero padding."""
+    wave_attention_backward_full).  The core terms are credited for the pairs
+    the bucket mask admits (`admitted`; every causal pair if None) with the
+    (2 + C)-wide feature dot product, not its 32-wide zero padding; the
+    kernels execute every causal pair of a computed tile."""
     E, M, F = H * D, B * T, 2 + C
-    P = B * H * (T * (T + 1) // 2)
+    P = B * H * (T * (T + 1) // 2) if admitted is None else admitted
     proj = 2 * M * E * H * F          # phase + content projections
     vproj = 2 * M * E * D             # per-head value projections
     outp = 2 * M * E * E
@@ -499,7 +513,10 @@ def run_wave(args, cfg, pkg, torch):
         step()
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) / args.steps * 1e3
-    fl = wave_credited_flops(B, H, T, D, C)
+    _, _, cache = pkg.wave_attention_forward(W, x, out=out)
+    admitted, causal = wave_admitted_pairs(cache.bucket, torch)
+    fl = wave_credited_flops(B, H, T, D, C, admitted)
+    fl_exec = wave_credited_flops(B, H, T, D, C)
     dom = max(("wave_fwd", "wave_bwd_dkv", "wave_bwd_dq"), key=lambda n: kern[n]["avg_ms"])
     achieved = fl[dom] / (kern[dom]["avg_ms"] * 1e-3) / 1e12
     return {
@@ -511,11 +528,14 @@ def run_wave(args, cfg, pkg, torch):
         "config": {"workload": cfg["name"], "batch": B, "heads": H, "seq_len": T, "head_dim": D,
                    "content_dim": C, "parallelism": "none (1 GPU)"},
         "tflops": fl["total"] / (ms_per_step * 1e-3) / 1e12,
+        "mask_fraction": admitted / causal,
+        "credit": "core FLOPs over the admitted (bucket-mask) pairs only",
         "kernel_ms_per_step": {n: round(kern[n]["total_ms"], 5) for n in names},
         "ms_per_step_with_events": wall / args.steps * 1e3,
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS,
                      "traffic": load_traffic(dom, cfg), "algorithmic_flops_per_launch": fl[dom],
+                     "executed_pair_flops_per_launch": fl_exec[dom],
                      "avg_launch_ms": kern[dom]["avg_ms"]},
     }
 
