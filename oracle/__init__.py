@@ -297,18 +297,26 @@ def fwd_bhtd(q, k, v, precision: str = "f32", want_lse=False):
     return (o, np.stack(lses)) if want_lse else o
 
 
-def fwd_bwd_bhtd(q, k, v, do, precision: str = "f32"):
+def fwd_bwd_bhtd(q, k, v, do, precision: str = "f32", nthreads: int = 1):
     """Forward then backward (att from the oracle's own forward) over a
-    [B,H,T,D] batch.  Returns O, dQ, dK, dV in [B,H,T,D] and LSE [B,H,T]."""
+    [B,H,T,D] batch, one sequence per task (nthreads > 1: a thread pool; the C
+    calls release the GIL).  Returns O, dQ, dK, dV in [B,H,T,D] and LSE [B,H,T]."""
     B, H, T, D = q.shape
     qs, ks, vs, dos = (bhtd_to_seq(a) for a in (q, k, v, do))
-    O, dQ, dK, dV, L = [], [], [], [], []
-    for b in range(B):
+
+    def one(b):
         o, att, lse = core_fwd(qs[b], ks[b], vs[b], H, precision, want_att=True, want_lse=True)
         dq, dk, dv = attention_backward(dos[b], qs[b], ks[b], vs[b], att, H, precision)
-        O.append(o); dQ.append(dq); dK.append(dk); dV.append(dv); L.append(lse)
-    cv = lambda xs: seq_to_bhtd(np.stack(xs), H)
-    return cv(O), cv(dQ), cv(dK), cv(dV), np.stack(L)
+        return o, dq, dk, dv, lse
+
+    if nthreads > 1:
+        from concurrent.futures import ThreadPoolExecutor
+        with ThreadPoolExecutor(min(nthreads, B)) as ex:
+            res = list(ex.map(one, range(B)))
+    else:
+        res = [one(b) for b in range(B)]
+    cv = lambda i: seq_to_bhtd(np.stack([r[i] for r in res]), H)
+    return cv(0), cv(1), cv(2), cv(3), np.stack([r[4] for r in res])
 
 
 def batch_fwd_bwd_f32_threaded(q_seq, k_seq, v_seq, do_seq, n_head: int, nthreads: int):
@@ -358,6 +366,19 @@ def phase_bucket(phase: float, precision: str = "f32") -> int:
     f = _wave_fn("wao_phase_bucket", precision, ctypes.c_int)
     f.argtypes = [real]
     return int(f(phase))
+
+
+def phases(r, s, precision: str = "f32"):
+    """atan2(s, r) and its bucket for arrays of (r, s), with the reference's
+    f32 (atan2f) or f64 operations (src/common/attn.rs:121-128, :169-174)."""
+    dt = _dt(precision)
+    r, s = _c(np.asarray(r).ravel(), dt), _c(np.asarray(s).ravel(), dt)
+    ph = np.empty_like(r)
+    bk = np.empty(r.shape, dtype=np.int32)
+    f = _wave_fn("wao_phases", precision)
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_long, ctypes.c_void_p, ctypes.c_void_p]
+    f(r.ctypes.data, s.ctypes.data, r.size, ph.ctypes.data, bk.ctypes.data)
+    return ph, bk
 
 
 def wave_fwd(x, w, precision: str = "f32", phase_in=None):

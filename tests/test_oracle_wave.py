@@ -263,3 +263,22 @@ def test_kv_step_equals_the_last_prefill_row(precision):
         np.testing.assert_array_equal(st["phase_new"], full["phase"][:, t])
         phases[:, t] = st["phase_new"]
         values[:, t] = st["v_new"]
+
+
+def test_phases_follow_atan2_and_the_bucket_formula():
+    """oracle.phases: f32 atan2 of (s, r) then phase_to_bucket, element by element
+    equal to the scalar bucket function; f64 phases equal numpy's arctan2
+    (closed forms at the axes and diagonals included)."""
+    r = np.array([1.0, 0.0, -1.0, 0.0, 1.0, -1.0, 0.3, -2.5], np.float32)
+    s = np.array([0.0, 1.0, 0.0, -1.0, 1.0, -1.0, 0.7, 0.1], np.float32)
+    ph, bk = oracle.phases(r, s, "f32")
+    np.testing.assert_allclose(ph[:6], [0.0, np.pi / 2, np.pi, -np.pi / 2, np.pi / 4, -3 * np.pi / 4], rtol=1e-7)
+    assert bk.tolist() == [oracle.phase_bucket(float(p), "f32") for p in ph]
+    assert bk[0] == 0 and bk[4] in (0, 1)           # pi/4 sits on the 0|1 bucket boundary
+    ph64, _ = oracle.phases(r.astype(np.float64), s.astype(np.float64), "f64")
+    np.testing.assert_array_equal(ph64, np.arctan2(s.astype(np.float64), r.astype(np.float64)))
+    rng = np.random.default_rng(0)
+    rr, ss = rng.normal(size=1000).astype(np.float32), rng.normal(size=1000).astype(np.float32)
+    p2, b2 = oracle.phases(rr, ss, "f32")
+    np.testing.assert_allclose(p2, np.arctan2(ss.astype(np.float64), rr.astype(np.float64)), atol=4e-7)
+    assert b2.tolist() == [oracle.phase_bucket(float(p), "f32") for p in p2]

@@ -1,0 +1,33 @@
+"""Host AddressSanitizer + UndefinedBehaviorSanitizer runs (CPU only, no GPU
+needed): the oracle's C restatement through every entry point at ragged
+shapes (tests/cpp/oracle_sanitize.c), and the C ABI's host layer -- argument
+validation, size arithmetic, error strings, the threaded generator, the timing
+bookkeeping -- built with the host code instrumented
+(tests/cpp/abi_sanitize.cpp against wave-engine_amd/_build_san).  A sanitizer
+report or a failed expectation fails the test."""
+import os
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+CPP = ROOT / "tests" / "cpp"
+ENV = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0",
+           UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1")
+
+
+@pytest.fixture(scope="module")
+def built():
+    jobs = os.environ.get("MAX_JOBS", "8")
+    r = subprocess.run(["make", "-s", "-C", str(CPP), f"-j{jobs}", "sanitize"], capture_output=True, text=True,
+                       timeout=1200)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+
+
+@pytest.mark.parametrize("prog", ["oracle_sanitize", "abi_sanitize"])
+def test_sanitized_run_is_clean(built, prog):
+    r = subprocess.run([str(CPP / "_san" / prog)], capture_output=True, text=True, env=ENV, timeout=600)
+    out = r.stdout + r.stderr
+    assert "AddressSanitizer" not in out and "runtime error" not in out, out[-4000:]
+    assert r.returncode == 0 and f"{prog}: OK" in r.stdout, out[-4000:]
