@@ -26,6 +26,14 @@ def pkg():
     return __graft_entry__.load_package()
 
 
+def widen_b(B, H, T, blocks=256):
+    """The smallest batch B' >= B at which a [B',H,T,D] layout leaves the
+    small-problem kernels for the 64-row tile kernels (B'*H*ceil(T/64) >= 256;
+    rows longer than 1024 never take the small path), so that a small test
+    shape can exercise either kernel family."""
+    return max(B, -(-blocks // (H * ((T + 63) // 64))))
+
+
 def errors(got, want):
     """(max_abs, rel_l2) of got vs want, both promoted to float64."""
     g = np.asarray(got, dtype=np.float64)

@@ -62,10 +62,12 @@ int main() {
   expect(wha_attn_fwd(nullptr, cp, cp, p, nullptr, &L, 0.125f, nullptr) == WHA_ERR_INVALID, "fwd NULL");
   expect(wha_attn_bwd(nullptr, cp, cp, cp, cp, cp, p, p, p, nullptr, 0, &L, 0.125f, nullptr) == WHA_ERR_INVALID,
          "bwd NULL");
-  expect(wha_attn_fwd_keep(cp, cp, cp, p, p, nullptr, &L, 0.125f, nullptr) == WHA_ERR_INVALID, "keep NULL scores");
+  // 256 tiles of 64 rows: not a small problem, so the kept pair keeps scores and checks the buffer
+  wha_layout Lk = bhtd(8, 16, 128, 64);
+  expect(wha_attn_fwd_keep(cp, cp, cp, p, p, nullptr, &Lk, 0.125f, nullptr) == WHA_ERR_INVALID, "keep NULL scores");
   float* odd = reinterpret_cast<float*>((uintptr_t(1) << 20) + 4);
-  expect(wha_attn_fwd_keep(cp, cp, cp, p, p, odd, &L, 0.125f, nullptr) == WHA_ERR_INVALID, "keep odd scores");
-  expect(wha_attn_bwd_kept(cp, cp, cp, cp, cp, cp, nullptr, p, p, p, nullptr, 0, &L, 0.125f, nullptr) ==
+  expect(wha_attn_fwd_keep(cp, cp, cp, p, p, odd, &Lk, 0.125f, nullptr) == WHA_ERR_INVALID, "keep odd scores");
+  expect(wha_attn_bwd_kept(cp, cp, cp, cp, cp, cp, nullptr, p, p, p, nullptr, 0, &Lk, 0.125f, nullptr) ==
              WHA_ERR_INVALID,
          "kept NULL scores");
   expect(wha_attn_bwd_from_probs(nullptr, cp, cp, cp, cp, p, p, p, nullptr, 0, &L, 0.125f, nullptr) ==

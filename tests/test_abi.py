@@ -217,15 +217,18 @@ def test_scores_size_and_kept_pair_validation(pkg):
     assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(B, H, T, 64))) == B * H * rows * 64 * 4
     assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_seq(B, T, 12, 768))) == B * H * rows * 64 * 4
     for D in (100, 128, 52, 48):
-        assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(2, 2, 100, D))) > 0
-    for D in (44, 42, 16, 50):
+        assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(8, 16, 100, D))) > 0
+        # small problems (fewer than 256 tiles of 64 rows, T <= 1024) run the split-sweep kernels: nothing kept
         assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(2, 2, 100, D))) == 0
-    odd = pkg.layout_bhtd(2, 2, 100, 64)
+    assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(1, 2, 2048, 64))) > 0
+    for D in (44, 42, 16, 50):
+        assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(8, 16, 100, D))) == 0
+    odd = pkg.layout_bhtd(8, 16, 100, 64)
     odd.stride_t = 66
     assert L.wha_attn_scores_size(ctypes.byref(odd)) == 0
     assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(0, 1, 1, 64))) == 0
 
-    lay = pkg.layout_bhtd(1, 1, 64, 64)
+    lay = pkg.layout_bhtd(8, 16, 128, 64)   # 256 tiles of 64 rows: not a small problem, scores are kept
     p = ctypes.c_void_p(0x100000)
     rc = L.wha_attn_fwd_keep(p, p, p, p, p, None, ctypes.byref(lay), 0.125, None)
     assert rc == WHA_ERR_INVALID and b"scores" in L.wha_last_error()

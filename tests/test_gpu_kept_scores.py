@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import assert_parity, errors
+from conftest import assert_parity, errors, widen_b
 
 pytestmark = pytest.mark.gpu
 
@@ -40,12 +40,19 @@ SHAPES = [(1, 1, 1, 64), (1, 2, 17, 64), (2, 2, 100, 64), (3, 1, 48, 64), (2, 3,
 
 @pytest.mark.parametrize("B,H,T,D", SHAPES)
 def test_kept_pair_small_shapes(pkg, torch_dev, B, H, T, D):
+    """Ragged shapes with the batch widened past the small-problem threshold
+    (small problems keep no scores); the oracle on the first and last sequence."""
     torch, dev = torch_dev
+    B = widen_b(B, H, T)
     print(f"case kept B={B} H={H} T={T} D={D}", flush=True)
     q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=2000 + T + D)
     got, kept = run_pair(pkg, torch, dev, q, k, v, do, keep=True)
     covered = pkg.attn_scores_bytes(pkg.layout_bhtd(B, H, T, D)) > 0
     assert kept == covered
+    assert covered == (D % 4 == 0 and 48 <= D <= 128)
+    sel = sorted({0, B - 1})
+    q, k, v, do = (a[sel] for a in (q, k, v, do))
+    got = [a[sel] for a in got]
     r32 = oracle.fwd_bwd_bhtd(q, k, v, do, "f32")
     r64 = oracle.fwd_bwd_bhtd(q, k, v, do, "f64")
     for i, n in enumerate(("O", "dQ", "dK", "dV")):
@@ -54,7 +61,9 @@ def test_kept_pair_small_shapes(pkg, torch_dev, B, H, T, D):
         print(f"  {n}: vs f32 max_abs={ma:.2e} rel_l2={rl:.2e} | vs f64 {errors(g, r64[i])[1]:.2e}", flush=True)
     assert np.abs(got[1] - r64[4]).max() < 2e-5
     # the recompute pair on the same inputs: same softmax, scores rounded in another order
-    ref, _ = run_pair(pkg, torch, dev, q, k, v, do, keep=False)
+    qw, kw, vw, dow = pkg.synth_inputs(B, H, T, D, seed=2000 + T + D)
+    ref, _ = run_pair(pkg, torch, dev, qw, kw, vw, dow, keep=False)
+    ref = [a[sel] for a in ref]
     if D != 48:  # the same forward kernel (head dim 48 keeps on the 64-wide one, else the exact 48-wide)
         assert np.array_equal(got[0], ref[0]) and np.array_equal(got[1], ref[1])
     for a, b in zip(got, ref):
@@ -121,7 +130,8 @@ def test_kept_pair_fused_qkv_layout_is_bit_identical(pkg, torch_dev):
     and dq, dk, dv written into one [B][T][3E] gradient buffer gives the same bits
     as on contiguous [B,H,T,D] tensors."""
     torch, dev = torch_dev
-    for (B, H, T, D) in ((2, 12, 300, 64), (1, 4, 130, 48), (1, 2, 200, 128)):
+    for (B, H, T, D) in ((widen_b(2, 12, 300), 12, 300, 64), (widen_b(1, 4, 130), 4, 130, 48),
+                         (widen_b(1, 2, 200), 2, 200, 128)):
         print(f"case kept fused-qkv B={B} H={H} T={T} D={D}", flush=True)
         E = H * D
         q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=6)

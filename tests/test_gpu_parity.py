@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import assert_parity, errors
+from conftest import assert_parity, errors, widen_b
 
 pytestmark = pytest.mark.gpu
 
@@ -48,17 +48,27 @@ def report(tag, got, ref32, ref64=None):
         print(msg, flush=True)
 
 
+# as given these are small problems (the split-sweep kernels); widened (wide=True) they run the
+# 64-row tile kernels, one tile per block; the last one has enough heads for paired tiles at ragged T
 SMALL = [(1, 1, 1, 64), (1, 2, 17, 64), (2, 3, 63, 48), (1, 2, 65, 42), (2, 2, 100, 64),
          (1, 1, 257, 128), (2, 2, 130, 32), (1, 1, 64, 16), (1, 4, 200, 8), (1, 2, 129, 100),
-         (3, 1, 48, 64), (2, 2, 97, 56), (1, 3, 40, 52)]
+         (3, 1, 48, 64), (2, 2, 97, 56), (1, 3, 40, 52), (8, 12, 900, 64)]
 
 
+@pytest.mark.parametrize("wide", [False, True])
 @pytest.mark.parametrize("B,H,T,D", SMALL)
-def test_fused_small_shapes(pkg, torch_dev, B, H, T, D):
+def test_fused_small_shapes(pkg, torch_dev, B, H, T, D, wide):
+    """Each shape as given (the small-problem kernels) and with the batch widened
+    past the small-problem threshold (the 64-row tile kernels), the oracle run
+    on the first and last sequence of the widened batch."""
     torch, dev = torch_dev
+    if wide:
+        B = widen_b(B, H, T)
     print(f"case fused B={B} H={H} T={T} D={D}", flush=True)
     q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=1000 + T + D)
     o, lse, dq, dk, dv = gpu_fwd_bwd(pkg, torch, dev, q, k, v, do)
+    sel = sorted({0, B - 1})
+    q, k, v, do, o, lse, dq, dk, dv = (a[sel] for a in (q, k, v, do, o, lse, dq, dk, dv))
     r32 = oracle.fwd_bwd_bhtd(q, k, v, do, "f32")
     r64 = oracle.fwd_bwd_bhtd(q, k, v, do, "f64")
     report(f"B{B}H{H}T{T}D{D}", (o, dq, dk, dv), r32, r64)
@@ -129,7 +139,9 @@ def test_reference_layout_is_bit_identical(pkg, torch_dev):
     """The reference's per-sequence [T][H*D] layout (batched [B][T][E]) is read in
     place through strides and gives the same bits as [B,H,T,D]."""
     torch, dev = torch_dev
-    for (B, H, T, D) in ((2, 12, 300, 64), (2, 4, 256, 42)):
+    # small problems and (widened batches) the 64-row tile kernels
+    for (B, H, T, D) in ((2, 12, 300, 64), (2, 4, 256, 42), (widen_b(2, 12, 300), 12, 300, 64),
+                         (widen_b(2, 4, 256), 4, 256, 42)):
         q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=5)
         base = gpu_fwd_bwd(pkg, torch, dev, q, k, v, do)
         seq = [torch.from_numpy(oracle.bhtd_to_seq(a)).to(dev) for a in (q, k, v, do)]
@@ -142,19 +154,21 @@ def test_reference_layout_is_bit_identical(pkg, torch_dev):
             np.testing.assert_array_equal(a, b_)
 
 
-def test_deterministic(pkg, torch_dev):
+@pytest.mark.parametrize("wide", [False, True])
+def test_deterministic(pkg, torch_dev, wide):
     torch, dev = torch_dev
-    q, k, v, do = pkg.synth_inputs(2, 4, 333, 64, seed=3)
+    q, k, v, do = pkg.synth_inputs(widen_b(2, 4, 333) if wide else 2, 4, 333, 64, seed=3)
     a = gpu_fwd_bwd(pkg, torch, dev, q, k, v, do)
     b = gpu_fwd_bwd(pkg, torch, dev, q, k, v, do)
     for x, y in zip(a, b):
         np.testing.assert_array_equal(x, y)
 
 
-def test_causality(pkg, torch_dev):
+@pytest.mark.parametrize("wide", [False, True])
+def test_causality(pkg, torch_dev, wide):
     """Changing K and V at position j leaves O, LSE and dQ of rows < j unchanged."""
     torch, dev = torch_dev
-    B, H, T, D = 1, 2, 200, 64
+    B, H, T, D = (widen_b(1, 2, 200) if wide else 1), 2, 200, 64
     q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=8)
     a = gpu_fwd_bwd(pkg, torch, dev, q, k, v, do)
     j = 150
@@ -280,8 +294,10 @@ def test_workspace_explicit_and_too_small(pkg, torch_dev):
 
 
 def test_kernel_timing_hooks(pkg, torch_dev):
+    """Per-kernel event timing on the 64-row tile kernels (a layout above the
+    small-problem threshold, which runs no separate statistics pass)."""
     torch, dev = torch_dev
-    q, k, v, do = pkg.synth_inputs(1, 2, 128, 64, seed=4)
+    q, k, v, do = pkg.synth_inputs(widen_b(1, 2, 128), 2, 128, 64, seed=4)
     tq, tk, tv, tdo = to_dev(torch, dev, q, k, v, do)
     pkg.timing_reset()
     pkg.timing_enable(True)

@@ -546,8 +546,8 @@ template <int DP, bool DS_OUT, bool PADQ, bool SAVED, bool PROBS = false>
 __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ stats, float* __restrict__ dK,
-    float* __restrict__ dV, float* __restrict__ DS, const float* __restrict__ SC, View L, float scale,
-    float scale_log2) {
+    float* __restrict__ dV, float* __restrict__ DS, const float* __restrict__ SC, View L, int unpaired,
+    float scale, float scale_log2) {
   constexpr int DG = DP / 4, NDT = DP / 16;
   constexpr int QPR = DP / 4;            // quads per row
   constexpr int BSUB = 32;               // queries per sub-tile
@@ -615,7 +615,8 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
 
   // key tiles pair and n_kt-1-pair: every block does n_kt+1 tiles of work.
   // One key tile: 64 keys, wave w owns keys 64kt + 16w .. +15.
-  const int n_pass = (n_kt - 1 - pair != pair) ? 2 : 1;
+  // paired: key tiles p and n_kt-1-p; unpaired: one tile per block, the longest first
+  const int n_pass = (!unpaired && n_kt - 1 - pair != pair) ? 2 : 1;
   // sub-tiles this block sweeps, and how many it has left
   const int work = (n_st - 2 * pair) + (n_pass == 2 ? n_st - 2 * (n_kt - 1 - pair) : 0);
   int left = work;
@@ -738,14 +739,14 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
     };
 
     // one sub-tile: wait for its loads, start the next one's, then consume it
-    auto step = [&](int st, const float* Qs, const float* Os, const float* Sts, float* Qn, float* On,
+    auto step = [&](int st, int nx, const float* Qs, const float* Os, const float* Sts, float* Qn, float* On,
                     float* Sn, const float (&sc)[8], float (&sc_next)[8]) {
       wait_vmem();
-      __syncthreads();  // sub-tile st is in LDS; every wave is done with sub-tile st-1
+      __syncthreads();  // sub-tile st is in LDS; every wave is done with the previous one
       prio_by_remaining(left--, work);
-      if (st + 1 < n_st) {
-        fetch(st + 1, Qn, On, Sn);
-        if constexpr (SAVED) load_sc(st + 1, sc_next);
+      if (nx >= 0) {  // the next sub-tile of the sweep
+        fetch(nx, Qn, On, Sn);
+        if constexpr (SAVED) load_sc(nx, sc_next);
       }
       const int qb = st * BSUB;
       if (qb + BSUB - 1 < k0w) return;  // every row precedes every key of the wave
@@ -755,14 +756,21 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
         compute(std::true_type{}, qb, Qs, Os, Sts, sc);
     };
 
+    // Sweep order: the first pass (the longer key tile) runs from the last
+    // sub-tile back to its diagonal, the second from its diagonal forward.  The
+    // blocks of one head then read at most two distinct Q/dO sub-tiles at any
+    // time (every block in its first pass the same one, every block in its
+    // second pass the same other one), which stay in their XCD's L2.
     const int st0 = 2 * kt;
-    float scA[8], scB[8];  // SAVED: scores of the even / odd sub-tiles
+    const int nsub = n_st - st0;
+    auto st_at = [&](int j) { return pass == 0 ? n_st - 1 - j : st0 + j; };
+    float scA[8], scB[8];  // SAVED: scores of the even / odd steps
     __syncthreads();  // the previous key tile's last sub-tile has been read by every wave
-    fetch(st0, Qs0, Os0, St0);
-    if constexpr (SAVED) load_sc(st0, scA);
-    for (int st = st0; st < n_st; st += 2) {
-      step(st, Qs0, Os0, St0, Qs1, Os1, St1, scA, scB);
-      if (st + 1 < n_st) step(st + 1, Qs1, Os1, St1, Qs0, Os0, St0, scB, scA);
+    fetch(st_at(0), Qs0, Os0, St0);
+    if constexpr (SAVED) load_sc(st_at(0), scA);
+    for (int j = 0; j < nsub; j += 2) {
+      step(st_at(j), j + 1 < nsub ? st_at(j + 1) : -1, Qs0, Os0, St0, Qs1, Os1, St1, scA, scB);
+      if (j + 1 < nsub) step(st_at(j + 1), j + 2 < nsub ? st_at(j + 2) : -1, Qs1, Os1, St1, Qs0, Os0, St0, scB, scA);
     }
     store_row_frag_split<DP>(dK + base, krow, L.T, L.D, L.st, g, dkacc, scale);
     store_row_frag_split<DP>(dV + base, krow, L.T, L.D, L.st, g, dvacc, 1.f);
@@ -787,7 +795,8 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
 template <int DP, bool PADQ>
 __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __restrict__ K,
                                                               const float* __restrict__ DS,
-                                                              float* __restrict__ dQ, View L, float scale) {
+                                                              float* __restrict__ dQ, View L, int unpaired,
+                                                              float scale) {
   constexpr int NDT = DP / 16, BN = 64;
   constexpr int QPR = DP / 4;            // quads per row
   constexpr int TILE = BN * DP;
@@ -843,7 +852,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __res
   };
 
   const float* dsh = DS + (int64_t)bh * ds_rows(L.T) * 64;
-  const int n_pass = (n_qt - 1 - pair != pair) ? 2 : 1;
+  // paired: query tiles n_qt-1-p and p; unpaired: one tile per block, the longest first
+  const int n_pass = (!unpaired && n_qt - 1 - pair != pair) ? 2 : 1;
   const int work = (n_qt - pair) + (n_pass == 2 ? pair + 1 : 0);  // key tiles this block sweeps
   int left = work;
   for (int pass = 0; pass < n_pass; ++pass) {
@@ -864,13 +874,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __res
     // roles, so no register copies)
     float4 dA[4], dB[4];
 
-    auto step = [&](int kt, const float* Ks, float* Kn, const float4* dcur, float4* dnext) {
+    auto step = [&](int kt, int nx, const float* Ks, float* Kn, const float4* dcur, float4* dnext) {
       wait_vmem();
-      __syncthreads();  // K tile kt is in LDS; every wave is done with tile kt-1
+      __syncthreads();  // K tile kt is in LDS; every wave is done with the previous one
       prio_by_remaining(left--, work);
-      if (kt + 1 < n_kt) {
-        fetch(kt + 1, Kn);
-        load_ds(kt + 1, dnext);
+      if (nx >= 0) {  // the next tile of the sweep
+        fetch(nx, Kn);
+        load_ds(nx, dnext);
       }
       if (kt < qt) {
 #pragma unroll
@@ -903,12 +913,16 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __res
       }
     };
 
+    // Sweep order as in the forward: the first pass from key tile 0 forward,
+    // the second from its diagonal back, so the blocks of one head read at most
+    // two distinct K tiles at any time.
+    auto kt_at = [&](int j) { return pass == 0 ? j : n_kt - 1 - j; };
     __syncthreads();  // the previous pass's last tile has been read by every wave
-    fetch(0, Ks0);
-    load_ds(0, dA);
-    for (int kt = 0; kt < n_kt; kt += 2) {
-      step(kt, Ks0, Ks1, dA, dB);
-      if (kt + 1 < n_kt) step(kt + 1, Ks1, Ks0, dB, dA);
+    fetch(kt_at(0), Ks0);
+    load_ds(kt_at(0), dA);
+    for (int j = 0; j < n_kt; j += 2) {
+      step(kt_at(j), j + 1 < n_kt ? kt_at(j + 1) : -1, Ks0, Ks1, dA, dB);
+      if (j + 1 < n_kt) step(kt_at(j + 1), j + 2 < n_kt ? kt_at(j + 2) : -1, Ks1, Ks0, dB, dA);
     }
     store_row_frag_split<DP>(dQ + base, qrow, L.T, L.D, L.st, g, acc, scale);
   }
@@ -1015,8 +1029,8 @@ hipError_t bwd_dma_t(const float* q, const float* k, const float* v, const float
                      const float* lse, float* dq, float* dk, float* dv, float* stats, float* ds, const View& L,
                      float scale, hipStream_t stream, const float* sc) {
   const float sl2 = (float)((double)scale * 1.4426950408889634);
-  const int n_t64 = (L.T + 63) / 64;
-  const dim3 grid((unsigned)((n_t64 + 1) / 2 * L.B * L.H));
+  const int unp = dma_unpaired(L);
+  const dim3 grid((unsigned)(dma_tiles(L, unp) * L.B * L.H));
   hipError_t e;
   {
     TimingScope ts("attn_bwd_delta", stream);
@@ -1030,15 +1044,16 @@ hipError_t bwd_dma_t(const float* q, const float* k, const float* v, const float
     TimingScope ts("attn_bwd_dkv", stream);
     if (sc != nullptr)
       hipLaunchKernelGGL((attn_bwd_dkv_dma_kernel<DP, true, PADQ, true>), grid, dim3(256), 0, stream, q, k, v, d_o,
-                         (const float*)stats, dk, dv, ds, sc, L, scale, sl2);
+                         (const float*)stats, dk, dv, ds, sc, L, unp, scale, sl2);
     else
       hipLaunchKernelGGL((attn_bwd_dkv_dma_kernel<DP, true, PADQ, false>), grid, dim3(256), 0, stream, q, k, v,
-                         d_o, (const float*)stats, dk, dv, ds, sc, L, scale, sl2);
+                         d_o, (const float*)stats, dk, dv, ds, sc, L, unp, scale, sl2);
     e = hipGetLastError();
   }
   if (e != hipSuccess) return e;
   TimingScope ts("attn_bwd_dq", stream);
-  hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<DP, PADQ>), grid, dim3(256), 0, stream, k, (const float*)ds, dq, L, scale);
+  hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<DP, PADQ>), grid, dim3(256), 0, stream, k, (const float*)ds, dq, L, unp,
+                     scale);
   return hipGetLastError();
 }
 
@@ -1165,6 +1180,8 @@ hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const
                            float* delta, float* ds, const View& L, bool vec, float scale,
                            hipStream_t stream, const float* sc) {
   if (sc != nullptr && (ds == nullptr || !WHA_DKV_DMA || !scores_kept(L, vec))) return hipErrorInvalidValue;
+  if (sc == nullptr && ds != nullptr && small_problem(L))
+    return launch_attn_bwd_small(q, k, v, o, d_o, lse, dq, dk, dv, ds, L, scale, stream);
   if (WHA_DKV_DMA && ds != nullptr && vec && (sc != nullptr ? kept_head_dim(L.D) : dma_head_dim(L.D))) {
     if (L.D == 64) return bwd_dma_t<64, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
     if (L.D < 64) return bwd_dma_t<64, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
@@ -1192,24 +1209,24 @@ template <int DP, bool PADQ, bool AV>
 hipError_t bwd_probs_dma_t(const float* d_o, const float* q, const float* k, const float* v, const float* att,
                            float* dq, float* dk, float* dv, float* delta, float* stats, float* ds, const View& L,
                            float scale, hipStream_t stream) {
-  const int n_t64 = (L.T + 63) / 64;
   hipError_t e;
   {
     TimingScope ts("attn_bwd_probs_delta", stream);
     e = launch_probs_delta_dma(d_o, v, att, stats, L, AV, stream);
   }
   if (e != hipSuccess) return e;
-  const dim3 grid((unsigned)((n_t64 + 1) / 2 * L.B * L.H));
+  const int unp = dma_unpaired(L);
+  const dim3 grid((unsigned)(dma_tiles(L, unp) * L.B * L.H));
   {
     TimingScope ts("attn_bwd_probs_dkv", stream);
     hipLaunchKernelGGL((attn_bwd_dkv_dma_kernel<DP, true, PADQ, true, true>), grid, dim3(256), 0, stream, q, k, v,
-                       d_o, (const float*)stats, dk, dv, ds, att, L, scale, 0.f);
+                       d_o, (const float*)stats, dk, dv, ds, att, L, unp, scale, 0.f);
     e = hipGetLastError();
   }
   if (e != hipSuccess) return e;
   TimingScope ts("attn_bwd_probs_dq", stream);
   hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<DP, PADQ>), grid, dim3(256), 0, stream, k, (const float*)ds, dq, L,
-                     scale);
+                     unp, scale);
   return hipGetLastError();
 }
 }  // namespace

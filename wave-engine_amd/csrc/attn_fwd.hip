@@ -205,7 +205,7 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
                                                                      float* __restrict__ O,
                                                                      float* __restrict__ LSE,
                                                                      float* __restrict__ SC, View L,
-                                                                     float scale_log2,
+                                                                     int unpaired, float scale_log2,
                                                                      const float* __restrict__ ATT = nullptr) {
   constexpr int DG = DP / 4, NDT = DP / 16;
   constexpr int QPR = DP / 4;            // quads per row
@@ -266,7 +266,9 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
     }
   };
 
-  const int n_pass = (n_qt - 1 - pair != pair) ? 2 : 1;
+  // paired: query tiles n_qt-1-p and p (equal work per block); unpaired: one
+  // tile per block, the longest first (grids too small to fill every slot)
+  const int n_pass = (!unpaired && n_qt - 1 - pair != pair) ? 2 : 1;
   // sub-tiles this block sweeps, and how many it has left
   auto subs_of = [&](int qt) { return (min(L.T, (qt + 1) * 64) + BSUB - 1) / BSUB; };
   const int work = subs_of(n_qt - 1 - pair) + (n_pass == 2 ? subs_of(pair) : 0);
@@ -405,14 +407,14 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
     };
 
     // one sub-tile: wait for its loads, start the next one's, then consume it
-    auto step = [&](int st, const float* Ks, const float* Vs, float* Kn, float* Vn, const floatx4 (&at)[NKT],
-                    floatx4 (&at_next)[NKT]) {
+    auto step = [&](int st, int nx, const float* Ks, const float* Vs, float* Kn, float* Vn,
+                    const floatx4 (&at)[NKT], floatx4 (&at_next)[NKT]) {
       wait_vmem();
-      __syncthreads();  // sub-tile st is in LDS; every wave is done with sub-tile st-1
+      __syncthreads();  // sub-tile st is in LDS; every wave is done with the previous one
       prio_by_remaining(left--, work);
-      if (st + 1 < n_sub) {
-        fetch(st + 1, Kn, Vn);
-        if constexpr (DELTA) load_att(st + 1, at_next);
+      if (nx >= 0) {  // the next sub-tile of the sweep
+        fetch(nx, Kn, Vn);
+        if constexpr (DELTA) load_att(nx, at_next);
       }
       const int k0 = st * BSUB;
       if (k0 > q0 + 15) return;  // every key follows every query of the wave
@@ -422,12 +424,19 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
         compute(std::true_type{}, k0, Ks, Vs, at);
     };
 
+    // Sweep order: the first pass (the longer query tile) runs from key 0
+    // forward, the second from its diagonal back to key 0, so the blocks of one
+    // head read at most two distinct K/V sub-tiles at any time (every block in
+    // its first pass the same one, every block in its second pass the same
+    // other one).  The first sub-tile a wave computes always holds a key at or
+    // before every query of the wave, so its running max starts finite.
+    auto st_at = [&](int j) { return pass == 0 ? j : n_sub - 1 - j; };
     __syncthreads();  // the previous pass's last sub-tile has been read by every wave
-    fetch(0, Ks0, Vs0);
-    if constexpr (DELTA) load_att(0, atA);
-    for (int st = 0; st < n_sub; st += 2) {
-      step(st, Ks0, Vs0, Ks1, Vs1, atA, atB);
-      if (st + 1 < n_sub) step(st + 1, Ks1, Vs1, Ks0, Vs0, atB, atA);
+    fetch(st_at(0), Ks0, Vs0);
+    if constexpr (DELTA) load_att(st_at(0), atA);
+    for (int j = 0; j < n_sub; j += 2) {
+      step(st_at(j), j + 1 < n_sub ? st_at(j + 1) : -1, Ks0, Vs0, Ks1, Vs1, atA, atB);
+      if (j + 1 < n_sub) step(st_at(j + 1), j + 2 < n_sub ? st_at(j + 2) : -1, Ks1, Vs1, Ks0, Vs0, atB, atA);
     }
 
     if constexpr (DELTA) {
@@ -465,27 +474,27 @@ namespace {
 template <int DP, bool PADQ>
 void fwd_dma_t(const float* q, const float* k, const float* v, float* o, float* lse, float* sc, const View& L,
                float scale_log2, hipStream_t stream) {
-  const int n_qt = (L.T + 63) / 64;
-  const dim3 grid((unsigned)((n_qt + 1) / 2 * L.B * L.H));
+  const int unp = dma_unpaired(L);
+  const dim3 grid((unsigned)(dma_tiles(L, unp) * L.B * L.H));
   if (sc != nullptr)
-    hipLaunchKernelGGL((attn_fwd_dma_kernel<DP, PADQ, true>), grid, dim3(256), 0, stream, q, k, v, o, lse, sc, L,
+    hipLaunchKernelGGL((attn_fwd_dma_kernel<DP, PADQ, true>), grid, dim3(256), 0, stream, q, k, v, o, lse, sc, L, unp,
                        scale_log2);
   else
     hipLaunchKernelGGL((attn_fwd_dma_kernel<DP, PADQ, false>), grid, dim3(256), 0, stream, q, k, v, o, lse, sc, L,
-                       scale_log2);
+                       unp, scale_log2);
 }
 }  // namespace
 
-bool scores_kept(const View& L, bool vec) { return WHA_FWD_DMA && vec && kept_head_dim(L.D); }
+bool scores_kept(const View& L, bool vec) { return WHA_FWD_DMA && vec && kept_head_dim(L.D) && !small_problem(L); }
 
 namespace {
 template <int DP, bool PADQ, bool AV>
 void probs_delta_t(const float* d_o, const float* v, const float* att, float* stats, const View& L,
                    hipStream_t stream) {
-  const int n_qt = (L.T + 63) / 64;
-  const dim3 grid((unsigned)((n_qt + 1) / 2 * L.B * L.H));
+  const int unp = dma_unpaired(L);
+  const dim3 grid((unsigned)(dma_tiles(L, unp) * L.B * L.H));
   hipLaunchKernelGGL((attn_fwd_dma_kernel<DP, PADQ, false, true, AV>), grid, dim3(256), 0, stream, d_o, v, v,
-                     (float*)nullptr, stats, (float*)nullptr, L, 1.f, att);
+                     (float*)nullptr, stats, (float*)nullptr, L, unp, 1.f, att);
 }
 }  // namespace
 
@@ -510,6 +519,7 @@ hipError_t launch_probs_delta_dma(const float* d_o, const float* v, const float*
 hipError_t launch_attn_fwd(const float* q, const float* k, const float* v, float* o, float* lse,
                            const View& L, bool vec, float scale, hipStream_t stream, float* scores) {
   if (scores != nullptr && !scores_kept(L, vec)) return hipErrorInvalidValue;
+  if (scores == nullptr && small_problem(L)) return launch_attn_fwd_small(q, k, v, o, lse, L, scale, stream);
   if (WHA_FWD_DMA && vec && (scores != nullptr ? kept_head_dim(L.D) : dma_head_dim(L.D))) {
     const float scale_log2 = (float)((double)scale * 1.4426950408889634);
     TimingScope ts("attn_fwd", stream);

@@ -1,0 +1,517 @@
+// Causal attention forward and backward for small problems (gfx950, fp32 MFMA).
+//
+// Same results as attn_fwd.hip / attn_bwd.hip (the core of attention_cpu,
+// reference src/common/compute.rs:377-409, and attention_backward_single,
+// src/cpu/backward.rs:313-363), for problems with few (b,h) heads and short
+// rows: there the 64-row tile kernels launch fewer blocks than the chip has
+// CUs (the 168-dim config: 16 heads x 4 tiles = 64 blocks for 256 CUs) and
+// every block walks its causal sweep serially, so the step is latency-bound.
+//
+// Here a block covers 16 rows of one (b,h) with kSW waves (8; 4 at head dim
+// 128), and the causal sweep of those rows is split over the waves: wave w
+// takes the 16-row chunks w, w+kSW, ... of the other operand and keeps its own
+// partial state; the partials merge through LDS in a fixed order
+// (deterministic).  Grid = B*H*ceil(T/16) blocks per kernel, three kernels per
+// step instead of four:
+//   attn_fwd_small_kernel      O and LSE (online softmax per wave, LSE merge)
+//   attn_bwd_dkv_small_kernel  dK, dV and dS; Delta = dO.O of each query chunk
+//                              is formed in place (no statistics pass)
+//   attn_bwd_dq_small_kernel   dQ = scale * dS K from the dS workspace
+// Each wave stages its chunk's operands in its own LDS region: a 16-row chunk
+// is read from global memory row by row (consecutive lanes on consecutive
+// head-dim entries, so every load instruction touches one or two rows), and
+// the next chunk's loads are in flight while the current chunk is consumed.
+// From LDS each lane takes the two MFMA layouts the contractions need:
+//   row fragment     lane (lq, g) holds row lq, d = g*DG .. g*DG+DG-1
+//                    (A/B operands of contractions over the head dimension)
+//   column fragment  lane (lq, g) holds rows 4g+i (i < 4), d = NDT*lq+dt
+//                    (A operand of contractions over rows; the accumulators
+//                    then hold d = NDT*(4g+i)+dt, the layout store_row_frag writes)
+// Head dims pad to DP = 48, 64 or 128 with zeros (32-bit loads: any stride).
+#include <type_traits>
+
+#include "wha_launch.hpp"
+
+namespace wha {
+
+namespace {
+
+// Waves per block: 8, or 4 at head dim 128 (the VGPR budget of its fragments).
+template <int DP>
+constexpr int kSWof = DP == 128 ? 4 : 8;
+
+// A 16-row chunk of one tensor in a wave's registers: element lane + 64p of the
+// chunk is row (lane + 64p) / DP, head-dim entry (lane + 64p) % DP; zero past
+// T and D.
+template <int DP>
+struct ChunkRaw {
+  static constexpr int PER = 16 * DP / 64;
+  float r[PER];
+  __device__ __forceinline__ void load(const float* __restrict__ base, int row0, int T, int D, int64_t st,
+                                       int lane) {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int idx = lane + 64 * p;
+      const int row = row0 + idx / DP, d = idx % DP;
+      r[p] = (row < T && d < D) ? base[(int64_t)row * st + d] : 0.f;
+    }
+  }
+  // into a [16][DP + 4] LDS tile
+  __device__ __forceinline__ void store(float* tile, int lane) const {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      const int idx = lane + 64 * p;
+      tile[(idx / DP) * (DP + 4) + idx % DP] = r[p];
+    }
+  }
+};
+
+// Orders a wave's LDS writes before its following LDS reads (and reads before
+// later writes): the wave's lanes run in lockstep, so a wavefront-scope fence
+// and a scheduling barrier suffice.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Row fragment of a [16][DP + 4] LDS tile: row lq, entries g*DG .. +DG-1, times mul.
+template <int DP>
+__device__ __forceinline__ void row_frag(const float* tile, int lq, int g, float mul, float* out) {
+  constexpr int DG = DP / 4;
+  const float* p = tile + lq * (DP + 4) + g * DG;
+#pragma unroll
+  for (int c = 0; c < DG / 4; ++c) {
+    const float4 v = *reinterpret_cast<const float4*>(p + 4 * c);
+    out[4 * c + 0] = v.x * mul;
+    out[4 * c + 1] = v.y * mul;
+    out[4 * c + 2] = v.z * mul;
+    out[4 * c + 3] = v.w * mul;
+  }
+}
+
+// Column fragment of a [16][DP + 4] LDS tile: rows 4g+i, entries NDT*lq + dt.
+template <int DP>
+__device__ __forceinline__ void col_frag(const float* tile, int lq, int g, float (&out)[4][DP / 16]) {
+  constexpr int NDT = DP / 16;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) out[i][dt] = tile[(4 * g + i) * (DP + 4) + NDT * lq + dt];
+  }
+}
+
+// Adds the waves' partial accumulators (acc[dt][i] = X[row lq][NDT*(4g+i)+dt])
+// through LDS in wave order; wave 0 gets the sum in acc.  sm: kSW tiles of
+// [16][DP + 4] floats.
+template <int DP>
+__device__ __forceinline__ void sum_over_waves(float* sm, floatx4 (&acc)[DP / 16], int wave, int lq, int g) {
+  constexpr int NDT = DP / 16, kSW = kSWof<DP>, TILE = 16 * (DP + 4);
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sm[wave * TILE + lq * (DP + 4) + NDT * (4 * g + i) + dt] = acc[dt][i];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int off = lq * (DP + 4) + NDT * (4 * g + i) + dt;
+        float x = sm[off];
+#pragma unroll
+        for (int w = 1; w < kSW; ++w) x += sm[w * TILE + off];
+        acc[dt][i] = x;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+template <int DP>
+__global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const float* __restrict__ Q,
+                                                                       const float* __restrict__ K,
+                                                                       const float* __restrict__ V,
+                                                                       float* __restrict__ O,
+                                                                       float* __restrict__ LSE, View L,
+                                                                       float scale_log2) {
+  constexpr int DG = DP / 4, NDT = DP / 16, kSW = kSWof<DP>, TILE = 16 * (DP + 4);
+  // per wave: its K and V chunk tiles; after the sweep the first of them holds
+  // the wave's partial output for the merge
+  __shared__ __align__(16) float stage[kSW][2][TILE];
+  __shared__ __align__(16) float qs[TILE];
+  __shared__ float sm_m[kSW][16], sm_l[kSW][16];
+
+  const int BH = L.B * L.H;
+  const int n_g = (L.T + 15) / 16;
+  const int bh = blockIdx.x % BH;
+  const int qg = n_g - 1 - (int)(blockIdx.x / BH);  // the longest rows first
+  const int b = bh / L.H, h = bh % L.H;
+  const int64_t base = (int64_t)b * L.sb + (int64_t)h * L.sh;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 15, g = lane >> 4;
+  const int qrow = 16 * qg + lq;            // this lane's query (MFMA column)
+  const int key_last = min(qrow, L.T - 1);  // keys after it are masked
+  float* ks = stage[wave][0];
+  float* vs = stage[wave][1];
+
+  // the block's 16 queries, staged once by wave 0
+  if (wave == 0) {
+    ChunkRaw<DP> qr;
+    qr.load(Q + base, 16 * qg, L.T, L.D, L.st, lane);
+    qr.store(qs, lane);
+  }
+  ChunkRaw<DP> kr, vr;
+  if (wave <= qg) {
+    kr.load(K + base, 16 * wave, L.T, L.D, L.st, lane);
+    vr.load(V + base, 16 * wave, L.T, L.D, L.st, lane);
+  }
+  __syncthreads();
+  float qf[DG];
+  row_frag<DP>(qs, lq, g, scale_log2, qf);
+
+  float m = -INFINITY, l = 0.f;
+  floatx4 oacc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) oacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  for (int c = wave; c <= qg; c += kSW) {
+    kr.store(ks, lane);
+    vr.store(vs, lane);
+    wave_lds_sync();
+    if (c + kSW <= qg) {  // the next chunk's loads in flight during this one
+      kr.load(K + base, 16 * (c + kSW), L.T, L.D, L.st, lane);
+      vr.load(V + base, 16 * (c + kSW), L.T, L.D, L.st, lane);
+    }
+    const int key0 = 16 * c;  // <= 16*qg <= T-1: the chunk's first key is valid for every query here
+    float kf[DG], vv[4][NDT];
+    row_frag<DP>(ks, lq, g, 1.f, kf);
+    col_frag<DP>(vs, lq, g, vv);
+    // S^T[key][query] (log2 units): lane element i = key key0+4g+i, query qrow
+    floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < DG; ++j) s = mfma4(kf[j], qf[j], s);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = (key0 + 4 * g + i > key_last) ? -INFINITY : s[i];
+      s[i] = x;
+      mx = fmaxf(mx, x);
+    }
+    mx = pair_max32(pair_max16(mx));
+    const float m_new = fmaxf(m, mx);
+    const float alpha = fast_exp2(m - m_new);
+    float rs = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = fast_exp2(s[i] - m_new);
+      s[i] = p;
+      rs += p;
+    }
+    l = l * alpha + rs;
+    m = m_new;
+    // O^T[d][query] += V^T[d][key] P^T[key][query], MFMA k-index g <-> key key0+4g+i
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma4(vv[i][dt], s[i], oacc[dt]);
+    }
+    wave_lds_sync();  // this chunk's tiles are read before the next one overwrites them
+  }
+
+  // merge the waves' (max, sum, O) of each query: weights 2^(m_w - M);
+  // a wave with no chunk keeps m = -inf and weighs zero
+  const float lt = pair_sum32(pair_sum16(l));
+  if (g == 0) {
+    sm_m[wave][lq] = m;
+    sm_l[wave][lq] = lt;
+  }
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ks[lq * (DP + 4) + NDT * (4 * g + i) + dt] = oacc[dt][i];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kSW; ++w) M = fmaxf(M, sm_m[w][lq]);
+  float wt[kSW], Ls = 0.f;
+#pragma unroll
+  for (int w = 0; w < kSW; ++w) {
+    wt[w] = fast_exp2(sm_m[w][lq] - M);
+    Ls += wt[w] * sm_l[w][lq];
+  }
+  floatx4 out[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int off = lq * (DP + 4) + NDT * (4 * g + i) + dt;
+      float acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < kSW; ++w) acc += wt[w] * stage[w][0][off];
+      out[dt][i] = acc;
+    }
+  }
+  store_row_frag<DP, false>(O + base, qrow, L.T, L.D, L.st, g, out, 1.f / Ls);
+  if (LSE != nullptr && g == 0 && qrow < L.T) LSE[(int64_t)bh * L.T + qrow] = (M + log2f(Ls)) * kLn2;
+}
+
+// Key-stationary: a block owns keys 16kg .. 16kg+15 (lane column lq), its
+// waves sweep the query chunks kg+w, kg+w+kSW, ...  Per chunk: S = Q K^T and
+// dP = dO V^T (contractions over d, queries on MFMA rows), P = exp2(S - LSE),
+// dS = P (dP - Delta) with Delta = dO.O of the chunk's rows, then
+// dV^T += dO^T P and dK^T += Q^T dS (contractions over the chunk's rows).  dS
+// goes to the workspace (the 64-key column-block layout of ds_block_row, zeros
+// where masked and for rows past T) for attn_bwd_dq_small_kernel.
+template <int DP>
+__global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_dkv_small_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ O, const float* __restrict__ dO, const float* __restrict__ LSE, float* __restrict__ dK,
+    float* __restrict__ dV, float* __restrict__ DS, View L, float scale, float scale_log2) {
+  constexpr int DG = DP / 4, NDT = DP / 16, kSW = kSWof<DP>, TILE = 16 * (DP + 4);
+  // per wave: its Q, dO and O chunk tiles; after the sweep the space holds the
+  // waves' partial dV, then dK, for the sums
+  __shared__ __align__(16) float stage[kSW][3][TILE];
+
+  const int BH = L.B * L.H;
+  const int n_g = (L.T + 15) / 16;
+  const int bh = blockIdx.x % BH;
+  const int kg = (int)(blockIdx.x / BH);  // key group; kg = 0 (the longest sweep) first
+  const int b = bh / L.H, h = bh % L.H;
+  const int64_t base = (int64_t)b * L.sb + (int64_t)h * L.sh;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 15, g = lane >> 4;
+  const int krow = 16 * kg + lq;  // this lane's key (MFMA column)
+  float* qs = stage[wave][0];
+  float* os = stage[wave][1];  // dO
+  float* ys = stage[wave][2];  // O
+
+  // the block's 16 keys and values, staged once (waves 0 and 1, into wave 0's tiles)
+  if (wave < 2) {
+    ChunkRaw<DP> r;
+    r.load((wave == 0 ? K : V) + base, 16 * kg, L.T, L.D, L.st, lane);
+    r.store(stage[0][wave], lane);
+  }
+  __syncthreads();
+  float kf[DG], vf[DG];
+  row_frag<DP>(stage[0][0], lq, g, scale_log2, kf);
+  row_frag<DP>(stage[0][1], lq, g, 1.f, vf);
+  __syncthreads();  // every wave has its K / V fragments before wave 0 reuses its tiles
+
+  floatx4 dkacc[NDT], dvacc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+    dkacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    dvacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  // dS entry (q, krow): row q of the key's 64-key column block (q >= 16kg >= its first row)
+  const int kt = krow >> 6;
+  float* dsc = DS + ((int64_t)bh * ds_rows(L.T) + ds_block_row(kt, L.T) - (int64_t)64 * kt) * 64 + (krow & 63);
+  const float* lse = LSE + (int64_t)bh * L.T;
+
+  ChunkRaw<DP> qr, dr, orr;
+  float lsv[4];
+  auto load = [&](int c) {
+    qr.load(Q + base, 16 * c, L.T, L.D, L.st, lane);
+    dr.load(dO + base, 16 * c, L.T, L.D, L.st, lane);
+    orr.load(O + base, 16 * c, L.T, L.D, L.st, lane);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = 16 * c + 4 * g + i;
+      lsv[i] = q < L.T ? lse[q] * kLog2e : 0.f;
+    }
+  };
+  const int c0 = kg + wave;
+  if (c0 < n_g) load(c0);
+  for (int c = c0; c < n_g; c += kSW) {
+    const int q0 = 16 * c;
+    qr.store(qs, lane);
+    dr.store(os, lane);
+    orr.store(ys, lane);
+    float lse2[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lse2[i] = lsv[i];
+    wave_lds_sync();
+    if (c + kSW < n_g) load(c + kSW);  // the next chunk's loads in flight during this one
+
+    float qf[DG], df[DG], qc[4][NDT], dc[4][NDT];
+    row_frag<DP>(qs, lq, g, 1.f, qf);
+    row_frag<DP>(os, lq, g, 1.f, df);
+    col_frag<DP>(qs, lq, g, qc);
+    col_frag<DP>(os, lq, g, dc);
+    // Delta of query q0+lq (its d-range here, then the 4 lane groups); the
+    // accumulator rows are queries q0+4g+i: their Delta from lanes 4g+i
+    float dpart = 0.f;
+    {
+      float of[DG];
+      row_frag<DP>(ys, lq, g, 1.f, of);
+#pragma unroll
+      for (int j = 0; j < DG; ++j) dpart += df[j] * of[j];
+    }
+    const float delta_lq = pair_sum32(pair_sum16(dpart));
+    float dlt[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dlt[i] = __shfl(delta_lq, 4 * g + i, 64);
+    // S[query][key] (log2 units) and dP: lane element i = query q0+4g+i, key krow
+    floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f}, dp = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < DG; ++j) {
+      s = mfma4(qf[j], kf[j], s);
+      dp = mfma4(df[j], vf[j], dp);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = q0 + 4 * g + i;
+      const bool valid = (q >= krow) & (q < L.T) & (krow < L.T);
+      const float p = valid ? fast_exp2(s[i] - lse2[i]) : 0.f;
+      const float ds = valid ? p * (dp[i] - dlt[i]) : 0.f;
+      s[i] = p;
+      dp[i] = ds;
+      dsc[(int64_t)q * 64] = ds;  // q < 16*n_g <= rows of the layout
+    }
+    // dV^T[d][key] += dO^T[d][query] P[query][key]; dK^T[d][key] += Q^T[d][query] dS[query][key]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        dvacc[dt] = mfma4(dc[i][dt], s[i], dvacc[dt]);
+        dkacc[dt] = mfma4(qc[i][dt], dp[i], dkacc[dt]);
+      }
+    }
+    wave_lds_sync();  // this chunk's tiles are read before the next one overwrites them
+  }
+
+  float* sm = &stage[0][0][0];  // kSW * 3 tiles; the sums use the first kSW
+  __syncthreads();              // every wave is done with its staged chunks
+  sum_over_waves<DP>(sm, dvacc, wave, lq, g);
+  if (wave == 0) store_row_frag<DP, false>(dV + base, krow, L.T, L.D, L.st, g, dvacc, 1.f);
+  __syncthreads();  // wave 0 has read every partial of dV
+  sum_over_waves<DP>(sm, dkacc, wave, lq, g);
+  if (wave == 0) store_row_frag<DP, false>(dK + base, krow, L.T, L.D, L.st, g, dkacc, scale);
+}
+
+// Query-stationary dQ = scale * dS K: a block owns queries 16qg .. 16qg+15
+// (lane column lq), its waves take the key chunks w, w+kSW, ... <= qg.  A
+// lane's four dS values of a chunk (keys key0+4g .. +3 of its query) are one
+// 16-byte load; every one was written by attn_bwd_dkv_small_kernel (zeros
+// where masked).
+template <int DP>
+__global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_dq_small_kernel(const float* __restrict__ K,
+                                                                          const float* __restrict__ DS,
+                                                                          float* __restrict__ dQ, View L,
+                                                                          float scale) {
+  constexpr int NDT = DP / 16, kSW = kSWof<DP>, TILE = 16 * (DP + 4);
+  __shared__ __align__(16) float stage[kSW][TILE];
+
+  const int BH = L.B * L.H;
+  const int n_g = (L.T + 15) / 16;
+  const int bh = blockIdx.x % BH;
+  const int qg = n_g - 1 - (int)(blockIdx.x / BH);
+  const int b = bh / L.H, h = bh % L.H;
+  const int64_t base = (int64_t)b * L.sb + (int64_t)h * L.sh;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int lq = lane & 15, g = lane >> 4;
+  const int qrow = 16 * qg + lq;
+  const float* dsb = DS + (int64_t)bh * ds_rows(L.T) * 64;
+  float* ks = stage[wave];
+
+  floatx4 acc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  ChunkRaw<DP> kr;
+  floatx4 d4n = floatx4{0.f, 0.f, 0.f, 0.f};
+  auto load = [&](int c) {
+    const int key0 = 16 * c;
+    const int kt = key0 >> 6;  // qrow >= key0 >= 64kt: the row lies in the column block
+    d4n = *reinterpret_cast<const floatx4*>(dsb + (ds_block_row(kt, L.T) + qrow - 64 * kt) * 64 + (key0 & 63) +
+                                            4 * g);
+    kr.load(K + base, key0, L.T, L.D, L.st, lane);
+  };
+  if (wave <= qg) load(wave);
+  for (int c = wave; c <= qg; c += kSW) {
+    kr.store(ks, lane);
+    const floatx4 d4 = d4n;
+    wave_lds_sync();
+    if (c + kSW <= qg) load(c + kSW);  // the next chunk's loads in flight during this one
+    float kc[4][NDT];
+    col_frag<DP>(ks, lq, g, kc);
+    // dQ^T[d][query] += K^T[d][key] dS^T[key][query], k-index g <-> key key0+4g+i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma4(kc[i][dt], d4[i], acc[dt]);
+    }
+    wave_lds_sync();  // this chunk's tile is read before the next one overwrites it
+  }
+  __syncthreads();  // every wave is done with its staged chunks
+  sum_over_waves<DP>(&stage[0][0], acc, wave, lq, g);
+  if (wave == 0) store_row_frag<DP, false>(dQ + base, qrow, L.T, L.D, L.st, g, acc, scale);
+}
+
+bool small_problem(const View& L) {
+  return (int64_t)L.B * L.H * ((L.T + 63) / 64) < kSmallBlocks && L.T <= kSmallMaxT && padded_dim(L.D) != 0;
+}
+
+namespace {
+template <int DP>
+hipError_t fwd_small_t(const float* q, const float* k, const float* v, float* o, float* lse, const View& L,
+                       float scale, hipStream_t stream) {
+  const float sl2 = (float)((double)scale * 1.4426950408889634);
+  const dim3 grid((unsigned)((int64_t)L.B * L.H * ((L.T + 15) / 16)));
+  TimingScope ts("attn_fwd", stream);
+  hipLaunchKernelGGL(attn_fwd_small_kernel<DP>, grid, dim3(kSWof<DP> * 64), 0, stream, q, k, v, o, lse, L, sl2);
+  return hipGetLastError();
+}
+
+template <int DP>
+hipError_t bwd_small_t(const float* q, const float* k, const float* v, const float* o, const float* d_o,
+                       const float* lse, float* dq, float* dk, float* dv, float* ds, const View& L, float scale,
+                       hipStream_t stream) {
+  const float sl2 = (float)((double)scale * 1.4426950408889634);
+  const dim3 grid((unsigned)((int64_t)L.B * L.H * ((L.T + 15) / 16)));
+  {
+    TimingScope ts("attn_bwd_dkv", stream);
+    hipLaunchKernelGGL(attn_bwd_dkv_small_kernel<DP>, grid, dim3(kSWof<DP> * 64), 0, stream, q, k, v, o, d_o, lse,
+                       dk, dv, ds, L, scale, sl2);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  TimingScope ts("attn_bwd_dq", stream);
+  hipLaunchKernelGGL(attn_bwd_dq_small_kernel<DP>, grid, dim3(kSWof<DP> * 64), 0, stream, k, (const float*)ds, dq, L,
+                     scale);
+  return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_attn_fwd_small(const float* q, const float* k, const float* v, float* o, float* lse,
+                                 const View& L, float scale, hipStream_t stream) {
+  switch (padded_dim(L.D)) {
+    case 48: return fwd_small_t<48>(q, k, v, o, lse, L, scale, stream);
+    case 64: return fwd_small_t<64>(q, k, v, o, lse, L, scale, stream);
+    case 128: return fwd_small_t<128>(q, k, v, o, lse, L, scale, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_attn_bwd_small(const float* q, const float* k, const float* v, const float* o, const float* d_o,
+                                 const float* lse, float* dq, float* dk, float* dv, float* ds, const View& L,
+                                 float scale, hipStream_t stream) {
+  if (ds == nullptr) return hipErrorInvalidValue;
+  switch (padded_dim(L.D)) {
+    case 48: return bwd_small_t<48>(q, k, v, o, d_o, lse, dq, dk, dv, ds, L, scale, stream);
+    case 64: return bwd_small_t<64>(q, k, v, o, d_o, lse, dq, dk, dv, ds, L, scale, stream);
+    case 128: return bwd_small_t<128>(q, k, v, o, d_o, lse, dq, dk, dv, ds, L, scale, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace wha

@@ -76,7 +76,7 @@ __global__ __launch_bounds__(256) void wave_feat_kernel(const float* __restrict_
   for (int pidx = threadIdx.x; pidx < npos; pidx += 256) {
     const int tt = pidx / H, h = pidx % H;
     const float* pr = pblk + (int64_t)pidx * P;
-    const float phi = atan2f(pr[1], pr[0]);
+    const float phi = wave_phase(pr[1], pr[0]);
     const float n = softplus_f(hraw[h]);
     float sn, cn;
     sincosf(n * phi, &sn, &cn);

@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256) void wave_kv_query_kernel(const float* __restr
   if (i >= BH) return;
   const int h = i % H;
   const float r = proj[(int64_t)i * P + 0], s = proj[(int64_t)i * P + 1];
-  const float phi = atan2f(s, r);
+  const float phi = wave_phase(s, r);
   const float raw = hraw[h];
   const float n = raw > 20.f ? raw : logf(1.f + expf(raw));
   float sn, cn;

@@ -66,6 +66,15 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 __device__ __forceinline__ float xor_shfl(float x, int mask) { return __shfl_xor(x, mask, 64); }
 
+// phi = atan2(s, r) of the wave attention (src/common/attn.rs:121-128),
+// evaluated in double and rounded once to f32: the correctly rounded phase
+// (but for double-rounding cases of probability ~2^-29).  The reference's
+// f32::atan2 calls the host libm's atan2f; glibc 2.35's agrees with the
+// correctly rounded value on ~84% of inputs and is 1 ulp off otherwise, while
+// the device's f32 atan2f is up to 3 ulp off it -- and the phase decides a
+// discrete bucket, so the closer rounding keeps bucket flips rarer.
+__device__ __forceinline__ float wave_phase(float s, float r) { return (float)atan2((double)s, (double)r); }
+
 // Reductions over lane pairs (l, l^16) and (l, l^32) with the gfx950 VALU lane
 // swaps instead of an LDS permute.  With both operands = x,
 // v_permlane16_swap leaves lane l holding {x[l], x[l^16]} (in some order) and

@@ -37,6 +37,26 @@ inline bool dma_head_dim(int D) { return D % 4 == 0 && D > 48 && D <= 128; }
 // 0.164 ms per step).
 inline bool kept_head_dim(int D) { return D % 4 == 0 && D >= 48 && D <= 128; }
 
+// Small problems -- fewer than kSmallBlocks 64-row tiles over all (b,h) heads
+// and rows of at most kSmallMaxT -- run the 16-row split-sweep kernels of
+// attn_small.hip (wha_attn_fwd / wha_attn_bwd; such layouts keep no scores).
+constexpr int kSmallBlocks = 256;
+constexpr int kSmallMaxT = 1024;
+bool small_problem(const View& L);
+
+// Block-to-tile mapping of the direct-to-LDS kernels: by default a block takes
+// the 64-row tiles p and n-1-p of one (b,h) (equal causal work per block).
+// When those ceil(n/2)*B*H blocks would not give every CU three, each block
+// takes one tile instead, the longest first, so the shorter tiles fill the
+// slots the longer ones leave (the 384-dim config: 1024 blocks, not 512).
+inline int dma_unpaired(const View& L) {
+  return (int64_t)((L.T + 63) / 64 + 1) / 2 * L.B * L.H < 3 * 256 ? 1 : 0;
+}
+inline int64_t dma_tiles(const View& L, int unpaired) {
+  const int n = (L.T + 63) / 64;
+  return unpaired ? n : (n + 1) / 2;
+}
+
 // Optional per-kernel HIP-event timing (implemented in wha_api.hip).
 struct TimingScope {
   TimingScope(const char* name, hipStream_t stream);
@@ -51,6 +71,15 @@ struct TimingScope {
 hipError_t launch_attn_fwd(const float* q, const float* k, const float* v, float* o, float* lse,
                            const View& L, bool vec, float scale, hipStream_t stream, float* scores = nullptr);
 
+// The small-problem kernels (attn_small.hip): forward, and the backward as a
+// key-stationary pass (dK, dV, dS; Delta formed in place) plus dQ from dS
+// (ds: bwd_ds_floats(L) floats).
+hipError_t launch_attn_fwd_small(const float* q, const float* k, const float* v, float* o, float* lse,
+                                 const View& L, float scale, hipStream_t stream);
+hipError_t launch_attn_bwd_small(const float* q, const float* k, const float* v, const float* o, const float* d_o,
+                                 const float* lse, float* dq, float* dk, float* dv, float* ds, const View& L,
+                                 float scale, hipStream_t stream);
+
 // Delta pass of the from-probabilities backward on the forward's direct-to-LDS
 // tiles (dma_head_dim(D), 128-bit operands): stats <- the -Delta blocks of
 // attn_bwd_dkv_dma_kernel, Delta_t = sum_j att[t][j] (dO_t . V_j).  av: T % 4
@@ -59,7 +88,7 @@ hipError_t launch_probs_delta_dma(const float* d_o, const float* v, const float*
                                   bool av, hipStream_t stream);
 
 // Whether the forward can keep its scores for this layout (the direct-to-LDS
-// kernels: 16-byte-aligned operands, dma_head_dim(D)).
+// kernels: 16-byte-aligned operands, kept_head_dim(D), not a small problem).
 bool scores_kept(const View& L, bool vec);
 
 // Floats of the dS buffer the fused backward uses (the causal half of the
