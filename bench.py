@@ -451,6 +451,33 @@ def wave_admitted_pairs(bucket, torch):
     return admitted, bk.shape[0] * bk.shape[1] * (T * (T + 1) // 2)
 
 
+def wave_sparse_executed_pairs(bucket, torch):
+    """Pairs the bucket-sparse kernels execute: per (b,h), positions sorted by
+    bucket (stable) in 16-row chunks; a (query chunk, key chunk) block runs when
+    some bucket of one is within one of some bucket of the other and the key
+    chunk's first position is not after the query chunk's last (the schedule
+    of wave-engine_amd/csrc/wave_sparse.hip), 256 pairs per block."""
+    bk = bucket.long().reshape(-1, bucket.shape[-1])
+    N, T = bk.shape
+    NC = (T + 15) // 16
+    vals, pos = torch.sort(bk, dim=1, stable=True)
+    pad = NC * 16 - T
+    valid = torch.ones_like(vals, dtype=torch.bool)
+    if pad:
+        vals = torch.nn.functional.pad(vals, (0, pad))
+        pos = torch.nn.functional.pad(pos, (0, pad))
+        valid = torch.nn.functional.pad(valid, (0, pad))
+    vals, pos, valid = (a.reshape(N, NC, 16) for a in (vals, pos, valid))
+    sets = (torch.nn.functional.one_hot(vals, 8) * valid.unsqueeze(-1)).amax(dim=2).float()   # [N, NC, 8]
+    near = ((sets + sets.roll(1, dims=-1) + sets.roll(-1, dims=-1)) > 0).float()
+    bucket_live = torch.bmm(near, sets.transpose(1, 2)) > 0                                   # [N, qc, kc]
+    big = torch.iinfo(torch.int64).max
+    pmin = torch.where(valid, pos, torch.full_like(pos, big)).amin(dim=2)
+    pmax = torch.where(valid, pos, torch.full_like(pos, -1)).amax(dim=2)
+    causal = pmin.unsqueeze(1) <= pmax.unsqueeze(2)                                            # [N, qc, kc]
+    return 256 * int((bucket_live & causal).sum().item())
+
+
 def wave_credited_flops(B, H, T, D, C, admitted=None):
     """FLOPs of one wave-attention layer step (wave_attention_forward +
     wave_attention_backward_full).  The core terms are credited for the pairs
@@ -490,9 +517,10 @@ def run_wave(args, cfg, pkg, torch):
         _, _, cache = pkg.wave_attention_forward(W, x, out=out)
         pkg.wave_attention_backward_full(W, cache, dy, workspace=ws)
 
+    pkg.wave_set_bucket_sparse({"auto": "auto", "sparse": True, "dense": False}[args.wave_family])
     warm_s, _ = settle(step, args, torch)
-    names = ("wave_feat", "wave_fwd", "wave_bwd_delta", "wave_bwd_dkv", "wave_bwd_dq", "wave_feat_bwd",
-             "wave_harmonic", "linear_fwd", "linear_bwd_dx", "linear_bwd_dw")
+    names = ("wave_feat", "wave_sort", "wave_gather", "wave_fwd", "wave_bwd_delta", "wave_bwd_dkv", "wave_bwd_dq",
+             "wave_feat_bwd", "wave_harmonic", "linear_fwd", "linear_bwd_dx", "linear_bwd_dw")
     pkg.timing_reset()
     pkg.timing_enable(True)
     torch.cuda.synchronize()
@@ -516,7 +544,9 @@ def run_wave(args, cfg, pkg, torch):
     _, _, cache = pkg.wave_attention_forward(W, x, out=out)
     admitted, causal = wave_admitted_pairs(cache.bucket, torch)
     fl = wave_credited_flops(B, H, T, D, C, admitted)
-    fl_exec = wave_credited_flops(B, H, T, D, C)
+    sparse = args.wave_family == "sparse" or (args.wave_family == "auto" and T >= 1024)
+    executed = wave_sparse_executed_pairs(cache.bucket, torch) if sparse else causal
+    fl_exec = wave_credited_flops(B, H, T, D, C, executed)
     dom = max(("wave_fwd", "wave_bwd_dkv", "wave_bwd_dq"), key=lambda n: kern[n]["avg_ms"])
     achieved = fl[dom] / (kern[dom]["avg_ms"] * 1e-3) / 1e12
     return {
@@ -529,6 +559,9 @@ def run_wave(args, cfg, pkg, torch):
                    "content_dim": C, "parallelism": "none (1 GPU)"},
         "tflops": fl["total"] / (ms_per_step * 1e-3) / 1e12,
         "mask_fraction": admitted / causal,
+        "kernels": ("bucket-sparse (positions sorted by bucket, 16 x 16 blocks the mask can admit)" if sparse
+                    else "all causal pairs, mask per score"),
+        "executed_over_admitted": executed / admitted,
         "credit": "core FLOPs over the admitted (bucket-mask) pairs only",
         "kernel_ms_per_step": {n: round(kern[n]["total_ms"], 5) for n in names},
         "ms_per_step_with_events": wall / args.steps * 1e3,
@@ -796,6 +829,9 @@ def main():
     ap.add_argument("--settle", type=float, default=2.0,
                     help="seconds the step is repeated (after --warmup steps) before the first timed region")
     ap.add_argument("--config", default="768", choices=sorted(CONFIGS))
+    ap.add_argument("--wave-family", default="auto", choices=("auto", "sparse", "dense"),
+                    help="wave attention kernels (--config wave): the library's default (bucket-sparse from "
+                         "T = 1024), bucket-sparse, or all causal pairs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-suite", dest="suite", action="store_false",
                     help="768 only: leave out the other BASELINE configs")

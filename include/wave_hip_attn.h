@@ -326,6 +326,18 @@ int wha_wave_bwd(const float* x, const float* d_out, const wha_wave_weights* w, 
 int wha_wave_probs_rows(const wha_wave_cache* cache, const wha_wave_shape* shape, const int32_t* rows,
                         int32_t n_rows, float* out, void* stream);
 
+/* Kernel family of wha_wave_fwd / wha_wave_bwd, process-wide (no counterpart
+ * in the reference; for tests and benchmarks).  mode 1 = bucket-sparse: every
+ * (b,h)'s positions sorted by bucket, scores computed only in the 16 x 16
+ * blocks the bucket mask can admit, the previous-position term added per
+ * query; 0 = every causal pair scored and the mask applied per score;
+ * 2 (the default) = bucket-sparse for T >= 1024, where it is measured no
+ * slower, all pairs below.  Both give the reference's results within fp32
+ * rounding; the sparse family needs up to twice the score-gradient workspace,
+ * which wha_wave_bwd_workspace_size always includes.  Returns the previous
+ * mode, or -1 (mode unchanged) for a mode outside 0..2. */
+int wha_wave_set_bucket_sparse(int mode);
+
 /* Host forms (one sequence, host arrays, synchronous), for callers that keep
  * activations on the host as the reference does.  `w` holds HOST pointers in
  * the wha_wave_weights layout; x, out, d_attn_out, d_x are [T][n_embd].

@@ -72,6 +72,7 @@ extern "C" {
                         workspace_bytes: usize, stream: *mut c_void) -> c_int;
     pub fn wha_wave_probs_rows(cache: *const WhaWaveCache, shape: *const WhaWaveShape, rows: *const i32,
                                n_rows: i32, out: *mut f32, stream: *mut c_void) -> c_int;
+    pub fn wha_wave_set_bucket_sparse(mode: c_int) -> c_int;
     pub fn wha_wave_kv_prefill_workspace_size(shape: *const WhaWaveShape) -> usize;
     pub fn wha_wave_kv_prefill(x: *const f32, w: *const WhaWaveWeights, shape: *const WhaWaveShape,
                                kv: *const WhaWaveKvCache, out: *mut f32, workspace: *mut c_void,

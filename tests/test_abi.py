@@ -180,6 +180,31 @@ def test_wave_entry_points_validate_before_device_use(pkg):
     assert L.wha_wave_probs_rows(ctypes.byref(cache), ctypes.byref(sh), rows, 1, p, None) == WHA_ERR_INVALID
 
 
+def test_wave_kernel_family_switch(pkg):
+    """wha_wave_set_bucket_sparse: modes 0..2 (default 2, automatic), anything
+    else rejected with -1 and the mode unchanged; the backward workspace covers
+    the sparse family's score-gradient blocks (one [T16][64] block per 64
+    sorted keys) and sorted operands whatever the mode."""
+    L = pkg.lib()
+    prev = L.wha_wave_set_bucket_sparse(2)
+    try:
+        assert prev in (0, 1, 2)
+        assert L.wha_wave_set_bucket_sparse(7) == -1 and L.wha_wave_set_bucket_sparse(-1) == -1
+        assert L.wha_wave_set_bucket_sparse(0) == 2
+        assert L.wha_wave_set_bucket_sparse(1) == 0
+        assert L.wha_wave_set_bucket_sparse(2) == 1
+        assert pkg.wave_set_bucket_sparse("auto") == 2 and pkg.wave_set_bucket_sparse(False) == 2
+        with pytest.raises(ValueError):
+            pkg.wave_set_bucket_sparse(5)
+    finally:
+        L.wha_wave_set_bucket_sparse(prev)
+    B, T, E, H, C = 8, 1024, 768, 12, 16
+    sh = pkg.WaveShape(B, T, E, H, C)
+    n = L.wha_wave_bwd_workspace_size(ctypes.byref(sh))
+    sparse_ds = B * H * (T // 64) * T * 64 * 4
+    assert n > sparse_ds + B * T * E * 4 * 2
+
+
 @no_device
 def test_wave_kv_entry_points_validate(pkg):
     L = pkg.lib()

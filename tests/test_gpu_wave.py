@@ -1,8 +1,9 @@
 """Wave (harmonic coherence) attention on the GPU against the oracle
 (src/common/attn.rs:72-430): forward, cache, rows of att_weights_all, full and
-pathway backward.  The oracle replays the device's phases (phase_in) so both
-sides form the same bucket mask; the phases themselves, the projections and the
-buckets are checked separately (the bucket bit for bit)."""
+pathway backward, with both kernel families (bucket-sparse and all pairs).
+The oracle replays the device's phases (phase_in) so both sides form the same
+bucket mask; the phases themselves, the projections and the buckets are
+checked separately (the bucket bit for bit)."""
 import math
 
 import numpy as np
@@ -26,6 +27,15 @@ def torch_dev():
     return torch, torch.device("cuda:0")
 
 
+@pytest.fixture(params=["sparse", "dense"])
+def family(request, pkg):
+    """Both kernel families of wha_wave_fwd / wha_wave_bwd: bucket-sparse (the
+    default) and all causal pairs."""
+    prev = pkg.wave_set_bucket_sparse(request.param == "sparse")
+    yield request.param
+    pkg.wave_set_bucket_sparse(prev)
+
+
 def _setup(pkg, torch, dev, B, T, E, H, C, seed):
     w = make_wave_weights(H, C, E, seed)
     x = np.random.default_rng(seed + 1).normal(size=(B, T, E)).astype(np.float32)
@@ -36,9 +46,9 @@ def _setup(pkg, torch, dev, B, T, E, H, C, seed):
 
 
 @pytest.mark.parametrize("B,T,E,H,C", CONFIGS)
-def test_wave_forward_matches_oracle(pkg, torch_dev, B, T, E, H, C):
+def test_wave_forward_matches_oracle(pkg, torch_dev, family, B, T, E, H, C):
     torch, dev = torch_dev
-    print(f"wave fwd B{B} T{T} E{E} H{H} C{C}", flush=True)
+    print(f"wave fwd {family} B{B} T{T} E{E} H{H} C{C}", flush=True)
     w, x, W, tx = _setup(pkg, torch, dev, B, T, E, H, C, seed=7 + T)
     out, att_rows, cache = pkg.wave_attention_forward(W, tx)
     torch.cuda.synchronize()
@@ -74,9 +84,9 @@ def test_wave_forward_matches_oracle(pkg, torch_dev, B, T, E, H, C):
 
 
 @pytest.mark.parametrize("B,T,E,H,C", CONFIGS)
-def test_wave_backward_matches_oracle(pkg, torch_dev, B, T, E, H, C):
+def test_wave_backward_matches_oracle(pkg, torch_dev, family, B, T, E, H, C):
     torch, dev = torch_dev
-    print(f"wave bwd B{B} T{T} E{E} H{H} C{C}", flush=True)
+    print(f"wave bwd {family} B{B} T{T} E{E} H{H} C{C}", flush=True)
     w, x, W, tx = _setup(pkg, torch, dev, B, T, E, H, C, seed=11 + T)
     # d_out scaled by 1/sqrt(B*T) so that batch-summed weight gradients stay O(1)
     dy = (np.random.default_rng(T).normal(size=(B, T, E)) / math.sqrt(B * T)).astype(np.float32)
@@ -106,7 +116,7 @@ def test_wave_backward_matches_oracle(pkg, torch_dev, B, T, E, H, C):
     assert_parity("d_out_b", grads.out_proj_b.cpu().numpy(), s("d_out_b"))
 
 
-def test_wave_backward_is_deterministic(pkg, torch_dev):
+def test_wave_backward_is_deterministic(pkg, torch_dev, family):
     torch, dev = torch_dev
     B, T, E, H, C = 2, 300, 256, 4, 16
     w, x, W, tx = _setup(pkg, torch, dev, B, T, E, H, C, seed=3)

@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "wha_attn_scores_size", "wha_attn_fwd_keep", "wha_attn_bwd_kept",
     "wha_decode_workspace_size", "wha_decode_fwd", "wha_decode_fwd_noalloc", "wha_attn_probs_rows",
     "wha_wave_fwd", "wha_wave_bwd_workspace_size", "wha_wave_bwd", "wha_wave_probs_rows",
+    "wha_wave_set_bucket_sparse",
     "wha_wave_kv_prefill_workspace_size", "wha_wave_kv_prefill", "wha_wave_kv_decode_workspace_size",
     "wha_wave_kv_decode", "wha_host_wave_attention_forward", "wha_host_wave_attention_backward",
     "wha_linear_fwd", "wha_linear_bwd_dx", "wha_linear_bwd_dw_workspace_size", "wha_linear_bwd_dw",
@@ -159,6 +160,7 @@ def lib():
         L.wha_wave_bwd_workspace_size.restype = sz
         L.wha_wave_bwd.argtypes = [vp, vp, wwp, wsp, wcp, wgp, vp, sz, vp]
         L.wha_wave_probs_rows.argtypes = [wcp, wsp, ctypes.POINTER(ctypes.c_int32), i32, vp, vp]
+        L.wha_wave_set_bucket_sparse.argtypes = [ctypes.c_int]
         L.wha_host_wave_attention_forward.argtypes = [f32p, wwp, i32, i32, i32, i32, f32p, vp]
         L.wha_host_wave_attention_backward.argtypes = [f32p, f32p, wwp, i32, i32, i32, i32, wgp]
         kvp = ctypes.POINTER(_WaveKvC)
@@ -497,6 +499,18 @@ class AttnPlan:
         rc = self._b(*self._bwd_args)
         if rc:
             _check(self._bname, rc)
+
+
+def wave_set_bucket_sparse(mode) -> int:
+    """Selects the wave attention's kernel family (process-wide): True / 1 =
+    bucket-sparse (scores only in the 16 x 16 blocks of bucket-sorted
+    positions the mask can admit), False / 0 = every causal pair, "auto" / 2
+    (the default) = bucket-sparse from T = 1024.  Returns the previous mode."""
+    m = 2 if mode == "auto" else int(mode)
+    prev = lib().wha_wave_set_bucket_sparse(m)
+    if prev < 0:
+        raise ValueError(f"wave kernel family must be 0, 1 or 2 (got {mode!r})")
+    return prev
 
 
 # ------------------------------------------------------------------ timing

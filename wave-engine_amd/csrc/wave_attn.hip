@@ -33,22 +33,7 @@ namespace {
 constexpr int kFP = kWaveFeatures;  // padded feature width
 constexpr int kLDF = kFP + 4;       // LDS pitch of a feature tile
 
-// phase_to_bucket (src/common/kv_cache.rs:66-70) in f32, operation for operation:
-// fmod is exact and + and / are correctly rounded, so equal inputs give the
-// reference's bucket bit for bit.
-__device__ __forceinline__ int phase_bucket(float phi) {
-  const float tau = 6.28318548f;  // std::f32::consts::TAU
-  const float width = tau / 8.f;
-  const float nrm = fmodf(fmodf(phi, tau) + tau, tau);
-  const float q = nrm / width;
-  const int b = (q >= 0.f) ? (q < 8.f ? (int)q : 8) : 0;
-  return b < 7 ? b : 7;
-}
-
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : logf(1.f + expf(x)); }
-
-// Bucket relation of the mask: (kb - qb) mod 8 in {7, 0, 1}.
-__device__ __forceinline__ bool bucket_near(int kb, int qb) { return ((kb - qb + 1) & 7) <= 2; }
 }  // namespace
 
 // proj [B][T][H][P] (P = 2 + C: r, s, content) -> feat [B][H][T][32]
@@ -89,7 +74,7 @@ __global__ __launch_bounds__(256) void wave_feat_kernel(const float* __restrict_
       f[2 + j] = v;
     }
     ps[h * tn + tt] = phi;
-    bs[h * tn + tt] = phase_bucket(phi);
+    bs[h * tn + tt] = wave_phase_bucket(phi);
   }
   __syncthreads();
   // per head: tn feature rows (tn*8 float4), tn phases and buckets, each contiguous in memory
@@ -218,7 +203,7 @@ __global__ __launch_bounds__(NW * 64) void wave_fwd_kernel(const float* __restri
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int kk = 16 * mt + 4 * g + i;
-        const bool valid = (kk <= key_lim) & (bucket_near(kbv[i], qb) | (kk == prev));
+        const bool valid = (kk <= key_lim) & (wave_bucket_near(kbv[i], qb) | (kk == prev));
         const float x = valid ? s[mt][i] : -INFINITY;
         s[mt][i] = x;
         mx = fmaxf(mx, x);
@@ -410,7 +395,7 @@ __global__ __launch_bounds__(256) void wave_dkv_kernel(const float* __restrict__
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int q = qbase + 16 * mt + 4 * g + i;
-        const bool valid = (q >= krow) & (q < q_end) & (bucket_near(kb, bq4[i]) | (q == krow + 1));
+        const bool valid = (q >= krow) & (q < q_end) & (wave_bucket_near(kb, bq4[i]) | (q == krow + 1));
         float p = fast_exp2(s[mt][i] - lq4[i]);
         p = valid ? p : 0.f;
         s[mt][i] = p;
@@ -576,7 +561,7 @@ __global__ __launch_bounds__(256) void wave_probs_rows_kernel(const float* __res
     float p = -INFINITY;
     if (j <= t) {
       p = 0.f;
-      if (bucket_near(Bh[j], qb) || j == t - 1) {
+      if (wave_bucket_near(Bh[j], qb) || j == t - 1) {
         const float* kr = Fh + (int64_t)j * kFP;
         float dot = 0.f;
         for (int f = 0; f < kFP; ++f) dot += qs[f] * kr[f];

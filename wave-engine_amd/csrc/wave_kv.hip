@@ -26,15 +26,6 @@ constexpr int kKvGroups = kKvThreads / 16;
 constexpr int kKvUnroll = 4;
 constexpr int kKvMaxChunk = 1024;  // keys per block (wave_kv_chunk never exceeds it)
 
-__device__ __forceinline__ int phase_bucket_kv(float phi) {
-  const float tau = 6.28318548f;  // std::f32::consts::TAU
-  const float width = tau / 8.f;
-  const float nrm = fmodf(fmodf(phi, tau) + tau, tau);
-  const float q = nrm / width;
-  const int b = (q >= 0.f) ? (q < 8.f ? (int)q : 8) : 0;
-  return b < 7 ? b : 7;
-}
-__device__ __forceinline__ bool bucket_near_kv(int kb, int qb) { return ((kb - qb + 1) & 7) <= 2; }
 }  // namespace
 
 int wave_kv_chunk(int max_len) {
@@ -56,7 +47,7 @@ __global__ __launch_bounds__(256) void wave_kv_query_kernel(const float* __restr
   const float n = raw > 20.f ? raw : logf(1.f + expf(raw));
   float sn, cn;
   sincosf(n * phi, &sn, &cn);
-  qinfo[i] = make_float4(cn, sn, phi, __int_as_float(phase_bucket_kv(phi)));
+  qinfo[i] = make_float4(cn, sn, phi, __int_as_float(wave_phase_bucket(phi)));
 }
 
 // One chunk (<= 1024 keys) of one (b,h): partial (max, sum, o[DP]) in the log2
@@ -105,7 +96,7 @@ __global__ __launch_bounds__(kKvThreads) void wave_kv_split_kernel(const float4*
     const bool in = key < k_end;
     const int kb = in ? BK[hb + key] : 0;
     const float2 c = in ? CS[hb + key] : make_float2(0.f, 0.f);
-    valid[i] = in && (bucket_near_kv(kb, qb) || key == len - 1);
+    valid[i] = in && (wave_bucket_near(kb, qb) || key == len - 1);
     score[i] = cq * c.x + sq * c.y;
     const unsigned long long mask = __ballot(valid[i]);
     pos[i] = __popcll(mask & ((1ull << lane) - 1ull));

@@ -641,6 +641,26 @@ static int check_wave_weights(const wha_wave_weights* w, const char* fn) {
   return WHA_OK;
 }
 
+// 0: all pairs, 1: bucket-sparse, 2: bucket-sparse from kWaveSparseMinT positions
+static std::atomic<int> g_wave_sparse{2};
+static constexpr int kWaveSparseMinT = 1024;
+
+int wha_wave_set_bucket_sparse(int mode) {
+  if (mode < 0 || mode > 2) return -1;
+  return g_wave_sparse.exchange(mode);
+}
+
+// The bucket-sparse kernels serve a shape when their score-gradient buffer
+// (one [T16][64] block per 64 sorted keys, worst case every pair in the
+// window) fits the cap the dense layout has.
+static bool wave_sparse_fits(const wha_wave_shape* sh) {
+  return wha::wave_sparse_ds_floats(sh->B, sh->n_head, sh->T) * sizeof(float) <= kMaxDsBytes;
+}
+static bool wave_sparse_on(const wha_wave_shape* sh) {
+  const int mode = g_wave_sparse.load(std::memory_order_relaxed);
+  return (mode == 1 || (mode == 2 && sh->T >= kWaveSparseMinT)) && wave_sparse_fits(sh);
+}
+
 int wha_wave_fwd(const float* x, const wha_wave_weights* w, const wha_wave_shape* shape, float* out,
                  const wha_wave_cache* cache, void* stream) {
   static const char* fn = "wha_wave_fwd";
@@ -660,9 +680,16 @@ int wha_wave_fwd(const float* x, const wha_wave_weights* w, const wha_wave_shape
   if (e == hipSuccess)
     e = wha::launch_wave_features(cache->proj, w->harmonic_raw, cache->feat, cache->phase, cache->bucket, B, H, T,
                                   C, C, s);
-  if (e == hipSuccess)
-    e = wha::launch_wave_fwd(cache->feat, cache->bucket, cache->values, cache->merged, cache->lse, Lv,
-                             vec_ok(Lv, {cache->values, cache->merged}), cs, s);
+  const bool vec = vec_ok(Lv, {cache->values, cache->merged});
+  if (e == hipSuccess && wave_sparse_on(shape)) {
+    // sorted copies of the operands: library scratch (the backward sorts again)
+    void* ws = nullptr;
+    if ((rc = cached_workspace(wha::wave_sparse_fwd_floats(B, H, T, hd) * sizeof(float), s, &ws))) return rc;
+    e = wha::launch_wave_fwd_sparse(cache->feat, cache->bucket, cache->values, cache->merged, cache->lse,
+                                    static_cast<float*>(ws), Lv, vec, cs, s);
+  } else if (e == hipSuccess) {
+    e = wha::launch_wave_fwd(cache->feat, cache->bucket, cache->values, cache->merged, cache->lse, Lv, vec, cs, s);
+  }
   if (e == hipSuccess) e = wha::launch_linear_fwd(cache->merged, E, w->out_w, w->out_b, out, E, M, E, E, s);
   if (e != hipSuccess) return hip_fail(e, "wha_wave_fwd launch");
   g_err[0] = 0;
@@ -671,7 +698,7 @@ int wha_wave_fwd(const float* x, const wha_wave_weights* w, const wha_wave_shape
 
 // Workspace of wha_wave_bwd, in floats, each part rounded to 64 floats.
 struct WaveBwdParts {
-  size_t d_merged, delta, ds, dfk, dfq, dv, dproj, hpart, gemm, total;
+  size_t d_merged, delta, ds, dfk, dfq, dv, dproj, hpart, gemm, sorted, total;
 };
 
 static WaveBwdParts wave_bwd_parts(const wha_wave_shape* sh) {
@@ -682,7 +709,12 @@ static WaveBwdParts wave_bwd_parts(const wha_wave_shape* sh) {
   WaveBwdParts p{};
   p.d_merged = r64(B * T * E);
   p.delta = r64(B * H * T);
+  // dS for either kernel family, and the sparse family's sorted operands
   p.ds = r64(wha::bwd_ds_floats(wave_view(sh)));
+  if (wave_sparse_fits(sh)) {
+    p.ds = std::max(p.ds, r64(wha::wave_sparse_ds_floats((int)B, (int)H, (int)T)));
+    p.sorted = r64(wha::wave_sparse_bwd_floats((int)B, (int)H, (int)T, (int)(E / H)));
+  }
   p.dfk = r64(B * H * T * wha::kWaveFeatures);
   p.dfq = p.dfk;
   p.dv = r64(B * T * E);
@@ -692,7 +724,7 @@ static WaveBwdParts wave_bwd_parts(const wha_wave_shape* sh) {
   g = std::max(g, wha::linear_dw_workspace_floats((int)(H * P), (int)E, M));
   g = std::max(g, wha::linear_dw_workspace_floats(hd, hd, M, (int)H));
   p.gemm = r64(g);
-  p.total = p.d_merged + p.delta + p.ds + p.dfk + p.dfq + p.dv + p.dproj + p.hpart + p.gemm;
+  p.total = p.d_merged + p.delta + p.ds + p.dfk + p.dfq + p.dv + p.dproj + p.hpart + p.gemm + p.sorted;
   return p;
 }
 
@@ -718,7 +750,8 @@ int wha_wave_bwd(const float* x, const float* d_out, const wha_wave_weights* w, 
     return fail(WHA_ERR_INVALID, "%s: the weight gradients must be all non-NULL or all NULL", fn);
   const bool full = n_set == 7;
   const WaveBwdParts parts = wave_bwd_parts(shape);
-  if (parts.ds * sizeof(float) > kMaxDsBytes)
+  const bool sparse = wave_sparse_on(shape);
+  if (!sparse && wha::bwd_ds_floats(wave_view(shape)) * sizeof(float) > kMaxDsBytes)
     return fail(WHA_ERR_UNSUPPORTED, "%s: B*n_head*T^2 too large for the score-gradient buffer", fn);
   hipStream_t s = static_cast<hipStream_t>(stream);
   void* wsv = nullptr;
@@ -741,6 +774,8 @@ int wha_wave_bwd(const float* x, const float* d_out, const wha_wave_weights* w, 
   float* hpart = p;
   p += parts.hpart;
   float* gws = p;
+  p += parts.gemm;
+  float* sorted = p;
 
   const int B = shape->B, T = shape->T, E = shape->n_embd, H = shape->n_head, C = shape->content_dim;
   const int hd = E / H, HP = H * (2 + C), M = B * T;
@@ -750,7 +785,10 @@ int wha_wave_bwd(const float* x, const float* d_out, const wha_wave_weights* w, 
   hipError_t e = wha::launch_linear_bwd_dx(d_out, E, w->out_w, d_merged, E, M, E, E, s);
   if (e == hipSuccess && full)
     e = wha::launch_linear_bwd_dw(d_out, E, cache->merged, E, grads->d_out_w, grads->d_out_b, M, E, E, gws, s);
-  if (e == hipSuccess)
+  if (e == hipSuccess && sparse)
+    e = wha::launch_wave_bwd_core_sparse(cache->feat, cache->bucket, cache->values, cache->merged, d_merged,
+                                         cache->lse, delta, dfk, dfq, dv, ds, sorted, Lv, vec, cs, s);
+  else if (e == hipSuccess)
     e = wha::launch_wave_bwd_core(cache->feat, cache->bucket, cache->values, cache->merged, d_merged, cache->lse,
                                   delta, dfk, dfq, dv, ds, Lv, vec, cs, s);
   if (e == hipSuccess)

@@ -75,6 +75,23 @@ __device__ __forceinline__ float xor_shfl(float x, int mask) { return __shfl_xor
 // discrete bucket, so the closer rounding keeps bucket flips rarer.
 __device__ __forceinline__ float wave_phase(float s, float r) { return (float)atan2((double)s, (double)r); }
 
+// phase_to_bucket (src/common/kv_cache.rs:66-70) in f32, operation for operation:
+// fmod is exact and + and / are correctly rounded, so equal inputs give the
+// reference's bucket bit for bit.
+__device__ __forceinline__ int wave_phase_bucket(float phi) {
+  const float tau = 6.28318548f;  // std::f32::consts::TAU
+  const float width = tau / 8.f;
+  const float nrm = fmodf(fmodf(phi, tau) + tau, tau);
+  const float q = nrm / width;
+  const int b = (q >= 0.f) ? (q < 8.f ? (int)q : 8) : 0;
+  return b < 7 ? b : 7;
+}
+
+// The wave attention's bucket relation (src/common/attn.rs:189-224): key
+// bucket kb and query bucket qb within one of each other mod 8, i.e.
+// (kb - qb) mod 8 in {7, 0, 1}.  Symmetric in its arguments.
+__device__ __forceinline__ bool wave_bucket_near(int kb, int qb) { return ((kb - qb + 1) & 7) <= 2; }
+
 // Reductions over lane pairs (l, l^16) and (l, l^32) with the gfx950 VALU lane
 // swaps instead of an LDS permute.  With both operands = x,
 // v_permlane16_swap leaves lane l holding {x[l], x[l^16]} (in some order) and

@@ -183,6 +183,21 @@ hipError_t launch_wave_fwd(const float* feat, const int* bucket, const float* v,
 hipError_t launch_wave_bwd_core(const float* feat, const int* bucket, const float* v, const float* merged,
                                 const float* d_merged, const float* lse, float* delta, float* dfk, float* dfq,
                                 float* dv, float* ds, const View& Lv, bool vec, float cs, hipStream_t stream);
+
+// Bucket-sparse wave attention core (wave_sparse.hip): sorts every (b,h)'s
+// positions by bucket into ws and executes only the 16 x 16 blocks the bucket
+// mask can admit.  ws: wave_sparse_fwd_floats (forward) or
+// wave_sparse_bwd_floats (backward) floats, 16-byte aligned; ds:
+// wave_sparse_ds_floats floats.
+size_t wave_sparse_fwd_floats(int B, int H, int T, int D);
+size_t wave_sparse_bwd_floats(int B, int H, int T, int D);
+size_t wave_sparse_ds_floats(int B, int H, int T);
+hipError_t launch_wave_fwd_sparse(const float* feat, const int* bucket, const float* v, float* merged, float* lse,
+                                  float* ws, const View& Lv, bool vec, float cs, hipStream_t stream);
+hipError_t launch_wave_bwd_core_sparse(const float* feat, const int* bucket, const float* v, const float* merged,
+                                       const float* d_merged, const float* lse, float* delta, float* dfk, float* dfq,
+                                       float* dv, float* ds, float* ws, const View& Lv, bool vec, float cs,
+                                       hipStream_t stream);
 // Rows of the wave attention probabilities: out [B][H][rl.n][T].
 hipError_t launch_wave_probs_rows(const float* feat, const int* bucket, const float* lse, const RowList& rl,
                                   float* out, int B, int H, int T, float cs, hipStream_t stream);
