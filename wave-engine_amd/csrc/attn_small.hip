@@ -101,30 +101,33 @@ __device__ __forceinline__ void col_frag(const float* tile, int lq, int g, float
   }
 }
 
-// Adds the waves' partial accumulators (acc[dt][i] = X[row lq][NDT*(4g+i)+dt])
-// through LDS in wave order; wave 0 gets the sum in acc.  sm: kSW tiles of
-// [16][DP + 4] floats.
+// The waves' partial accumulators written to LDS by write_wave_part (wave w's
+// tile at sm + w*TILE) are summed by the whole block, one output element per
+// thread in turn, adding the waves in order (deterministic), and row r of the
+// 16 goes to row row0 + r of dst, times mul.  Requires a __syncthreads()
+// between the writes and this call.
 template <int DP>
-__device__ __forceinline__ void sum_over_waves(float* sm, floatx4 (&acc)[DP / 16], int wave, int lq, int g) {
-  constexpr int NDT = DP / 16, kSW = kSWof<DP>, TILE = 16 * (DP + 4);
+__device__ __forceinline__ void store_wave_sums(const float* sm, float* __restrict__ dst, int row0, int T, int D,
+                                                int64_t st, float mul) {
+  constexpr int kSW = kSWof<DP>, TILE = 16 * (DP + 4);
+  for (int e = threadIdx.x; e < 16 * DP; e += kSW * 64) {
+    const int r = e / DP, d = e % DP;
+    const int off = r * (DP + 4) + d;
+    float x = sm[off];
+#pragma unroll
+    for (int w = 1; w < kSW; ++w) x += sm[w * TILE + off];
+    if (row0 + r < T && d < D) dst[(int64_t)(row0 + r) * st + d] = x * mul;
+  }
+}
+
+// A wave's accumulators acc[dt][i] = X[row lq][NDT*(4g+i)+dt] into its LDS tile.
+template <int DP>
+__device__ __forceinline__ void write_wave_part(float* tile, const floatx4 (&acc)[DP / 16], int lq, int g) {
+  constexpr int NDT = DP / 16;
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sm[wave * TILE + lq * (DP + 4) + NDT * (4 * g + i) + dt] = acc[dt][i];
-  }
-  __syncthreads();
-  if (wave == 0) {
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int off = lq * (DP + 4) + NDT * (4 * g + i) + dt;
-        float x = sm[off];
-#pragma unroll
-        for (int w = 1; w < kSW; ++w) x += sm[w * TILE + off];
-        acc[dt][i] = x;
-      }
-    }
+    for (int i = 0; i < 4; ++i) tile[lq * (DP + 4) + NDT * (4 * g + i) + dt] = acc[dt][i];
   }
 }
 
@@ -142,7 +145,7 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
   // the wave's partial output for the merge
   __shared__ __align__(16) float stage[kSW][2][TILE];
   __shared__ __align__(16) float qs[TILE];
-  __shared__ float sm_m[kSW][16], sm_l[kSW][16];
+  __shared__ float sm_m[kSW][16], sm_l[kSW][16], sm_wt[kSW][16], sm_inv[16];
 
   const int BH = L.B * L.H;
   const int n_g = (L.T + 15) / 16;
@@ -237,30 +240,32 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
     for (int i = 0; i < 4; ++i) ks[lq * (DP + 4) + NDT * (4 * g + i) + dt] = oacc[dt][i];
   }
   __syncthreads();
-  if (wave != 0) return;
-  float M = -INFINITY;
+  // per query row: the waves' weights 2^(m_w - M) and 1 / sum, then the whole
+  // block forms the weighted sums, one output element per thread in turn
+  if (tid < 16) {
+    float M = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < kSW; ++w) M = fmaxf(M, sm_m[w][lq]);
-  float wt[kSW], Ls = 0.f;
+    for (int w = 0; w < kSW; ++w) M = fmaxf(M, sm_m[w][tid]);
+    float Ls = 0.f;
 #pragma unroll
-  for (int w = 0; w < kSW; ++w) {
-    wt[w] = fast_exp2(sm_m[w][lq] - M);
-    Ls += wt[w] * sm_l[w][lq];
-  }
-  floatx4 out[NDT];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int off = lq * (DP + 4) + NDT * (4 * g + i) + dt;
-      float acc = 0.f;
-#pragma unroll
-      for (int w = 0; w < kSW; ++w) acc += wt[w] * stage[w][0][off];
-      out[dt][i] = acc;
+    for (int w = 0; w < kSW; ++w) {
+      const float wt = fast_exp2(sm_m[w][tid] - M);
+      sm_wt[w][tid] = wt;
+      Ls += wt * sm_l[w][tid];
     }
+    sm_inv[tid] = 1.f / Ls;
+    const int q = 16 * qg + tid;
+    if (LSE != nullptr && q < L.T) LSE[(int64_t)bh * L.T + q] = (M + log2f(Ls)) * kLn2;
   }
-  store_row_frag<DP, false>(O + base, qrow, L.T, L.D, L.st, g, out, 1.f / Ls);
-  if (LSE != nullptr && g == 0 && qrow < L.T) LSE[(int64_t)bh * L.T + qrow] = (M + log2f(Ls)) * kLn2;
+  __syncthreads();
+  for (int e = tid; e < 16 * DP; e += kSW * 64) {
+    const int r = e / DP, d = e % DP;
+    const int off = r * (DP + 4) + d;
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < kSW; ++w) acc += sm_wt[w][r] * stage[w][0][off];
+    if (16 * qg + r < L.T && d < L.D) O[base + (int64_t)(16 * qg + r) * L.st + d] = acc * sm_inv[r];
+  }
 }
 
 // Key-stationary: a block owns keys 16kg .. 16kg+15 (lane column lq), its
@@ -277,7 +282,7 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_dkv_small_kernel(
     float* __restrict__ dV, float* __restrict__ DS, View L, float scale, float scale_log2) {
   constexpr int DG = DP / 4, NDT = DP / 16, kSW = kSWof<DP>, TILE = 16 * (DP + 4);
   // per wave: its Q, dO and O chunk tiles; after the sweep the space holds the
-  // waves' partial dV, then dK, for the sums
+  // waves' partial dV and dK for the sums
   __shared__ __align__(16) float stage[kSW][3][TILE];
 
   const int BH = L.B * L.H;
@@ -389,13 +394,14 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_dkv_small_kernel(
     wave_lds_sync();  // this chunk's tiles are read before the next one overwrites them
   }
 
-  float* sm = &stage[0][0][0];  // kSW * 3 tiles; the sums use the first kSW
-  __syncthreads();              // every wave is done with its staged chunks
-  sum_over_waves<DP>(sm, dvacc, wave, lq, g);
-  if (wave == 0) store_row_frag<DP, false>(dV + base, krow, L.T, L.D, L.st, g, dvacc, 1.f);
-  __syncthreads();  // wave 0 has read every partial of dV
-  sum_over_waves<DP>(sm, dkacc, wave, lq, g);
-  if (wave == 0) store_row_frag<DP, false>(dK + base, krow, L.T, L.D, L.st, g, dkacc, scale);
+  // the waves' partial dV in tiles 0 .. kSW-1 of the stage space, dK in kSW .. 2kSW-1
+  float* sm = &stage[0][0][0];
+  __syncthreads();  // every wave is done with its staged chunks
+  write_wave_part<DP>(sm + wave * TILE, dvacc, lq, g);
+  write_wave_part<DP>(sm + (kSW + wave) * TILE, dkacc, lq, g);
+  __syncthreads();
+  store_wave_sums<DP>(sm, dV + base, 16 * kg, L.T, L.D, L.st, 1.f);
+  store_wave_sums<DP>(sm + kSW * TILE, dK + base, 16 * kg, L.T, L.D, L.st, scale);
 }
 
 // Query-stationary dQ = scale * dS K: a block owns queries 16qg .. 16qg+15
@@ -453,8 +459,9 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_dq_small_kernel(const
     wave_lds_sync();  // this chunk's tile is read before the next one overwrites it
   }
   __syncthreads();  // every wave is done with its staged chunks
-  sum_over_waves<DP>(&stage[0][0], acc, wave, lq, g);
-  if (wave == 0) store_row_frag<DP, false>(dQ + base, qrow, L.T, L.D, L.st, g, acc, scale);
+  write_wave_part<DP>(stage[wave], acc, lq, g);
+  __syncthreads();
+  store_wave_sums<DP>(&stage[0][0], dQ + base, 16 * qg, L.T, L.D, L.st, scale);
 }
 
 bool small_problem(const View& L) {
