@@ -105,8 +105,10 @@ int wha_attn_bwd(const float* q, const float* k, const float* v,
  * q k^T (same workspace as wha_attn_bwd).  scores: wha_attn_scores_size bytes
  * of device memory, 16-byte aligned, opaque (its layout is internal), valid
  * until the next wha_attn_fwd_keep into it.  When wha_attn_scores_size is 0
- * (head dims outside 48..128 or not a multiple of 4, strides not multiples of
- * 4 floats, or a score buffer above 8 GiB) scores may be NULL and the pair
+ * (head dims outside 36..128 or not a multiple of 4, strides not multiples of
+ * 4 floats, a problem small enough for the split-sweep kernels -- fewer than
+ * 256 64-row tiles over all heads, T <= 1024 -- or a score buffer above
+ * 8 GiB) scores may be NULL and the pair
  * behaves exactly as wha_attn_fwd / wha_attn_bwd.  The pair also runs as
  * wha_attn_fwd / wha_attn_bwd when a tensor is not 16-byte aligned (the
  * forward then leaves scores untouched, and the backward, whose check covers

@@ -241,12 +241,12 @@ def test_scores_size_and_kept_pair_validation(pkg):
     rows = sum(T - 64 * kt for kt in range(T // 64))
     assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(B, H, T, 64))) == B * H * rows * 64 * 4
     assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_seq(B, T, 12, 768))) == B * H * rows * 64 * 4
-    for D in (100, 128, 52, 48):
+    for D in (100, 128, 52, 48, 44, 36):
         assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(8, 16, 100, D))) > 0
         # small problems (fewer than 256 tiles of 64 rows, T <= 1024) run the split-sweep kernels: nothing kept
         assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(2, 2, 100, D))) == 0
     assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(1, 2, 2048, 64))) > 0
-    for D in (44, 42, 16, 50):
+    for D in (32, 42, 16, 50):
         assert L.wha_attn_scores_size(ctypes.byref(pkg.layout_bhtd(8, 16, 100, D))) == 0
     odd = pkg.layout_bhtd(8, 16, 100, 64)
     odd.stride_t = 66

@@ -56,7 +56,7 @@ def guarded_like(torch, dev, shape, fill=None):
 
 # the last two: enough (b,h) heads for the paired block-to-tile mapping at a ragged T (odd tile count)
 RAGGED = [(2, 3, 100, 64), (1, 2, 129, 128), (2, 2, 1000, 64), (1, 2, 77, 48), (2, 2, 65, 42), (1, 1, 200, 56),
-          (1, 2, 33, 100), (8, 12, 900, 64), (8, 12, 900, 48)]
+          (1, 2, 33, 100), (2, 2, 97, 44), (8, 12, 900, 64), (8, 12, 900, 48)]
 
 
 @pytest.mark.parametrize("B,H,T,D", RAGGED)

@@ -52,7 +52,8 @@ def report(tag, got, ref32, ref64=None):
 # 64-row tile kernels, one tile per block; the last one has enough heads for paired tiles at ragged T
 SMALL = [(1, 1, 1, 64), (1, 2, 17, 64), (2, 3, 63, 48), (1, 2, 65, 42), (2, 2, 100, 64),
          (1, 1, 257, 128), (2, 2, 130, 32), (1, 1, 64, 16), (1, 4, 200, 8), (1, 2, 129, 100),
-         (3, 1, 48, 64), (2, 2, 97, 56), (1, 3, 40, 52), (8, 12, 900, 64)]
+         (3, 1, 48, 64), (2, 2, 97, 56), (1, 3, 40, 52), (2, 2, 97, 44), (1, 3, 70, 36), (8, 12, 900, 64),
+         (8, 12, 900, 48)]
 
 
 @pytest.mark.parametrize("wide", [False, True])
@@ -205,7 +206,8 @@ def test_from_probs_matches_reference_contract(pkg, torch_dev):
     Q K^T; masked entries (j > t) hold garbage that must never be read."""
     torch, dev = torch_dev
     rng = np.random.default_rng(0)
-    for (B, H, T, D) in ((2, 3, 100, 64), (1, 4, 96, 42), (1, 2, 257, 128), (1, 2, 130, 56), (1, 1, 70, 100)):
+    for (B, H, T, D) in ((2, 3, 100, 64), (1, 4, 96, 42), (1, 2, 257, 128), (1, 2, 130, 56), (1, 1, 70, 100),
+                         (1, 2, 130, 48), (1, 1, 70, 44)):
         print(f"case from_probs B={B} H={H} T={T} D={D}", flush=True)
         q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=11)
         qs, ks, vs, dos = (oracle.bhtd_to_seq(a) for a in (q, k, v, do))

@@ -500,8 +500,9 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
   store_row_frag<DP, VEC>(dV + base, krow, L.T, L.D, L.st, g, dvacc, 1.f);
 }
 
-// Key-stationary dK/dV (and dS) for head dim 64 with 128-bit-aligned operands:
-// the contractions of attn_bwd_dkv_kernel<64, 4, true, false, DS_OUT>,
+// Key-stationary dK/dV (and dS) for head dims 48, 64 and 128 (and those padded
+// up to them) with 128-bit-aligned operands: the contractions of
+// attn_bwd_dkv_kernel<DP, 4, true, false, DS_OUT>,
 // arranged to keep the MFMA pipe fed.  On gfx950 every VALU instruction a SIMD
 // issues costs MFMA issue time (an fp32 MFMA and a VALU op do not overlap), so
 // the loop is built to need as little VALU work as possible:
@@ -518,8 +519,9 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
 //     and dP accumulators, so P = exp2(S) and dS = P * dP;
 //   - masking runs only on sub-tiles that touch the diagonal or the end of the
 //     sequence (a wave-uniform test);
-//   - Q and dO sit in the swizzled Lds<64> layout (a DMA instruction fills four
-//     unpadded rows; lane l fetches the logical quad that belongs at position l);
+//   - Q and dO sit in the swizzled Lds<DP> layout (a DMA instruction fills 64
+//     quads of unpadded rows; lane l fetches the logical quad that belongs at
+//     position l);
 //   - each accumulator is one dependent MFMA chain (back-to-back accumulation
 //     into the same registers issues at full rate), so S and dP of a sub-tile
 //     take 8 registers each.
@@ -538,9 +540,9 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
 // no exponential, rows and columns clamped into the tensor (those entries are
 // masked), entries after the diagonal never used unmasked; the stats blocks
 // then hold only -Delta (the Delta pass, launch_probs_delta_dma).
-// three blocks per CU at head dim 64, two at 128 (LDS and VGPR budgets)
+// three blocks per CU at head dims 48 and 64, two at 128 (LDS and VGPR budgets)
 #ifndef WHA_DMA_WPE
-#define WHA_DMA_WPE(DP) __attribute__((amdgpu_waves_per_eu((DP) == 64 ? 3 : 2)))
+#define WHA_DMA_WPE(DP) __attribute__((amdgpu_waves_per_eu((DP) <= 64 ? 3 : 2)))
 #endif
 template <int DP, bool DS_OUT, bool PADQ, bool SAVED, bool PROBS = false>
 __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
@@ -552,9 +554,14 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
   constexpr int QPR = DP / 4;            // quads per row
   constexpr int BSUB = 32;               // queries per sub-tile
   constexpr int TILE = BSUB * DP;        // floats per operand sub-tile
-  constexpr int NF = BSUB * QPR / 256;   // DMA instructions per wave per operand
+  // 64-quad DMA chunks per operand sub-tile: 8 or 16 (each wave fetches a
+  // quarter of Q and of dO) or, at DP = 48, 6 (waves 0-1 fetch Q, waves 2-3 dO,
+  // three each)
+  constexpr int CH = BSUB * QPR / 64;
+  constexpr bool SPLIT = CH == 6;
+  constexpr int NF = SPLIT ? 3 : CH / 4;  // chunks per wave and operand it fetches
   using LT = Lds<DP, true>;
-  static_assert(LT::SWZ, "the DMA layout is the swizzled unpadded row");
+  static_assert(LT::SWZ && (SPLIT || CH % 4 == 0), "the DMA layout is the swizzled unpadded row");
   __shared__ __align__(16) float Qs0[TILE], Qs1[TILE];
   __shared__ __align__(16) float Os0[TILE], Os1[TILE];
   __shared__ __align__(16) float St0[2 * BSUB], St1[2 * BSUB];
@@ -575,19 +582,22 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
   const int wave = tid >> 6, lane = tid & 63;
   const int lq = lane & 15, g = lane >> 4;
 
-  // This lane's fetch: wave w fills LDS quads 64(NF*w+u) .. +63 of both
-  // operands (u < NF): quad p = 64(NF*w+u) + lane is row p / QPR of the
-  // sub-tile, position p % QPR, which holds logical quad (p % QPR) ^ swz(row).
-  // Byte offsets from the sub-tile's first row; the last sub-tile clamps rows
-  // to T-1.
+  // This lane's fetch: wave w fills LDS chunk ch(u) = NF*w+u of both operands
+  // (u < NF), or at DP = 48 chunk 3(w&1)+u (u < 3) of Q (w < 2) or of dO
+  // (w >= 2): quad p = 64 ch + lane is row p / QPR of the sub-tile, stored
+  // position p % QPR, which holds logical quad pq(row, p % QPR).  Byte offsets
+  // from the sub-tile's first row; the last sub-tile clamps rows to T-1.
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const bool o_half = SPLIT && wv >= 2;  // wave-uniform: this wave fetches dO
+  auto chunk = [&](int u) { return SPLIT ? 3 * (wv & 1) + u : NF * wv + u; };
   int rrow[NF], rcol[NF];
   uint32_t roff[NF];
   bool pad[NF];  // PADQ: this lane's quad lies past the head dim (fetched from g_zero_quad)
 #pragma unroll
   for (int u = 0; u < NF; ++u) {
-    const int p = 64 * (NF * wave + u) + lane;
+    const int p = 64 * chunk(u) + lane;
     rrow[u] = p / QPR;
-    rcol[u] = (p % QPR) ^ LT::swz(rrow[u]);
+    rcol[u] = LT::pq(rrow[u], p % QPR);
     pad[u] = PADQ && 4 * rcol[u] >= L.D;
     roff[u] = (uint32_t)(rrow[u] * L.st + 4 * rcol[u]) * 4u;
   }
@@ -602,13 +612,24 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
 #pragma unroll
       for (int u = 0; u < NF; ++u) off[u] = (uint32_t)((min(q0 + rrow[u], L.T - 1) - q0) * L.st + 4 * rcol[u]) * 4u;
     }
+    if constexpr (SPLIT) {
+      const char* src = o_half ? os : qs;
+      float* dst = o_half ? Od : Qd;
 #pragma unroll
-    for (int u = 0; u < NF; ++u) {
-      const float* qp = reinterpret_cast<const float*>(qs + off[u]);
-      const float* op = reinterpret_cast<const float*>(os + off[u]);
-      if (PADQ && pad[u]) qp = op = g_zero_quad;
-      dma_quad(qp, Qd + 256 * (NF * wave + u));
-      dma_quad(op, Od + 256 * (NF * wave + u));
+      for (int u = 0; u < NF; ++u) {
+        const float* sp = reinterpret_cast<const float*>(src + off[u]);
+        if (PADQ && pad[u]) sp = g_zero_quad;
+        dma_quad(sp, dst + 256 * chunk(u));
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < NF; ++u) {
+        const float* qp = reinterpret_cast<const float*>(qs + off[u]);
+        const float* op = reinterpret_cast<const float*>(os + off[u]);
+        if (PADQ && pad[u]) qp = op = g_zero_quad;
+        dma_quad(qp, Qd + 256 * chunk(u));
+        dma_quad(op, Od + 256 * chunk(u));
+      }
     }
     if (wave == 0) dma_dword(stg + st * 64 + lane, Sd);
   };
@@ -777,10 +798,11 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
   }
 }
 
-// dQ = scale * dS K for head dim 64 with 128-bit-aligned operands, written for
-// few VALU instructions per MFMA like attn_bwd_dkv_dma_kernel:
+// dQ = scale * dS K for head dims 48, 64 and 128 (and those padded up to them)
+// with 128-bit-aligned operands, written for few VALU instructions per MFMA
+// like attn_bwd_dkv_dma_kernel:
 //   - 64-key K tiles go from global memory straight into LDS (global_load_lds,
-//     swizzled Lds<64> layout, two slots in separate arrays, loop unrolled by
+//     swizzled Lds<DP> layout, two slots in separate arrays, loop unrolled by
 //     two, one barrier per tile);
 //   - a lane's 16 dS values of the next tile come as four 128-bit loads from
 //     one address (dS rows sit at 256-byte pitch), straight into the MFMA B
@@ -801,6 +823,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __res
   constexpr int QPR = DP / 4;            // quads per row
   constexpr int TILE = BN * DP;
   constexpr int NF = BN * QPR / 256;     // DMA instructions per wave per tile
+  static_assert(BN * QPR % 256 == 0, "a K tile is a whole number of DMA instructions per wave");
   using LT = Lds<DP, true>;
   __shared__ __align__(16) float Ks0[TILE], Ks1[TILE];
 
@@ -818,8 +841,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __res
   const int lq = lane & 15, g = lane >> 4;
 
   // this lane's part of a K tile fetch: wave w fills LDS quads 64(NF*w+u) ..
-  // +63 (u < NF): quad p = 64(NF*w+u) + lane is row p / QPR, position p % QPR
-  // <- logical quad (p % QPR) ^ swz(row); byte offsets from the tile's first row
+  // +63 (u < NF): quad p = 64(NF*w+u) + lane is row p / QPR, stored position
+  // p % QPR <- logical quad pq(row, p % QPR); byte offsets from the tile's first row
   int krow_[NF], kcol[NF];
   uint32_t koff[NF];
   bool pad[NF];  // PADQ: this lane's quad lies past the head dim (fetched from g_zero_quad)
@@ -827,7 +850,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __res
   for (int u = 0; u < NF; ++u) {
     const int p = 64 * (NF * wave + u) + lane;
     krow_[u] = p / QPR;
-    kcol[u] = (p % QPR) ^ LT::swz(krow_[u]);
+    kcol[u] = LT::pq(krow_[u], p % QPR);
     pad[u] = PADQ && 4 * kcol[u] >= L.D;
     koff[u] = (uint32_t)(krow_[u] * L.st + 4 * kcol[u]) * 4u;
   }
@@ -1183,6 +1206,8 @@ hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const
   if (sc == nullptr && ds != nullptr && small_problem(L))
     return launch_attn_bwd_small(q, k, v, o, d_o, lse, dq, dk, dv, ds, L, scale, stream);
   if (WHA_DKV_DMA && ds != nullptr && vec && (sc != nullptr ? kept_head_dim(L.D) : dma_head_dim(L.D))) {
+    if (L.D == 48) return bwd_dma_t<48, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
+    if (L.D < 48) return bwd_dma_t<48, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
     if (L.D == 64) return bwd_dma_t<64, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
     if (L.D < 64) return bwd_dma_t<64, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
     if (L.D == 128) return bwd_dma_t<128, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
@@ -1241,6 +1266,8 @@ hipError_t launch_attn_bwd_probs(const float* d_o, const float* q, const float* 
 #define WHA_BWDP_DMA(DP, PADQ)                                                                                \
   return av ? bwd_probs_dma_t<DP, PADQ, true>(d_o, q, k, v, att, dq, dk, dv, delta, stats, ds, L, scale, stream) \
             : bwd_probs_dma_t<DP, PADQ, false>(d_o, q, k, v, att, dq, dk, dv, delta, stats, ds, L, scale, stream)
+    if (L.D == 48) WHA_BWDP_DMA(48, false);
+    if (L.D < 48) WHA_BWDP_DMA(48, true);
     if (L.D == 64) WHA_BWDP_DMA(64, false);
     if (L.D < 64) WHA_BWDP_DMA(64, true);
     if (L.D == 128) WHA_BWDP_DMA(128, false);

@@ -165,13 +165,14 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
     LSE[(int64_t)bh * L.T + qrow] = (m_i + log2f(l_sum)) * kLn2;
 }
 
-// Forward for head dims 52..64 and 68..128 (128-bit-aligned operands), arranged like the
-// backward's direct-to-LDS kernels because on gfx950 every VALU instruction
-// costs MFMA issue time:
-//   - 32-key sub-tiles of K and V go from global memory straight into LDS
-//     (global_load_lds, swizzled Lds<64> layout, two slots in separate arrays,
-//     loop unrolled by two, one barrier per sub-tile, per-lane fetch offsets
-//     computed once);
+// Forward for head dims 36..128 (multiples of 4, 128-bit-aligned operands; 48,
+// 64 and 128 exact, others padded up to them), arranged like the backward's
+// direct-to-LDS kernels because on gfx950 every VALU instruction costs MFMA
+// issue time:
+//   - 32-key sub-tiles of K and V (16-key at DP = 128) go from global memory
+//     straight into LDS (global_load_lds, swizzled Lds<DP> layout, two slots
+//     in separate arrays, loop unrolled by two, one barrier per sub-tile,
+//     per-lane fetch offsets computed once);
 //   - masking runs only on sub-tiles that reach past a query of the wave or
 //     past T (a wave-uniform test, separate code);
 //   - the running max is refreshed, and O and the row sum rescaled, only when
@@ -208,13 +209,17 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
                                                                      int unpaired, float scale_log2,
                                                                      const float* __restrict__ ATT = nullptr) {
   constexpr int DG = DP / 4, NDT = DP / 16;
-  constexpr int QPR = DP / 4;            // quads per row
-  constexpr int BSUB = 2048 / DP;        // keys per sub-tile (8 KB per operand)
-  constexpr int NKT = BSUB / 16;         // 16-key groups per sub-tile
-  constexpr int TILE = BSUB * DP;        // floats per operand sub-tile
-  constexpr int NF = BSUB * QPR / 256;   // DMA instructions per wave per operand
+  constexpr int QPR = DP / 4;                      // quads per row
+  constexpr int BSUB = DP == 48 ? 32 : 2048 / DP;  // keys per sub-tile (8 KB per operand; 6 KB at 48)
+  constexpr int NKT = BSUB / 16;                   // 16-key groups per sub-tile
+  constexpr int TILE = BSUB * DP;                  // floats per operand sub-tile
+  // 64-quad DMA chunks per operand sub-tile: 8 (each wave fetches two of K
+  // and two of V) or, at DP = 48, 6 (waves 0-1 fetch K, waves 2-3 V, three each)
+  constexpr int CH = BSUB * QPR / 64;
+  constexpr bool SPLIT = CH == 6;
+  constexpr int NU = SPLIT ? 3 : 2;                // chunks per wave and operand it fetches
   using LT = Lds<DP, true>;
-  static_assert(NF == 2 && LT::SWZ, "sub-tiles of 512 quads in the swizzled unpadded layout");
+  static_assert((CH == 8 || SPLIT) && LT::SWZ, "sub-tiles of 512 or 384 quads in the swizzled unpadded layout");
   __shared__ __align__(16) float Ks0[TILE], Ks1[TILE];
   __shared__ __align__(16) float Vs0[TILE], Vs1[TILE];
 
@@ -232,17 +237,21 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
   const int wave = tid >> 6, lane = tid & 63;
   const int lq = lane & 15, g = lane >> 4;
 
-  // this lane's fetch: wave w fills LDS quads 64(2w+u) .. +63 of K and V
-  // (u = 0, 1): quad p = 64(2w+u) + lane is row p / QPR, position p % QPR <-
-  // logical quad (p % QPR) ^ swz(row); byte offsets from the sub-tile's first row
-  int rrow[2], rcol[2];
-  uint32_t roff[2];
-  bool pad[2];  // PADQ: this lane's quad lies past the head dim (fetched from g_zero_quad)
+  // this lane's fetch: wave w fills LDS chunk ch(u) = 2w+u of K and V (u < 2),
+  // or at DP = 48 chunk 3(w&1)+u (u < 3) of K (w < 2) or of V (w >= 2): quad
+  // p = 64 ch + lane is row p / QPR, stored position p % QPR <- logical quad
+  // pq(row, p % QPR); byte offsets from the sub-tile's first row
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const bool v_half = SPLIT && wv >= 2;  // wave-uniform: this wave fetches V
+  int rrow[NU], rcol[NU];
+  uint32_t roff[NU];
+  bool pad[NU];  // PADQ: this lane's quad lies past the head dim (fetched from g_zero_quad)
+  auto chunk = [&](int u) { return SPLIT ? 3 * (wv & 1) + u : 2 * wv + u; };
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int p = 64 * (2 * wave + u) + lane;
+  for (int u = 0; u < NU; ++u) {
+    const int p = 64 * chunk(u) + lane;
     rrow[u] = p / QPR;
-    rcol[u] = (p % QPR) ^ LT::swz(rrow[u]);
+    rcol[u] = LT::pq(rrow[u], p % QPR);
     pad[u] = PADQ && 4 * rcol[u] >= L.D;
     roff[u] = (uint32_t)(rrow[u] * L.st + 4 * rcol[u]) * 4u;
   }
@@ -250,19 +259,33 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
     const int k0 = st * BSUB;
     const char* ks = kg + st * sub_bytes;
     const char* vs = vg + st * sub_bytes;
-    uint32_t off[2] = {roff[0], roff[1]};
+    uint32_t off[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) off[u] = roff[u];
     if (k0 + BSUB > L.T) {  // last sub-tile: rows past T read row T-1
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < NU; ++u)
         off[u] = (uint32_t)((min(k0 + rrow[u], L.T - 1) - k0) * L.st + 4 * rcol[u]) * 4u;
     }
+    if constexpr (SPLIT) {
+      if (DELTA && v_half) return;  // the Delta pass reads no V
+      const char* src = v_half ? vs : ks;
+      float* dst = v_half ? Vd : Kd;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const float* kp = reinterpret_cast<const float*>(ks + off[u]);
-      const float* vp = reinterpret_cast<const float*>(vs + off[u]);
-      if (PADQ && pad[u]) kp = vp = g_zero_quad;
-      dma_quad(kp, Kd + 256 * (2 * wave + u));
-      if constexpr (!DELTA) dma_quad(vp, Vd + 256 * (2 * wave + u));
+      for (int u = 0; u < NU; ++u) {
+        const float* sp = reinterpret_cast<const float*>(src + off[u]);
+        if (PADQ && pad[u]) sp = g_zero_quad;
+        dma_quad(sp, dst + 256 * chunk(u));
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const float* kp = reinterpret_cast<const float*>(ks + off[u]);
+        const float* vp = reinterpret_cast<const float*>(vs + off[u]);
+        if (PADQ && pad[u]) kp = vp = g_zero_quad;
+        dma_quad(kp, Kd + 256 * chunk(u));
+        if constexpr (!DELTA) dma_quad(vp, Vd + 256 * chunk(u));
+      }
     }
   };
 
@@ -504,7 +527,11 @@ hipError_t launch_probs_delta_dma(const float* d_o, const float* v, const float*
 #define WHA_PD(DP, PADQ)                                                 \
   (av ? probs_delta_t<DP, PADQ, true>(d_o, v, att, stats, L, stream)   \
       : probs_delta_t<DP, PADQ, false>(d_o, v, att, stats, L, stream))
-  if (L.D == 64)
+  if (L.D == 48)
+    WHA_PD(48, false);
+  else if (L.D < 48)
+    WHA_PD(48, true);
+  else if (L.D == 64)
     WHA_PD(64, false);
   else if (L.D < 64)
     WHA_PD(64, true);
@@ -523,7 +550,11 @@ hipError_t launch_attn_fwd(const float* q, const float* k, const float* v, float
   if (WHA_FWD_DMA && vec && (scores != nullptr ? kept_head_dim(L.D) : dma_head_dim(L.D))) {
     const float scale_log2 = (float)((double)scale * 1.4426950408889634);
     TimingScope ts("attn_fwd", stream);
-    if (L.D == 64)
+    if (L.D == 48)
+      fwd_dma_t<48, false>(q, k, v, o, lse, scores, L, scale_log2, stream);
+    else if (L.D < 48)
+      fwd_dma_t<48, true>(q, k, v, o, lse, scores, L, scale_log2, stream);
+    else if (L.D == 64)
       fwd_dma_t<64, false>(q, k, v, o, lse, scores, L, scale_log2, stream);
     else if (L.D < 64)
       fwd_dma_t<64, true>(q, k, v, o, lse, scores, L, scale_log2, stream);

@@ -140,20 +140,31 @@ __device__ __forceinline__ float pair_sum32(float x) {
 // probe: a padded pitch such as DP+4 leaves both read patterns 2-way
 // conflicted).  For DP = 64 rows are unpadded and quad c of row r is stored at
 // quad c ^ (r & 11), which keeps all three patterns conflict-free for every
-// lane grouping consistent with the probe; DP = 128 uses the XOR in swz().  Kernels opt in (ALLOW_SWZ): the
-// XOR costs per-lane address registers, which only pays where LDS traffic
-// matters more than VGPRs.  Other DP, and kernels that do not opt in, keep a
-// 4-float pad.
+// lane grouping consistent with the probe; DP = 128 uses the XOR in swz().
+// DP = 48 rows (12 quads) are unpadded too, with rows 4..7 of every 16 rotated
+// by half a row (quad c at (c + 6) mod 12 when r & 4): the rows-by-lane reads
+// (quads 3g + j) stay conflict-free for every such lane grouping, and the
+// contractions over rows read single floats d = 16dt + lq (lds_read_seg), 32
+// lanes of which always hit 32 different banks.  Kernels opt in (ALLOW_SWZ):
+// the permutation costs per-lane address registers, which only pays where LDS
+// traffic matters more than VGPRs.  Other DP, and kernels that do not opt in,
+// keep a 4-float pad.
 template <int DP, bool ALLOW_SWZ = false>
 struct Lds {
-  static constexpr bool SWZ = WHA_LDS_SWZ && ALLOW_SWZ && (DP == 64 || DP == 128);
+  static constexpr bool SWZ = WHA_LDS_SWZ && ALLOW_SWZ && (DP == 48 || DP == 64 || DP == 128);
   static constexpr int PITCH = SWZ ? DP : DP + WHA_LDS_PAD;
   // XOR applied to the quad index of row r (128-float rows: rows by lane read
   // quads 8g + j, and the contractions over rows read quads lq and lq + 16 --
   // see lds_read_seg -- which r & 11 does not keep apart)
   __device__ __forceinline__ static int swz(int r) { return DP == 64 ? (r & 11) : ((r & 3) | ((r >> 1) & 4)); }
+  // stored position of quad c in row r (an involution in c: it also maps a
+  // stored position back to its quad)
+  __device__ __forceinline__ static int pq(int r, int c) {
+    if constexpr (DP == 48) return (r & 4) ? (c < 6 ? c + 6 : c - 6) : c;
+    else return c ^ swz(r);
+  }
   // float offset of quad c of row r
-  __device__ __forceinline__ static int at(int r, int c) { return r * PITCH + 4 * (SWZ ? (c ^ swz(r)) : c); }
+  __device__ __forceinline__ static int at(int r, int c) { return r * PITCH + 4 * (SWZ ? pq(r, c) : c); }
   // float offset of head-dim entry d of row r (a quad-aligned group of N <= 4
   // entries starting at d stays contiguous)
   __device__ __forceinline__ static int at_d(int r, int d) { return SWZ ? at(r, d >> 2) + (d & 3) : r * PITCH + d; }
@@ -232,18 +243,19 @@ struct TileStage {
 
 // Reads N head-dim entries of row r of an Lds<DP, SW> tile for lane lq: the
 // entries [N*lq, N*lq + N) (padded tiles, and swizzled 64-wide tiles where
-// N = 4), or for swizzled 128-wide tiles quads lq and lq + 16 (d = 4lq..4lq+3
-// and 64+4lq..64+4lq+3), the split layout store_row_frag_split writes back.
+// N = 4), for swizzled 128-wide tiles quads lq and lq + 16 (d = 4lq..4lq+3
+// and 64+4lq..64+4lq+3), or for swizzled 48-wide tiles d = lq, 16+lq, 32+lq
+// (three 32-bit reads): the split layouts store_row_frag_split writes back.
 template <int DP, int N, bool SW = false>
 __device__ __forceinline__ void lds_read_seg(const float* tile, int r, int lq, float* out) {
   using LT = Lds<DP, SW>;
-  if (LT::SWZ && N == 4) {
+  if constexpr (LT::SWZ && N == 4) {
     const float4 v = *reinterpret_cast<const float4*>(tile + LT::at(r, lq));
     out[0] = v.x;
     out[1] = v.y;
     out[2] = v.z;
     out[3] = v.w;
-  } else if (LT::SWZ && N == 8) {
+  } else if constexpr (LT::SWZ && N == 8) {
     const float4 v = *reinterpret_cast<const float4*>(tile + LT::at(r, lq));
     const float4 w = *reinterpret_cast<const float4*>(tile + LT::at(r, lq + 16));
     out[0] = v.x;
@@ -254,8 +266,11 @@ __device__ __forceinline__ void lds_read_seg(const float* tile, int r, int lq, f
     out[5] = w.y;
     out[6] = w.z;
     out[7] = w.w;
+  } else if constexpr (LT::SWZ && DP == 48 && N == 3) {
+#pragma unroll
+    for (int dt = 0; dt < 3; ++dt) out[dt] = tile[LT::at_d(r, 16 * dt + lq)];
   } else {
-    static_assert(!LT::SWZ || N == 4 || N == 8, "swizzled tiles are read in whole quads");
+    static_assert(!LT::SWZ, "swizzled tiles are read in whole quads, or as d = 16dt + lq at DP = 48");
     const float* p = tile + r * LT::PITCH + N * lq;
     if (N % 4 == 0) {
 #pragma unroll
@@ -399,7 +414,8 @@ __device__ __forceinline__ void store_row_frag(float* __restrict__ base, int row
 // with lds_read_seg<DP, NDT, true> (swizzled tiles): for DP = 64 the layout of
 // store_row_frag; for DP = 128 d-tile dt < 4 holds d = 4m + dt and dt >= 4
 // holds d = 64 + 4m + dt - 4 (m = MFMA row), so lane (lq, g) stores quads
-// 4g+i and 16+4g+i of row `row`.  128-bit stores, columns >= D skipped.
+// 4g+i and 16+4g+i of row `row`; for DP = 48 d-tile dt holds d = 16dt + m, so
+// the lane stores quads 4dt+g.  128-bit stores, columns >= D skipped.
 template <int DP>
 __device__ __forceinline__ void store_row_frag_split(float* __restrict__ base, int row, int T, int D, int64_t st,
                                                      int g, const floatx4* acc, float mul) {
@@ -409,6 +425,16 @@ __device__ __forceinline__ void store_row_frag_split(float* __restrict__ base, i
   }
   if (row >= T) return;
   float* dst = base + (int64_t)row * st;
+  if (DP == 48) {
+#pragma unroll
+    for (int dt = 0; dt < 3; ++dt) {
+      const int c = 16 * dt + 4 * g;
+      if (c < D)
+        *reinterpret_cast<float4*>(dst + c) =
+            make_float4(acc[dt][0] * mul, acc[dt][1] * mul, acc[dt][2] * mul, acc[dt][3] * mul);
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll

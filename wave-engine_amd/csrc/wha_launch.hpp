@@ -23,19 +23,14 @@ inline int padded_dim(int D) {
   return 0;
 }
 
-// Head dims the direct-to-LDS kernels serve (with 128-bit operands): 64 and
-// 128, and 52..60 / 68..124 on the 64- / 128-wide kernels with the LDS quads
-// past D fetched as zeros (those pad the same way in the register-staged
-// kernels).  48 keeps its exact 48-wide kernels: padded to 64 here it needs a
-// third more MFMA work, which cancels the gain (measured on the 384-dim
-// config: 0.167 vs 0.164 ms per step).
-inline bool dma_head_dim(int D) { return D % 4 == 0 && D > 48 && D <= 128; }
+// Head dims the direct-to-LDS kernels serve (with 128-bit operands): 48, 64
+// and 128, and 36..44 / 52..60 / 68..124 on the 48- / 64- / 128-wide kernels
+// with the LDS quads past D fetched as zeros (those pad the same way in the
+// register-staged kernels).
+inline bool dma_head_dim(int D) { return D % 4 == 0 && D > 32 && D <= 128; }
 
-// Head dims of the kept-scores pair: the above and 48 (padded to 64).  With the
-// scores kept the padded dK/dV kernel skips the Q K^T recompute, which makes
-// the pair faster than the exact 48-wide kernels (384-dim config: 0.154 vs
-// 0.164 ms per step).
-inline bool kept_head_dim(int D) { return D % 4 == 0 && D >= 48 && D <= 128; }
+// Head dims of the kept-scores pair: the same.
+inline bool kept_head_dim(int D) { return dma_head_dim(D); }
 
 // Small problems -- fewer than kSmallBlocks 64-row tiles over all (b,h) heads
 // and rows of at most kSmallMaxT -- run the 16-row split-sweep kernels of
