@@ -562,6 +562,8 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
   constexpr int NF = SPLIT ? 3 : CH / 4;  // chunks per wave and operand it fetches
   using LT = Lds<DP, true>;
   static_assert(LT::SWZ && (SPLIT || CH % 4 == 0), "the DMA layout is the swizzled unpadded row");
+  // MFMA A-operand row m <-> query row arow(m) of a 16-row group (dma48_row)
+  auto arow = [](int m) { return dma48_row<DP>(m); };
   __shared__ __align__(16) float Qs0[TILE], Qs1[TILE];
   __shared__ __align__(16) float Os0[TILE], Os1[TILE];
   __shared__ __align__(16) float St0[2 * BSUB], St1[2 * BSUB];
@@ -631,7 +633,8 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
         dma_quad(op, Od + 256 * chunk(u));
       }
     }
-    if (wave == 0) dma_dword(stg + st * 64 + lane, Sd);
+    // stats position 16a + 4g + i holds the row 16a + arow(4g+i) (floatx4 reads below)
+    if (wave == 0) dma_dword(stg + st * 64 + arow(lane), Sd);
   };
 
   // key tiles pair and n_kt-1-pair: every block does n_kt+1 tiles of work.
@@ -646,8 +649,8 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
     const int k0w = kt * 64 + wave * 16;
     const int krow = k0w + lq;
     float kf[SAVED ? 1 : DG], vf[DG];
-    if constexpr (!SAVED) load_row_frag<DP, true>(K + base, krow, L.T, L.D, L.st, g, scale_log2, kf);
-    load_row_frag<DP, true>(V + base, krow, L.T, L.D, L.st, g, 1.f, vf);
+    if constexpr (!SAVED) load_row_frag_dma<DP>(K + base, krow, L.T, L.D, L.st, g, scale_log2, kf);
+    load_row_frag_dma<DP>(V + base, krow, L.T, L.D, L.st, g, 1.f, vf);
     floatx4 dkacc[NDT], dvacc[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
@@ -655,9 +658,12 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
       dvacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
     const int q_end = krow < L.T ? L.T : 0;  // valid queries: krow <= q < q_end
-    const int64_t kcol = ((int64_t)bh * ds_rows(L.T) + ds_block_row(kt, L.T) - (int64_t)64 * kt) * 64 + wave * 16 + lq;
+    // this lane's key column of the dS and score layouts (key 16w + lq; at
+    // DP = 48 the keys of each 16-column group sit in tr16 order)
+    const int64_t kcol = ((int64_t)bh * ds_rows(L.T) + ds_block_row(kt, L.T) - (int64_t)64 * kt) * 64 + wave * 16 +
+                         arow(lq);
     float* dsw = DS_OUT ? DS + kcol : nullptr;
-    // SAVED: a lane's scores of sub-tile st (rows 32st+16mt+4g+i, this lane's key)
+    // SAVED: a lane's scores of sub-tile st (rows 32st+16mt+arow(4g+i), this lane's key)
     auto load_sc = [&](int st, float (&dst)[8]) {
       if constexpr (PROBS) {
         const float* src = SC + (int64_t)bh * L.T * L.T + min(krow, L.T - 1);
@@ -665,14 +671,14 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
         for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            dst[4 * mt + i] = src[(int64_t)min(st * BSUB + 16 * mt + 4 * g + i, L.T - 1) * L.T];
+            dst[4 * mt + i] = src[(int64_t)min(st * BSUB + 16 * mt + arow(4 * g + i), L.T - 1) * L.T];
         }
       } else {
-        const float* src = SC + kcol + (int64_t)(st * BSUB + 4 * g) * 64;
+        const float* src = SC + kcol + (int64_t)(st * BSUB) * 64;
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) dst[4 * mt + i] = src[(16 * mt + i) * 64];
+          for (int i = 0; i < 4; ++i) dst[4 * mt + i] = src[(16 * mt + arow(4 * g + i)) * 64];
         }
       }
     };
@@ -693,13 +699,13 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
 #pragma unroll
         for (int j = 0; j < DG / 4; ++j) {
           if constexpr (!SAVED) {
-            const float4 a = lds_read_quad<DP, true>(Qs, 16 * mt + lq, (DG / 4) * g + j);
+            const float4 a = lds_read_quad<DP, true>(Qs, 16 * mt + arow(lq), dma48_quad<DP>(g, j));
             s[mt] = mfma4(a.x, kf[4 * j + 0], s[mt]);
             s[mt] = mfma4(a.y, kf[4 * j + 1], s[mt]);
             s[mt] = mfma4(a.z, kf[4 * j + 2], s[mt]);
             s[mt] = mfma4(a.w, kf[4 * j + 3], s[mt]);
           }
-          const float4 c = lds_read_quad<DP, true>(Os, 16 * mt + lq, (DG / 4) * g + j);
+          const float4 c = lds_read_quad<DP, true>(Os, 16 * mt + arow(lq), dma48_quad<DP>(g, j));
           dp[mt] = mfma4(c.x, vf[4 * j + 0], dp[mt]);
           dp[mt] = mfma4(c.y, vf[4 * j + 1], dp[mt]);
           dp[mt] = mfma4(c.z, vf[4 * j + 2], dp[mt]);
@@ -714,14 +720,14 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
           for (int i = 0; i < 4; ++i) s[mt][i] = PROBS ? sc[4 * mt + i] : s[mt][i] + sc[4 * mt + i];
         }
       }
-      // lane element (mt,i): query qb+16mt+4g+i, key krow
+      // lane element (mt,i): query qb+16mt+arow(4g+i), key krow
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float p = PROBS ? s[mt][i] : fast_exp2(s[mt][i]);
           if (MASKED) {
-            const int q = qb + 16 * mt + 4 * g + i;
+            const int q = qb + 16 * mt + arow(4 * g + i);
             const bool valid = (q >= krow) & (q < q_end);
             s[mt][i] = valid ? p : 0.f;
             dp[mt][i] = valid ? p * dp[mt][i] : 0.f;
@@ -733,11 +739,11 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
       }
 
       if (DS_OUT) {
-        float* dsq = dsw + (int64_t)(qb + 4 * g) * 64;
+        float* dsq = dsw + (int64_t)qb * 64;
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) dsq[(16 * mt + i) * 64] = dp[mt][i];
+          for (int i = 0; i < 4; ++i) dsq[(16 * mt + arow(4 * g + i)) * 64] = dp[mt][i];
         }
       }
 
@@ -748,8 +754,8 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float oa[NDT], qa[NDT];
-          lds_read_seg<DP, NDT, true>(Os, 16 * mt + 4 * g + i, lq, oa);
-          lds_read_seg<DP, NDT, true>(Qs, 16 * mt + 4 * g + i, lq, qa);
+          lds_read_seg<DP, NDT, true>(Os, 16 * mt + arow(4 * g + i), lq, oa);
+          lds_read_seg<DP, NDT, true>(Qs, 16 * mt + arow(4 * g + i), lq, qa);
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt) {
             dvacc[dt] = mfma4(oa[dt], s[mt][i], dvacc[dt]);
@@ -806,7 +812,9 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
 //     two, one barrier per tile);
 //   - a lane's 16 dS values of the next tile come as four 128-bit loads from
 //     one address (dS rows sit at 256-byte pitch), straight into the MFMA B
-//     operand (k-step (c, e) <-> key 16c + 4g + e);
+//     operand (k-step (c, e) <-> column 16c + 4g + e, which holds key
+//     16c + dma48_row(4g + e): the dK/dV kernel writes the keys of each
+//     16-column group in tr16 order at DP = 48);
 //   - one dependent accumulator chain per d-tile; 16-key chunks that lie after
 //     every query of the wave are skipped (only in the diagonal tile, a
 //     wave-uniform test).  Every dS entry read there was written by the
@@ -884,7 +892,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __res
     const int q0 = qt * 64 + wave * 16;
     const int qrow = q0 + lq;
     const int n_kt = qt + 1;
-    // dS of key tile kt for this lane: row qrow of column block kt, keys 16c + 4g .. +3
+    // dS of key tile kt for this lane: row qrow of column block kt, columns 16c + 4g .. +3
     auto load_ds = [&](int kt, float4* dsv) {
       const float* src = dsh + (ds_block_row(kt, L.T) + qrow - 64 * kt) * 64 + 4 * g;
 #pragma unroll
@@ -913,7 +921,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __res
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             float ka[NDT];
-            lds_read_seg<DP, NDT, true>(Ks, 16 * c + 4 * g + e, lq, ka);
+            lds_read_seg<DP, NDT, true>(Ks, 16 * c + dma48_row<DP>(4 * g + e), lq, ka);
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma4(ka[dt], dv[e], acc[dt]);
           }
@@ -928,7 +936,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __res
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             float ka[NDT];
-            lds_read_seg<DP, NDT, true>(Ks, 16 * c + 4 * g + e, lq, ka);
+            lds_read_seg<DP, NDT, true>(Ks, 16 * c + dma48_row<DP>(4 * g + e), lq, ka);
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma4(ka[dt], dv[e], acc[dt]);
           }

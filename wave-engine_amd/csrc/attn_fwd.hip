@@ -220,6 +220,9 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
   constexpr int NU = SPLIT ? 3 : 2;                // chunks per wave and operand it fetches
   using LT = Lds<DP, true>;
   static_assert((CH == 8 || SPLIT) && LT::SWZ, "sub-tiles of 512 or 384 quads in the swizzled unpadded layout");
+  // MFMA A-operand row m <-> tile row arow(m) (dma48_row; the Delta pass keeps
+  // rows in order: its att loads want four consecutive keys per lane)
+  auto arow = [](int m) { return DELTA ? m : dma48_row<DP>(m); };
   __shared__ __align__(16) float Ks0[TILE], Ks1[TILE];
   __shared__ __align__(16) float Vs0[TILE], Vs1[TILE];
 
@@ -301,7 +304,7 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
     const int q0 = qt * 64 + wave * 16;                  // first query of this wave
     const int qrow = q0 + lq;                            // this lane's query
     float qf[DG];
-    load_row_frag<DP, true>(Q + base, qrow, L.T, L.D, L.st, g, scale_log2, qf);
+    load_row_frag_dma<DP>(Q + base, qrow, L.T, L.D, L.st, g, scale_log2, qf);
     // running max m_i (log2 units) and row sum; -m_i in every element of neg_m,
     // from which the S accumulators start (MFMA srcC), so the scores come out
     // already shifted by the running max.  The first sub-tile sets m_i exactly.
@@ -334,14 +337,14 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
 
     auto compute = [&](auto masked, int k0, const float* Ks, const float* Vs, const floatx4 (&at)[NKT]) {
       constexpr bool MASKED = decltype(masked)::value;
-      // S^T[key][query] in log2 units: MFMA rows are keys 16mt + lq, columns the wave's queries
+      // S^T[key][query] in log2 units: MFMA rows are keys 16mt + arow(lq), columns the wave's queries
       floatx4 s[NKT];
 #pragma unroll
       for (int mt = 0; mt < NKT; ++mt) {
         WHA_FENCE();
 #pragma unroll
         for (int j = 0; j < DG / 4; ++j) {
-          const float4 a = lds_read_quad<DP, true>(Ks, 16 * mt + lq, (DG / 4) * g + j);
+          const float4 a = lds_read_quad<DP, true>(Ks, 16 * mt + arow(lq), dma48_quad<DP>(g, j));
           s[mt] = mfma4(a.x, qf[4 * j + 0], j == 0 ? neg_m : s[mt]);
           s[mt] = mfma4(a.y, qf[4 * j + 1], s[mt]);
           s[mt] = mfma4(a.z, qf[4 * j + 2], s[mt]);
@@ -361,7 +364,9 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
         }
         return;
       }
-      // lane element (mt,i): key k0 + 16mt + 4g + i of query qrow, as s - m_i
+      // lane element (mt,i): key k0 + 16mt + arow(4g+i) of query qrow, as s - m_i;
+      // kept at column 16mt + 4g + i of the score layout, which at DP = 48
+      // therefore holds the keys of each 16-column group in tr16 order
       if constexpr (SAVE) {
         const int kt = k0 >> 6;
         float* dst = sc_row + (ds_block_row(kt, L.T) - (int64_t)64 * kt) * 64 + (k0 & 63);
@@ -373,7 +378,7 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
         for (int mt = 0; mt < NKT; ++mt) {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            s[mt][i] = (k0 + 16 * mt + 4 * g + i > key_last) ? -INFINITY : s[mt][i];
+            s[mt][i] = (k0 + 16 * mt + arow(4 * g + i) > key_last) ? -INFINITY : s[mt][i];
         }
       }
       // largest shifted score of the query (its keys here, then the 4 lane groups)
@@ -422,7 +427,7 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float va[NDT];
-          lds_read_seg<DP, NDT, true>(Vs, 16 * mt + 4 * g + i, lq, va);
+          lds_read_seg<DP, NDT, true>(Vs, 16 * mt + arow(4 * g + i), lq, va);
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma4(va[dt], s[mt][i], oacc[dt]);
         }

@@ -141,11 +141,15 @@ __device__ __forceinline__ float pair_sum32(float x) {
 // conflicted).  For DP = 64 rows are unpadded and quad c of row r is stored at
 // quad c ^ (r & 11), which keeps all three patterns conflict-free for every
 // lane grouping consistent with the probe; DP = 128 uses the XOR in swz().
-// DP = 48 rows (12 quads) are unpadded too, with rows 4..7 of every 16 rotated
-// by half a row (quad c at (c + 6) mod 12 when r & 4): the rows-by-lane reads
-// (quads 3g + j) stay conflict-free for every such lane grouping, and the
-// contractions over rows read single floats d = 16dt + lq (lds_read_seg), 32
-// lanes of which always hit 32 different banks.  Kernels opt in (ALLOW_SWZ):
+// DP = 48 rows (12 quads) are unpadded too, quad c of row r stored at
+// c ^ ((r >> 2) & 3) (within its aligned group of four).  Its kernels pair it
+// with a different assignment (dma48_row, dma48_quad): the A operand row m of
+// an MFMA is tile row tr16(m) (rows transposed in 4 x 4 blocks), rows-by-lane
+// reads take quads 4j + g, and the contractions over rows read single floats
+// d = 16dt + lq (lds_read_seg) of rows tr16(4g + i).  Then every ds_read_b128
+// is conflict-free for every lane grouping consistent with the probe, and the
+// 64 lanes of every 32-bit read hit 64 different banks (with rows not
+// transposed no layout of 48-float rows does both).  Kernels opt in (ALLOW_SWZ):
 // the permutation costs per-lane address registers, which only pays where LDS
 // traffic matters more than VGPRs.  Other DP, and kernels that do not opt in,
 // keep a 4-float pad.
@@ -160,7 +164,7 @@ struct Lds {
   // stored position of quad c in row r (an involution in c: it also maps a
   // stored position back to its quad)
   __device__ __forceinline__ static int pq(int r, int c) {
-    if constexpr (DP == 48) return (r & 4) ? (c < 6 ? c + 6 : c - 6) : c;
+    if constexpr (DP == 48) return c ^ ((r >> 2) & 3);
     else return c ^ swz(r);
   }
   // float offset of quad c of row r
@@ -324,6 +328,18 @@ static __device__ __align__(16) float g_zero_quad[4];
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Index m = 4a + b of a 16-row group -> 4b + a (an involution).
+__host__ __device__ __forceinline__ int tr16(int m) { return ((m & 3) << 2) | ((m >> 2) & 3) | (m & ~15); }
+// Tile row of MFMA A-operand row m in the swizzled direct-to-LDS kernels:
+// transposed in 4 x 4 blocks at DP = 48, else m itself.
+template <int DP>
+__device__ __forceinline__ int dma48_row(int m) { return DP == 48 ? tr16(m) : m; }
+// Quad of k-step group j read by lane group g in a contraction over the head
+// dimension (DG/4 groups of four k-steps): quads 4j + g at DP = 48, else the
+// lane group's own contiguous range (DG/4) g + j.
+template <int DP>
+__device__ __forceinline__ int dma48_quad(int g, int j) { return DP == 48 ? 4 * j + g : (DP / 16) * g + j; }
+
 // Reads quad c of row r of an Lds<DP, SW> tile.
 template <int DP, bool SW = false>
 __device__ __forceinline__ float4 lds_read_quad(const float* tile, int r, int c) {
@@ -356,6 +372,30 @@ __device__ __forceinline__ void load_row_frag(const float* __restrict__ base, in
   } else {
 #pragma unroll
     for (int s = 0; s < DG; ++s) frag[s] = 0.f;
+  }
+}
+
+// The row fragment matching dma48_quad: lane group g holds quads
+// dma48_quad<DP>(g, j), j < DP/16, of row `row` in order (x[row][16j + 4g ..
+// +3] at DP = 48; load_row_frag's contiguous range otherwise), times mul; zero
+// past T and D.  128-bit loads.
+template <int DP>
+__device__ __forceinline__ void load_row_frag_dma(const float* __restrict__ base, int row, int T, int D,
+                                                  int64_t st, int g, float mul, float* frag) {
+  if constexpr (DP != 48) {
+    load_row_frag<DP, true>(base, row, T, D, st, g, mul, frag);
+  } else {
+    const float* src = base + (int64_t)min(row, T - 1) * st;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int c = 4 * dma48_quad<DP>(g, j);
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (row < T && c < D) v = *reinterpret_cast<const float4*>(src + c);
+      frag[4 * j + 0] = v.x * mul;
+      frag[4 * j + 1] = v.y * mul;
+      frag[4 * j + 2] = v.z * mul;
+      frag[4 * j + 3] = v.w * mul;
+    }
   }
 }
 
