@@ -587,7 +587,7 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
   // This lane's fetch: wave w fills LDS chunk ch(u) = NF*w+u of both operands
   // (u < NF), or at DP = 48 chunk 3(w&1)+u (u < 3) of Q (w < 2) or of dO
   // (w >= 2): quad p = 64 ch + lane is row p / QPR of the sub-tile, stored
-  // position p % QPR, which holds logical quad pq(row, p % QPR).  Byte offsets
+  // position p % QPR, which holds logical quad pq_inv(row, p % QPR).  Byte offsets
   // from the sub-tile's first row; the last sub-tile clamps rows to T-1.
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   const bool o_half = SPLIT && wv >= 2;  // wave-uniform: this wave fetches dO
@@ -599,7 +599,7 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
   for (int u = 0; u < NF; ++u) {
     const int p = 64 * chunk(u) + lane;
     rrow[u] = p / QPR;
-    rcol[u] = LT::pq(rrow[u], p % QPR);
+    rcol[u] = LT::pq_inv(rrow[u], p % QPR);
     pad[u] = PADQ && 4 * rcol[u] >= L.D;
     roff[u] = (uint32_t)(rrow[u] * L.st + 4 * rcol[u]) * 4u;
   }
@@ -850,7 +850,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __res
 
   // this lane's part of a K tile fetch: wave w fills LDS quads 64(NF*w+u) ..
   // +63 (u < NF): quad p = 64(NF*w+u) + lane is row p / QPR, stored position
-  // p % QPR <- logical quad pq(row, p % QPR); byte offsets from the tile's first row
+  // p % QPR <- logical quad pq_inv(row, p % QPR); byte offsets from the tile's first row
   int krow_[NF], kcol[NF];
   uint32_t koff[NF];
   bool pad[NF];  // PADQ: this lane's quad lies past the head dim (fetched from g_zero_quad)
@@ -858,7 +858,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __res
   for (int u = 0; u < NF; ++u) {
     const int p = 64 * (NF * wave + u) + lane;
     krow_[u] = p / QPR;
-    kcol[u] = LT::pq(krow_[u], p % QPR);
+    kcol[u] = LT::pq_inv(krow_[u], p % QPR);
     pad[u] = PADQ && 4 * kcol[u] >= L.D;
     koff[u] = (uint32_t)(krow_[u] * L.st + 4 * kcol[u]) * 4u;
   }

@@ -243,7 +243,7 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
   // this lane's fetch: wave w fills LDS chunk ch(u) = 2w+u of K and V (u < 2),
   // or at DP = 48 chunk 3(w&1)+u (u < 3) of K (w < 2) or of V (w >= 2): quad
   // p = 64 ch + lane is row p / QPR, stored position p % QPR <- logical quad
-  // pq(row, p % QPR); byte offsets from the sub-tile's first row
+  // pq_inv(row, p % QPR); byte offsets from the sub-tile's first row
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   const bool v_half = SPLIT && wv >= 2;  // wave-uniform: this wave fetches V
   int rrow[NU], rcol[NU];
@@ -254,7 +254,7 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
   for (int u = 0; u < NU; ++u) {
     const int p = 64 * chunk(u) + lane;
     rrow[u] = p / QPR;
-    rcol[u] = LT::pq(rrow[u], p % QPR);
+    rcol[u] = LT::pq_inv(rrow[u], p % QPR);
     pad[u] = PADQ && 4 * rcol[u] >= L.D;
     roff[u] = (uint32_t)(rrow[u] * L.st + 4 * rcol[u]) * 4u;
   }

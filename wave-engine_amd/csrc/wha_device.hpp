@@ -141,15 +141,17 @@ __device__ __forceinline__ float pair_sum32(float x) {
 // conflicted).  For DP = 64 rows are unpadded and quad c of row r is stored at
 // quad c ^ (r & 11), which keeps all three patterns conflict-free for every
 // lane grouping consistent with the probe; DP = 128 uses the XOR in swz().
-// DP = 48 rows (12 quads) are unpadded too, quad c of row r stored at
-// c ^ ((r >> 2) & 3) (within its aligned group of four).  Its kernels pair it
-// with a different assignment (dma48_row, dma48_quad): the A operand row m of
-// an MFMA is tile row tr16(m) (rows transposed in 4 x 4 blocks), rows-by-lane
-// reads take quads 4j + g, and the contractions over rows read single floats
-// d = 16dt + lq (lds_read_seg) of rows tr16(4g + i).  Then every ds_read_b128
-// is conflict-free for every lane grouping consistent with the probe, and the
-// 64 lanes of every 32-bit read hit 64 different banks (with rows not
-// transposed no layout of 48-float rows does both).  Kernels opt in (ALLOW_SWZ):
+// DP = 48 rows (12 quads) are unpadded too: the three 16-float groups of a
+// row are stored in the order 1, 2, 0 and quad c within its group at
+// c ^ ((r >> 2) & 3).  Its kernels pair it with a different assignment
+// (dma48_row, dma48_quad): the A operand row m of an MFMA is tile row tr16(m)
+// (rows transposed in 4 x 4 blocks), rows-by-lane reads take quads 4j + g, and
+// the contractions over rows read d = 2lq, 2lq+1 (one 64-bit read) and
+// d = 32 + lq (one 32-bit read) of rows tr16(4g + i) (lds_read_seg).  Then
+// every ds_read_b128 is conflict-free for every lane grouping consistent with
+// the probe, each 32-lane half of a ds_read_b64 (the halves the LDS serves
+// together, measured with a probe) and all 64 lanes of a 32-bit read hit
+// different banks.  Kernels opt in (ALLOW_SWZ):
 // the permutation costs per-lane address registers, which only pays where LDS
 // traffic matters more than VGPRs.  Other DP, and kernels that do not opt in,
 // keep a 4-float pad.
@@ -161,11 +163,14 @@ struct Lds {
   // quads 8g + j, and the contractions over rows read quads lq and lq + 16 --
   // see lds_read_seg -- which r & 11 does not keep apart)
   __device__ __forceinline__ static int swz(int r) { return DP == 64 ? (r & 11) : ((r & 3) | ((r >> 1) & 4)); }
-  // stored position of quad c in row r (an involution in c: it also maps a
-  // stored position back to its quad)
+  // stored position of quad c in row r, and the quad stored at position p
   __device__ __forceinline__ static int pq(int r, int c) {
-    if constexpr (DP == 48) return c ^ ((r >> 2) & 3);
+    if constexpr (DP == 48) return 4 * (c < 4 ? 2 : (c >> 2) - 1) + ((c & 3) ^ ((r >> 2) & 3));
     else return c ^ swz(r);
+  }
+  __device__ __forceinline__ static int pq_inv(int r, int p) {
+    if constexpr (DP == 48) return 4 * (p < 8 ? (p >> 2) + 1 : 0) + ((p & 3) ^ ((r >> 2) & 3));
+    else return p ^ swz(r);
   }
   // float offset of quad c of row r
   __device__ __forceinline__ static int at(int r, int c) { return r * PITCH + 4 * (SWZ ? pq(r, c) : c); }
@@ -248,8 +253,9 @@ struct TileStage {
 // Reads N head-dim entries of row r of an Lds<DP, SW> tile for lane lq: the
 // entries [N*lq, N*lq + N) (padded tiles, and swizzled 64-wide tiles where
 // N = 4), for swizzled 128-wide tiles quads lq and lq + 16 (d = 4lq..4lq+3
-// and 64+4lq..64+4lq+3), or for swizzled 48-wide tiles d = lq, 16+lq, 32+lq
-// (three 32-bit reads): the split layouts store_row_frag_split writes back.
+// and 64+4lq..64+4lq+3), or for swizzled 48-wide tiles d = 2lq, 2lq+1 and
+// 32+lq (a 64-bit and a 32-bit read): the split layouts store_row_frag_split
+// writes back.
 template <int DP, int N, bool SW = false>
 __device__ __forceinline__ void lds_read_seg(const float* tile, int r, int lq, float* out) {
   using LT = Lds<DP, SW>;
@@ -271,10 +277,12 @@ __device__ __forceinline__ void lds_read_seg(const float* tile, int r, int lq, f
     out[6] = w.z;
     out[7] = w.w;
   } else if constexpr (LT::SWZ && DP == 48 && N == 3) {
-#pragma unroll
-    for (int dt = 0; dt < 3; ++dt) out[dt] = tile[LT::at_d(r, 16 * dt + lq)];
+    const float2 v = *reinterpret_cast<const float2*>(tile + LT::at_d(r, 2 * lq));
+    out[0] = v.x;
+    out[1] = v.y;
+    out[2] = tile[LT::at_d(r, 32 + lq)];
   } else {
-    static_assert(!LT::SWZ, "swizzled tiles are read in whole quads, or as d = 16dt + lq at DP = 48");
+    static_assert(!LT::SWZ, "swizzled tiles are read in whole quads, or as d = 2lq, 2lq+1, 32+lq at DP = 48");
     const float* p = tile + r * LT::PITCH + N * lq;
     if (N % 4 == 0) {
 #pragma unroll
@@ -454,8 +462,9 @@ __device__ __forceinline__ void store_row_frag(float* __restrict__ base, int row
 // with lds_read_seg<DP, NDT, true> (swizzled tiles): for DP = 64 the layout of
 // store_row_frag; for DP = 128 d-tile dt < 4 holds d = 4m + dt and dt >= 4
 // holds d = 64 + 4m + dt - 4 (m = MFMA row), so lane (lq, g) stores quads
-// 4g+i and 16+4g+i of row `row`; for DP = 48 d-tile dt holds d = 16dt + m, so
-// the lane stores quads 4dt+g.  128-bit stores, columns >= D skipped.
+// 4g+i and 16+4g+i of row `row`; for DP = 48 d-tiles 0 and 1 hold d = 2m and
+// 2m + 1, d-tile 2 holds d = 32 + m, so the lane stores quads 2g, 2g+1 and
+// 8+g.  128-bit stores, columns >= D skipped.
 template <int DP>
 __device__ __forceinline__ void store_row_frag_split(float* __restrict__ base, int row, int T, int D, int64_t st,
                                                      int g, const floatx4* acc, float mul) {
@@ -467,12 +476,12 @@ __device__ __forceinline__ void store_row_frag_split(float* __restrict__ base, i
   float* dst = base + (int64_t)row * st;
   if (DP == 48) {
 #pragma unroll
-    for (int dt = 0; dt < 3; ++dt) {
-      const int c = 16 * dt + 4 * g;
-      if (c < D)
-        *reinterpret_cast<float4*>(dst + c) =
-            make_float4(acc[dt][0] * mul, acc[dt][1] * mul, acc[dt][2] * mul, acc[dt][3] * mul);
-    }
+    for (int h = 0; h < 2; ++h)  // d = 8g + 4h + e <- d-tile e & 1 of row 4g + 2h + (e >> 1)
+      *reinterpret_cast<float4*>(dst + 8 * g + 4 * h) =
+          make_float4(acc[0][2 * h] * mul, acc[1][2 * h] * mul, acc[0][2 * h + 1] * mul, acc[1][2 * h + 1] * mul);
+    if (32 + 4 * g < D)
+      *reinterpret_cast<float4*>(dst + 32 + 4 * g) =
+          make_float4(acc[2][0] * mul, acc[2][1] * mul, acc[2][2] * mul, acc[2][3] * mul);
     return;
   }
 #pragma unroll
