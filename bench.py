@@ -199,6 +199,9 @@ def attn_pair(args, cfg, pkg, torch, keep, inputs=None, settle_s=None):
     kern, ms_events = timed_kernels(step, args.steps, ATTN_KERNELS, pkg, torch)
     ms = timed_plain(step, args.steps, torch)
     flops = credited_flops(B, H, T, D)
+    if kern["attn_bwd_dq"]["launches"] == 0:  # small problems: one backward kernel forms dK, dV and dQ
+        flops["attn_bwd_dkv"] += flops["attn_bwd_dq"]
+        flops["attn_bwd_dq"] = 0
     dom = max(("attn_fwd", "attn_bwd_dq", "attn_bwd_dkv"), key=lambda n: kern[n]["avg_ms"])
     achieved = flops[dom] / (kern[dom]["avg_ms"] * 1e-3) / 1e12
     variant = "kept" if plan.keeps_scores else "recompute"

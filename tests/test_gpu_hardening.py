@@ -396,8 +396,8 @@ def test_kept_pair_falls_back_on_unaligned_tensors(pkg, torch_dev):
 
 def test_small_problems_take_the_split_sweep_kernels(pkg, torch_dev):
     """Dispatch: below 256 tiles of 64 rows (and T <= 1024) the backward is the
-    two-kernel small path (no statistics pass, no kept scores); above it the
-    64-row tile kernels run with their statistics pass."""
+    one-kernel small path (no statistics pass, no separate dQ pass, no kept
+    scores); above it the 64-row tile kernels run with their statistics pass."""
     torch, dev = torch_dev
     for (B, H, T, D), small in (((4, 4, 256, 42), True), ((1, 2, 200, 64), True), ((16, 4, 256, 64), False),
                                 ((1, 2, 1100, 64), False)):
@@ -411,5 +411,6 @@ def test_small_problems_take_the_split_sweep_kernels(pkg, torch_dev):
         pkg.timing_enable(False)
         n_delta = pkg.timing_read("attn_bwd_delta")[1]
         n_dkv = pkg.timing_read("attn_bwd_dkv")[1]
+        n_dq = pkg.timing_read("attn_bwd_dq")[1]
         pkg.timing_reset()
-        assert n_dkv == 1 and n_delta == (0 if small else 1), (B, H, T, D, n_delta, n_dkv)
+        assert n_dkv == 1 and n_delta == n_dq == (0 if small else 1), (B, H, T, D, n_delta, n_dkv, n_dq)

@@ -1212,7 +1212,7 @@ hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const
                            hipStream_t stream, const float* sc) {
   if (sc != nullptr && (ds == nullptr || !WHA_DKV_DMA || !scores_kept(L, vec))) return hipErrorInvalidValue;
   if (sc == nullptr && ds != nullptr && small_problem(L))
-    return launch_attn_bwd_small(q, k, v, o, d_o, lse, dq, dk, dv, ds, L, scale, stream);
+    return launch_attn_bwd_small(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
   if (WHA_DKV_DMA && ds != nullptr && vec && (sc != nullptr ? kept_head_dim(L.D) : dma_head_dim(L.D))) {
     if (L.D == 48) return bwd_dma_t<48, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
     if (L.D < 48) return bwd_dma_t<48, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);

@@ -11,12 +11,13 @@
 // 128), and the causal sweep of those rows is split over the waves: wave w
 // takes the 16-row chunks w, w+kSW, ... of the other operand and keeps its own
 // partial state; the partials merge through LDS in a fixed order
-// (deterministic).  Grid = B*H*ceil(T/16) blocks per kernel, three kernels per
+// (deterministic).  Grid = B*H*ceil(T/16) blocks per kernel, two kernels per
 // step instead of four:
-//   attn_fwd_small_kernel      O and LSE (online softmax per wave, LSE merge)
-//   attn_bwd_dkv_small_kernel  dK, dV and dS; Delta = dO.O of each query chunk
-//                              is formed in place (no statistics pass)
-//   attn_bwd_dq_small_kernel   dQ = scale * dS K from the dS workspace
+//   attn_fwd_small_kernel  O and LSE (online softmax per wave, LSE merge)
+//   attn_bwd_small_kernel  dK, dV (key-stationary) and dQ (query-stationary,
+//                          S and dP recomputed) of the block's 16 rows in one
+//                          launch; Delta = dO.O formed in place (no
+//                          statistics pass, no dS workspace)
 // Each wave stages its chunk's operands in its own LDS region: a 16-row chunk
 // is read from global memory row by row (consecutive lanes on consecutive
 // head-dim entries, so every load instruction touches one or two rows), and
@@ -268,200 +269,203 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
   }
 }
 
-// Key-stationary: a block owns keys 16kg .. 16kg+15 (lane column lq), its
-// waves sweep the query chunks kg+w, kg+w+kSW, ...  Per chunk: S = Q K^T and
-// dP = dO V^T (contractions over d, queries on MFMA rows), P = exp2(S - LSE),
-// dS = P (dP - Delta) with Delta = dO.O of the chunk's rows, then
-// dV^T += dO^T P and dK^T += Q^T dS (contractions over the chunk's rows).  dS
-// goes to the workspace (the 64-key column-block layout of ds_block_row, zeros
-// where masked and for rows past T) for attn_bwd_dq_small_kernel.
+// The backward in one launch.  Block kg owns keys 16kg .. 16kg+15 (dK, dV)
+// and queries 16kg .. 16kg+15 (dQ); its tasks are
+//   - query chunks kg .. n_g-1 of a key-stationary pass (lane column lq = key):
+//     S = Q K^T and dP = dO V^T (contractions over d, queries on MFMA rows),
+//     P = exp2(S - LSE), dS = P (dP - Delta) with Delta = dO.O of the chunk's
+//     rows formed in place, then dV^T += dO^T P and dK^T += Q^T dS
+//     (contractions over the chunk's rows);
+//   - key chunks 0 .. kg of a query-stationary pass (lane column lq = query)
+//     that forms S^T and dP^T the same way (P from the saved LSE, Delta of the
+//     block's own queries) and dQ^T += K^T dS^T,
+// n_g + 1 tasks for every block.  Task t goes to wave t % kSW, the
+// key-stationary ones first; each wave keeps its partial dK, dV and dQ, and
+// the partials merge through LDS in a fixed order (deterministic).  No dS
+// leaves the chip.
 template <int DP>
-__global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_dkv_small_kernel(
+__global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    const float* __restrict__ O, const float* __restrict__ dO, const float* __restrict__ LSE, float* __restrict__ dK,
-    float* __restrict__ dV, float* __restrict__ DS, View L, float scale, float scale_log2) {
+    const float* __restrict__ O, const float* __restrict__ dO, const float* __restrict__ LSE, float* __restrict__ dQ,
+    float* __restrict__ dK, float* __restrict__ dV, View L, float scale, float scale_log2) {
   constexpr int DG = DP / 4, NDT = DP / 16, kSW = kSWof<DP>, TILE = 16 * (DP + 4);
-  // per wave: its Q, dO and O chunk tiles; after the sweep the space holds the
-  // waves' partial dV and dK for the sums
-  __shared__ __align__(16) float stage[kSW][3][TILE];
+  // stage[s][w]: wave w's staged chunk s (Q, dO, O of a query chunk, or K, V of
+  // a key chunk); after the sweep its partial dV (s = 0), dK (1), dQ (2).
+  // own: the block's K, V rows (its keys) and Q, dO, O rows (its queries).
+  __shared__ __align__(16) float stage[3][kSW][TILE];
+  __shared__ __align__(16) float own[5][TILE];
 
   const int BH = L.B * L.H;
   const int n_g = (L.T + 15) / 16;
   const int bh = blockIdx.x % BH;
-  const int kg = (int)(blockIdx.x / BH);  // key group; kg = 0 (the longest sweep) first
+  const int kg = (int)(blockIdx.x / BH);  // kg = 0 (the longest key-stationary sweep) first
   const int b = bh / L.H, h = bh % L.H;
   const int64_t base = (int64_t)b * L.sb + (int64_t)h * L.sh;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int lq = lane & 15, g = lane >> 4;
-  const int krow = 16 * kg + lq;  // this lane's key (MFMA column)
-  float* qs = stage[wave][0];
-  float* os = stage[wave][1];  // dO
-  float* ys = stage[wave][2];  // O
+  const int row = 16 * kg + lq;  // this lane's key (first pass) and query (second pass)
+  const int n_kv = n_g - kg;     // key-stationary tasks
 
-  // the block's 16 keys and values, staged once (waves 0 and 1, into wave 0's tiles)
-  if (wave < 2) {
+  for (int t = wave; t < 5; t += kSW) {
+    const float* src = t == 0 ? K : t == 1 ? V : t == 2 ? Q : t == 3 ? dO : O;
     ChunkRaw<DP> r;
-    r.load((wave == 0 ? K : V) + base, 16 * kg, L.T, L.D, L.st, lane);
-    r.store(stage[0][wave], lane);
+    r.load(src + base, 16 * kg, L.T, L.D, L.st, lane);
+    r.store(own[t], lane);
   }
   __syncthreads();
-  float kf[DG], vf[DG];
-  row_frag<DP>(stage[0][0], lq, g, scale_log2, kf);
-  row_frag<DP>(stage[0][1], lq, g, 1.f, vf);
-  __syncthreads();  // every wave has its K / V fragments before wave 0 reuses its tiles
 
-  floatx4 dkacc[NDT], dvacc[NDT];
+  floatx4 dkacc[NDT], dvacc[NDT], dqacc[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) {
     dkacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
     dvacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    dqacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
-  // dS entry (q, krow): row q of the key's 64-key column block (q >= 16kg >= its first row)
-  const int kt = krow >> 6;
-  float* dsc = DS + ((int64_t)bh * ds_rows(L.T) + ds_block_row(kt, L.T) - (int64_t)64 * kt) * 64 + (krow & 63);
   const float* lse = LSE + (int64_t)bh * L.T;
 
-  ChunkRaw<DP> qr, dr, orr;
-  float lsv[4];
-  auto load = [&](int c) {
-    qr.load(Q + base, 16 * c, L.T, L.D, L.st, lane);
-    dr.load(dO + base, 16 * c, L.T, L.D, L.st, lane);
-    orr.load(O + base, 16 * c, L.T, L.D, L.st, lane);
+  // ---- key-stationary tasks: query chunks c = kg + wave, kg + wave + kSW, ...
+  if (wave < n_kv) {
+    float* qs = stage[0][wave];
+    float* os = stage[1][wave];  // dO
+    float* ys = stage[2][wave];  // O
+    float kf[DG], vf[DG];
+    row_frag<DP>(own[0], lq, g, scale_log2, kf);
+    row_frag<DP>(own[1], lq, g, 1.f, vf);
+    ChunkRaw<DP> qr, dr, orr;
+    float lsv[4];
+    auto load = [&](int c) {
+      qr.load(Q + base, 16 * c, L.T, L.D, L.st, lane);
+      dr.load(dO + base, 16 * c, L.T, L.D, L.st, lane);
+      orr.load(O + base, 16 * c, L.T, L.D, L.st, lane);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int q = 16 * c + 4 * g + i;
-      lsv[i] = q < L.T ? lse[q] * kLog2e : 0.f;
-    }
-  };
-  const int c0 = kg + wave;
-  if (c0 < n_g) load(c0);
-  for (int c = c0; c < n_g; c += kSW) {
-    const int q0 = 16 * c;
-    qr.store(qs, lane);
-    dr.store(os, lane);
-    orr.store(ys, lane);
-    float lse2[4];
+      for (int i = 0; i < 4; ++i) {
+        const int q = 16 * c + 4 * g + i;
+        lsv[i] = q < L.T ? lse[q] * kLog2e : 0.f;
+      }
+    };
+    load(kg + wave);
+    for (int c = kg + wave; c < n_g; c += kSW) {
+      const int q0 = 16 * c;
+      qr.store(qs, lane);
+      dr.store(os, lane);
+      orr.store(ys, lane);
+      float lse2[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) lse2[i] = lsv[i];
-    wave_lds_sync();
-    if (c + kSW < n_g) load(c + kSW);  // the next chunk's loads in flight during this one
+      for (int i = 0; i < 4; ++i) lse2[i] = lsv[i];
+      wave_lds_sync();
+      if (c + kSW < n_g) load(c + kSW);  // the next chunk's loads in flight during this one
 
-    float qf[DG], df[DG], qc[4][NDT], dc[4][NDT];
-    row_frag<DP>(qs, lq, g, 1.f, qf);
-    row_frag<DP>(os, lq, g, 1.f, df);
-    col_frag<DP>(qs, lq, g, qc);
-    col_frag<DP>(os, lq, g, dc);
-    // Delta of query q0+lq (its d-range here, then the 4 lane groups); the
-    // accumulator rows are queries q0+4g+i: their Delta from lanes 4g+i
-    float dpart = 0.f;
+      float qf[DG], df[DG], qc[4][NDT], dc[4][NDT];
+      row_frag<DP>(qs, lq, g, 1.f, qf);
+      row_frag<DP>(os, lq, g, 1.f, df);
+      col_frag<DP>(qs, lq, g, qc);
+      col_frag<DP>(os, lq, g, dc);
+      // Delta of query q0+lq (its d-range here, then the 4 lane groups); the
+      // accumulator rows are queries q0+4g+i: their Delta from lanes 4g+i
+      float dpart = 0.f;
+      {
+        float of[DG];
+        row_frag<DP>(ys, lq, g, 1.f, of);
+#pragma unroll
+        for (int j = 0; j < DG; ++j) dpart += df[j] * of[j];
+      }
+      const float delta_lq = pair_sum32(pair_sum16(dpart));
+      float dlt[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dlt[i] = __shfl(delta_lq, 4 * g + i, 64);
+      // S[query][key] (log2 units) and dP: lane element i = query q0+4g+i, key row
+      floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f}, dp = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < DG; ++j) {
+        s = mfma4(qf[j], kf[j], s);
+        dp = mfma4(df[j], vf[j], dp);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int q = q0 + 4 * g + i;
+        const bool valid = (q >= row) & (q < L.T) & (row < L.T);
+        const float p = valid ? fast_exp2(s[i] - lse2[i]) : 0.f;
+        dp[i] = valid ? p * (dp[i] - dlt[i]) : 0.f;
+        s[i] = p;
+      }
+      // dV^T[d][key] += dO^T[d][query] P[query][key]; dK^T[d][key] += Q^T[d][query] dS[query][key]
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          dvacc[dt] = mfma4(dc[i][dt], s[i], dvacc[dt]);
+          dkacc[dt] = mfma4(qc[i][dt], dp[i], dkacc[dt]);
+        }
+      }
+      wave_lds_sync();  // this chunk's tiles are read before the next one overwrites them
+    }
+  }
+
+  // ---- query-stationary tasks: key chunk j is task n_kv + j, j = 0 .. kg
+  const int j0 = ((wave - n_kv) % kSW + kSW) % kSW;  // this wave's first
+  if (j0 <= kg) {
+    float* ks = stage[0][wave];
+    float* vs = stage[1][wave];
+    float qf[DG], df[DG];
+    row_frag<DP>(own[2], lq, g, scale_log2, qf);
+    row_frag<DP>(own[3], lq, g, 1.f, df);
+    float dpart = 0.f;  // Delta of query row
     {
       float of[DG];
-      row_frag<DP>(ys, lq, g, 1.f, of);
+      row_frag<DP>(own[4], lq, g, 1.f, of);
 #pragma unroll
       for (int j = 0; j < DG; ++j) dpart += df[j] * of[j];
     }
-    const float delta_lq = pair_sum32(pair_sum16(dpart));
-    float dlt[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dlt[i] = __shfl(delta_lq, 4 * g + i, 64);
-    // S[query][key] (log2 units) and dP: lane element i = query q0+4g+i, key krow
-    floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f}, dp = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < DG; ++j) {
-      s = mfma4(qf[j], kf[j], s);
-      dp = mfma4(df[j], vf[j], dp);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int q = q0 + 4 * g + i;
-      const bool valid = (q >= krow) & (q < L.T) & (krow < L.T);
-      const float p = valid ? fast_exp2(s[i] - lse2[i]) : 0.f;
-      const float ds = valid ? p * (dp[i] - dlt[i]) : 0.f;
-      s[i] = p;
-      dp[i] = ds;
-      dsc[(int64_t)q * 64] = ds;  // q < 16*n_g <= rows of the layout
-    }
-    // dV^T[d][key] += dO^T[d][query] P[query][key]; dK^T[d][key] += Q^T[d][query] dS[query][key]
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        dvacc[dt] = mfma4(dc[i][dt], s[i], dvacc[dt]);
-        dkacc[dt] = mfma4(qc[i][dt], dp[i], dkacc[dt]);
+    const float delta = pair_sum32(pair_sum16(dpart));
+    const float lse2 = row < L.T ? lse[row] * kLog2e : 0.f;
+    ChunkRaw<DP> kr, vr;
+    kr.load(K + base, 16 * j0, L.T, L.D, L.st, lane);
+    vr.load(V + base, 16 * j0, L.T, L.D, L.st, lane);
+    for (int c = j0; c <= kg; c += kSW) {
+      const int key0 = 16 * c;
+      kr.store(ks, lane);
+      vr.store(vs, lane);
+      wave_lds_sync();
+      if (c + kSW <= kg) {  // the next chunk's loads in flight during this one
+        kr.load(K + base, 16 * (c + kSW), L.T, L.D, L.st, lane);
+        vr.load(V + base, 16 * (c + kSW), L.T, L.D, L.st, lane);
       }
+      float kf[DG], vf[DG], kc[4][NDT];
+      row_frag<DP>(ks, lq, g, 1.f, kf);
+      row_frag<DP>(vs, lq, g, 1.f, vf);
+      col_frag<DP>(ks, lq, g, kc);
+      // S^T[key][query] (log2 units) and dP^T: lane element i = key key0+4g+i, query row
+      floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f}, dp = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < DG; ++j) {
+        s = mfma4(kf[j], qf[j], s);
+        dp = mfma4(vf[j], df[j], dp);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool valid = (key0 + 4 * g + i <= row) & (row < L.T);
+        const float p = valid ? fast_exp2(s[i] - lse2) : 0.f;
+        dp[i] = valid ? p * (dp[i] - delta) : 0.f;
+      }
+      // dQ^T[d][query] += K^T[d][key] dS^T[key][query], k-index g <-> key key0+4g+i
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) dqacc[dt] = mfma4(kc[i][dt], dp[i], dqacc[dt]);
+      }
+      wave_lds_sync();  // this chunk's tiles are read before the next one overwrites them
     }
-    wave_lds_sync();  // this chunk's tiles are read before the next one overwrites them
   }
 
-  // the waves' partial dV in tiles 0 .. kSW-1 of the stage space, dK in kSW .. 2kSW-1
-  float* sm = &stage[0][0][0];
   __syncthreads();  // every wave is done with its staged chunks
-  write_wave_part<DP>(sm + wave * TILE, dvacc, lq, g);
-  write_wave_part<DP>(sm + (kSW + wave) * TILE, dkacc, lq, g);
+  write_wave_part<DP>(stage[0][wave], dvacc, lq, g);
+  write_wave_part<DP>(stage[1][wave], dkacc, lq, g);
+  write_wave_part<DP>(stage[2][wave], dqacc, lq, g);
   __syncthreads();
-  store_wave_sums<DP>(sm, dV + base, 16 * kg, L.T, L.D, L.st, 1.f);
-  store_wave_sums<DP>(sm + kSW * TILE, dK + base, 16 * kg, L.T, L.D, L.st, scale);
-}
-
-// Query-stationary dQ = scale * dS K: a block owns queries 16qg .. 16qg+15
-// (lane column lq), its waves take the key chunks w, w+kSW, ... <= qg.  A
-// lane's four dS values of a chunk (keys key0+4g .. +3 of its query) are one
-// 16-byte load; every one was written by attn_bwd_dkv_small_kernel (zeros
-// where masked).
-template <int DP>
-__global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_dq_small_kernel(const float* __restrict__ K,
-                                                                          const float* __restrict__ DS,
-                                                                          float* __restrict__ dQ, View L,
-                                                                          float scale) {
-  constexpr int NDT = DP / 16, kSW = kSWof<DP>, TILE = 16 * (DP + 4);
-  __shared__ __align__(16) float stage[kSW][TILE];
-
-  const int BH = L.B * L.H;
-  const int n_g = (L.T + 15) / 16;
-  const int bh = blockIdx.x % BH;
-  const int qg = n_g - 1 - (int)(blockIdx.x / BH);
-  const int b = bh / L.H, h = bh % L.H;
-  const int64_t base = (int64_t)b * L.sb + (int64_t)h * L.sh;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int lq = lane & 15, g = lane >> 4;
-  const int qrow = 16 * qg + lq;
-  const float* dsb = DS + (int64_t)bh * ds_rows(L.T) * 64;
-  float* ks = stage[wave];
-
-  floatx4 acc[NDT];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-  ChunkRaw<DP> kr;
-  floatx4 d4n = floatx4{0.f, 0.f, 0.f, 0.f};
-  auto load = [&](int c) {
-    const int key0 = 16 * c;
-    const int kt = key0 >> 6;  // qrow >= key0 >= 64kt: the row lies in the column block
-    d4n = *reinterpret_cast<const floatx4*>(dsb + (ds_block_row(kt, L.T) + qrow - 64 * kt) * 64 + (key0 & 63) +
-                                            4 * g);
-    kr.load(K + base, key0, L.T, L.D, L.st, lane);
-  };
-  if (wave <= qg) load(wave);
-  for (int c = wave; c <= qg; c += kSW) {
-    kr.store(ks, lane);
-    const floatx4 d4 = d4n;
-    wave_lds_sync();
-    if (c + kSW <= qg) load(c + kSW);  // the next chunk's loads in flight during this one
-    float kc[4][NDT];
-    col_frag<DP>(ks, lq, g, kc);
-    // dQ^T[d][query] += K^T[d][key] dS^T[key][query], k-index g <-> key key0+4g+i
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma4(kc[i][dt], d4[i], acc[dt]);
-    }
-    wave_lds_sync();  // this chunk's tile is read before the next one overwrites it
-  }
-  __syncthreads();  // every wave is done with its staged chunks
-  write_wave_part<DP>(stage[wave], acc, lq, g);
-  __syncthreads();
-  store_wave_sums<DP>(&stage[0][0], dQ + base, 16 * qg, L.T, L.D, L.st, scale);
+  store_wave_sums<DP>(&stage[0][0][0], dV + base, 16 * kg, L.T, L.D, L.st, 1.f);
+  store_wave_sums<DP>(&stage[1][0][0], dK + base, 16 * kg, L.T, L.D, L.st, scale);
+  store_wave_sums<DP>(&stage[2][0][0], dQ + base, 16 * kg, L.T, L.D, L.st, scale);
 }
 
 bool small_problem(const View& L) {
@@ -481,20 +485,13 @@ hipError_t fwd_small_t(const float* q, const float* k, const float* v, float* o,
 
 template <int DP>
 hipError_t bwd_small_t(const float* q, const float* k, const float* v, const float* o, const float* d_o,
-                       const float* lse, float* dq, float* dk, float* dv, float* ds, const View& L, float scale,
+                       const float* lse, float* dq, float* dk, float* dv, const View& L, float scale,
                        hipStream_t stream) {
   const float sl2 = (float)((double)scale * 1.4426950408889634);
   const dim3 grid((unsigned)((int64_t)L.B * L.H * ((L.T + 15) / 16)));
-  {
-    TimingScope ts("attn_bwd_dkv", stream);
-    hipLaunchKernelGGL(attn_bwd_dkv_small_kernel<DP>, grid, dim3(kSWof<DP> * 64), 0, stream, q, k, v, o, d_o, lse,
-                       dk, dv, ds, L, scale, sl2);
-  }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  TimingScope ts("attn_bwd_dq", stream);
-  hipLaunchKernelGGL(attn_bwd_dq_small_kernel<DP>, grid, dim3(kSWof<DP> * 64), 0, stream, k, (const float*)ds, dq, L,
-                     scale);
+  TimingScope ts("attn_bwd_dkv", stream);  // dK, dV and dQ
+  hipLaunchKernelGGL(attn_bwd_small_kernel<DP>, grid, dim3(kSWof<DP> * 64), 0, stream, q, k, v, o, d_o, lse, dq, dk,
+                     dv, L, scale, sl2);
   return hipGetLastError();
 }
 }  // namespace
@@ -510,13 +507,12 @@ hipError_t launch_attn_fwd_small(const float* q, const float* k, const float* v,
 }
 
 hipError_t launch_attn_bwd_small(const float* q, const float* k, const float* v, const float* o, const float* d_o,
-                                 const float* lse, float* dq, float* dk, float* dv, float* ds, const View& L,
-                                 float scale, hipStream_t stream) {
-  if (ds == nullptr) return hipErrorInvalidValue;
+                                 const float* lse, float* dq, float* dk, float* dv, const View& L, float scale,
+                                 hipStream_t stream) {
   switch (padded_dim(L.D)) {
-    case 48: return bwd_small_t<48>(q, k, v, o, d_o, lse, dq, dk, dv, ds, L, scale, stream);
-    case 64: return bwd_small_t<64>(q, k, v, o, d_o, lse, dq, dk, dv, ds, L, scale, stream);
-    case 128: return bwd_small_t<128>(q, k, v, o, d_o, lse, dq, dk, dv, ds, L, scale, stream);
+    case 48: return bwd_small_t<48>(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
+    case 64: return bwd_small_t<64>(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
+    case 128: return bwd_small_t<128>(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -66,14 +66,14 @@ struct TimingScope {
 hipError_t launch_attn_fwd(const float* q, const float* k, const float* v, float* o, float* lse,
                            const View& L, bool vec, float scale, hipStream_t stream, float* scores = nullptr);
 
-// The small-problem kernels (attn_small.hip): forward, and the backward as a
-// key-stationary pass (dK, dV, dS; Delta formed in place) plus dQ from dS
-// (ds: bwd_ds_floats(L) floats).
+// The small-problem kernels (attn_small.hip): forward, and the backward in one
+// launch (dK and dV key-stationary, dQ query-stationary with S and dP
+// recomputed; Delta formed in place; no workspace).
 hipError_t launch_attn_fwd_small(const float* q, const float* k, const float* v, float* o, float* lse,
                                  const View& L, float scale, hipStream_t stream);
 hipError_t launch_attn_bwd_small(const float* q, const float* k, const float* v, const float* o, const float* d_o,
-                                 const float* lse, float* dq, float* dk, float* dv, float* ds, const View& L,
-                                 float scale, hipStream_t stream);
+                                 const float* lse, float* dq, float* dk, float* dv, const View& L, float scale,
+                                 hipStream_t stream);
 
 // Delta pass of the from-probabilities backward on the forward's direct-to-LDS
 // tiles (dma_head_dim(D), 128-bit operands): stats <- the -Delta blocks of
