@@ -65,7 +65,14 @@ struct GemmArgs {
   float* rowsum = nullptr;
   int64_t rowsum_sb = 0;
   float* rowsum_part = nullptr;
+  // gemm_dma_kernel: bytes of one batch's A and B that its loads may touch
+  // (the buffer descriptors' extents; set by gemm_dma_ok)
+  uint32_t a_bytes = 0, b_bytes = 0;
 };
+
+// Word 3 of a raw buffer descriptor on gfx9-family GPUs (32-bit data format,
+// no swizzle, range-checked against the record count in bytes).
+constexpr int kRawBufferWord3 = 0x00020000;
 
 // Staging of one ROWS x KT operand tile; element (r, k) of the source is
 // p[r*s_r + k*s_k].  KC (s_k == 1, rows of the tile are source rows): LDS
@@ -446,8 +453,8 @@ struct DmaStage {
   static constexpr int QUADS = ROWS * KT / 4;
   static constexpr int IPW = QUADS / 256;  // DMA instructions per wave and stage (four waves)
   static_assert(QUADS % 256 == 0, "a stage must split evenly over four waves");
-  int64_t off[IPW];  // float offset of this lane's source quad for k0 = 0
-  int kq[IPW];       // k of that quad's first element within the stage
+  uint32_t off[IPW];  // byte offset of this lane's source quad for k0 = 0 (< 2 GiB: gemm_dma_ok)
+  int kq[IPW];        // k of that quad's first element within the stage
   // rows r0.. of the operand (extent R), element (r, k) at p[r*s_r + k*s_k]
   __device__ __forceinline__ void init(int64_t s_r, int64_t s_k, int r0, int R, int wave, int lane) {
 #pragma unroll
@@ -456,21 +463,36 @@ struct DmaStage {
       if (KC) {
         const int row = p / (KT / 4);
         const int c = (p % (KT / 4)) ^ gemm_swz<KT>(row);
-        off[u] = (int64_t)min(r0 + row, R - 1) * s_r + 4 * c;
+        off[u] = (uint32_t)(((int64_t)min(r0 + row, R - 1) * s_r + 4 * c) * 4);
         kq[u] = 4 * c;
       } else {
         const int kr = p / (ROWS / 4), rq = p % (ROWS / 4);
-        off[u] = (int64_t)kr * s_k + min(r0 + 4 * rq, R - 4);
+        off[u] = (uint32_t)(((int64_t)kr * s_k + min(r0 + 4 * rq, R - 4)) * 4);
         kq[u] = kr;
       }
     }
   }
-  __device__ __forceinline__ void issue(const float* base, int64_t s_k, int k0, int k_end, float* lds,
-                                        int wave) const {
+  // The stage at k0.  A stage wholly inside [.., k_end) is fetched with buffer
+  // loads: the operand's descriptor and the stage's byte offset k0*s_k*4 are
+  // wave-uniform (scalar registers), each lane adds its fixed offset, so the
+  // issue needs no per-lane address arithmetic.  A stage that reaches past
+  // k_end forms per-lane addresses and fetches the zero quad past it.
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, const float* base, int64_t s_k, int k0,
+                                        int k_end, float* lds, int wave) const {
+    if (k0 + KT <= k_end) {
+      const int soff = (int)((int64_t)k0 * s_k * 4);
 #pragma unroll
-    for (int u = 0; u < IPW; ++u) {
-      const float* src = k0 + kq[u] < k_end ? base + off[u] + (int64_t)k0 * s_k : g_zero_quad;
-      dma_quad(src, lds + 256 * (IPW * wave + u));
+      for (int u = 0; u < IPW; ++u)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rsrc, (__attribute__((address_space(3))) void*)(lds + 256 * (IPW * wave + u)), 16, (int)off[u], soff,
+            0, 0);
+    } else {
+      const char* b0 = reinterpret_cast<const char*>(base + (int64_t)k0 * s_k);
+#pragma unroll
+      for (int u = 0; u < IPW; ++u) {
+        const float* src = k0 + kq[u] < k_end ? reinterpret_cast<const float*>(b0 + off[u]) : g_zero_quad;
+        dma_quad(src, lds + 256 * (IPW * wave + u));
+      }
     }
   }
   // The MFMA operands of GemmStage::fetch from this layout (same tile and
@@ -536,6 +558,9 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(GemmArgs g) {
   DB db;
   da.init(g.a_sm, g.a_sk, m0, g.M, wave, lane);
   db.init(g.b_sn, g.b_sk, n0, g.N, wave, lane);
+  // buffer descriptors over each operand's extent (raw, 32-bit records)
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)g.a_bytes, kRawBufferWord3);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)Bm, (short)0, (int)g.b_bytes, kRawBufferWord3);
 
   floatx4 acc[4][MT];
 #pragma unroll
@@ -546,8 +571,8 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(GemmArgs g) {
   const int nst = k_end > k_begin ? (k_end - k_begin + KT - 1) / KT : 0;
   auto issue = [&](int s, float* Ad, float* Bd) {
     const int k0 = k_begin + s * KT;
-    da.issue(A, g.a_sk, k0, k_end, Ad, wave);
-    db.issue(Bm, g.b_sk, k0, k_end, Bd, wave);
+    da.issue(ra, A, g.a_sk, k0, k_end, Ad, wave);
+    db.issue(rb, Bm, g.b_sk, k0, k_end, Bd, wave);
   };
   auto step = [&](int s, const float* Ac, const float* Bc, float* An, float* Bn) {
     wait_vmem();
@@ -646,15 +671,18 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
 
 namespace {
 
-// Output tile: the largest of 128 x 128, 64 x 128 that gives at least four
+// Output tile: the largest of 128 x 128, 64 x 128 that gives at least eight
 // blocks per CU; 64-column tiles when N <= 64, and for N <= 256 when 64 x 128
 // tiles would leave CUs with fewer (same padding, twice the blocks).  Split-K
 // then aims for 1024 blocks.  Both thresholds were swept on the layer and wave
 // steps (tile 256/512/1024 blocks x split 512/1024/2048: 1024/1024 best, layer
-// 1.465 vs 1.501 ms at 512/512, wave 0.865 vs 0.877 ms).
+// 1.465 vs 1.501 ms at 512/512, wave 0.865 vs 0.877 ms); with the buffer-load
+// stages the tile threshold moved to 2048 (the 2304 x 768 c_attn forward in
+// 64 x 128 tiles, three full rounds of three blocks per CU: 126 vs 111 TFLOP/s,
+// layer step 1.369 vs 1.400 ms).
 constexpr int kCUs = 256;
 #ifndef WHA_GEMM_TILE_BLOCKS
-#define WHA_GEMM_TILE_BLOCKS (4 * kCUs)
+#define WHA_GEMM_TILE_BLOCKS (8 * kCUs)
 #endif
 #ifndef WHA_GEMM_SPLIT_BLOCKS
 #define WHA_GEMM_SPLIT_BLOCKS 1024
@@ -681,15 +709,25 @@ int gemm_splits(int M, int N, int K, int batch, int min_k = 256) {
 
 
 // The direct-to-LDS kernel serves the GEMMs with a k-contiguous A (y = x W^T
-// + b and dx = dy W; measured at M = 8192: layer step 1.477 vs 1.507 ms, the
-// c_attn forward 106 vs 91 TFLOP/s) when every row is 16-byte aligned along
-// its operand's contiguous direction (a_vec, b_vec), K % 4 == 0 and a
-// row-contiguous B has a multiple-of-4 extent.  The weight gradient (both
-// operands row-contiguous) keeps the register-staged stages, which measured
-// faster there (dW 0.373 vs 0.385 ms per layer step).
+// + b and dx = dy W; measured at M = 8192 with per-lane global addresses:
+// layer step 1.477 vs 1.507 ms, the c_attn forward 106 vs 91 TFLOP/s; with
+// buffer loads: 768 x 768 forward 106 vs 95, dx 117 vs 107, layer step 1.401
+// vs 1.460 ms) when every row is 16-byte aligned along its operand's
+// contiguous direction (a_vec, b_vec), K % 4 == 0, a row-contiguous B has a
+// multiple-of-4 extent and each operand spans less than 2 GiB.  The weight
+// gradient (both operands row-contiguous) keeps the register-staged stages,
+// which measured faster there (dW 0.373 vs 0.385 ms per layer step).
 template <bool A_KC, bool B_KC>
-bool gemm_dma_ok(const GemmArgs& g) {
-  return WHA_GEMM_DMA && A_KC && g.a_vec && g.b_vec && g.K % 4 == 0 && (B_KC || g.N % 4 == 0);
+bool gemm_dma_ok(GemmArgs& g) {
+  if (!(WHA_GEMM_DMA && A_KC && g.a_vec && g.b_vec && g.K % 4 == 0 && (B_KC || g.N % 4 == 0))) return false;
+  // DmaStage keeps 32-bit byte offsets and buffer extents: each operand's
+  // reachable extent (one batch) must stay below 2 GiB
+  const int64_t a_ext = 4 * ((int64_t)(g.M - 1) * g.a_sm + g.K);
+  const int64_t b_ext = 4 * (B_KC ? (int64_t)(g.N - 1) * g.b_sn + g.K : (int64_t)(g.K - 1) * g.b_sk + g.N);
+  if (a_ext >= ((int64_t)1 << 31) || b_ext >= ((int64_t)1 << 31)) return false;
+  g.a_bytes = (uint32_t)a_ext;
+  g.b_bytes = (uint32_t)b_ext;
+  return true;
 }
 
 template <int BM, int KT, int WN, bool A_KC, bool B_KC>
