@@ -883,6 +883,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __res
   };
 
   const float* dsh = DS + (int64_t)bh * ds_rows(L.T) * 64;
+  // buffer loads over this head's dS (below 2 GiB: every T up to about 30000)
+  const int64_t ds_head_bytes = ds_rows(L.T) * 256;
+  const bool ds_buf = ds_head_bytes < ((int64_t)1 << 31);
+  const __amdgpu_buffer_rsrc_t rds = buffer_rsrc(dsh, ds_buf ? (uint32_t)ds_head_bytes : 0u);
   // paired: query tiles n_qt-1-p and p; unpaired: one tile per block, the longest first
   const int n_pass = (!unpaired && n_qt - 1 - pair != pair) ? 2 : 1;
   const int work = (n_qt - pair) + (n_pass == 2 ? pair + 1 : 0);  // key tiles this block sweeps
@@ -892,11 +896,19 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __res
     const int q0 = qt * 64 + wave * 16;
     const int qrow = q0 + lq;
     const int n_kt = qt + 1;
-    // dS of key tile kt for this lane: row qrow of column block kt, columns 16c + 4g .. +3
+    // dS of key tile kt for this lane: row qrow of column block kt, columns
+    // 16c + 4g .. +3 (the block's first row is a uniform offset)
     auto load_ds = [&](int kt, float4* dsv) {
-      const float* src = dsh + (ds_block_row(kt, L.T) + qrow - 64 * kt) * 64 + 4 * g;
+      const int64_t blk = ds_block_row(kt, L.T) - (int64_t)64 * kt;
+      if (ds_buf) {
+        const int soff = (int)(blk * 256), voff = (qrow * 64 + 4 * g) * 4;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) dsv[c] = *reinterpret_cast<const float4*>(src + 16 * c);
+        for (int c = 0; c < 4; ++c) dsv[c] = buffer_load_quad(rds, voff + 64 * c, soff);
+      } else {
+        const float* src = dsh + (blk + qrow) * 64 + 4 * g;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) dsv[c] = *reinterpret_cast<const float4*>(src + 16 * c);
+      }
     };
     floatx4 acc[NDT];
 #pragma unroll

@@ -70,9 +70,6 @@ struct GemmArgs {
   uint32_t a_bytes = 0, b_bytes = 0;
 };
 
-// Word 3 of a raw buffer descriptor on gfx9-family GPUs (32-bit data format,
-// no swizzle, range-checked against the record count in bytes).
-constexpr int kRawBufferWord3 = 0x00020000;
 
 // Staging of one ROWS x KT operand tile; element (r, k) of the source is
 // p[r*s_r + k*s_k].  KC (s_k == 1, rows of the tile are source rows): LDS
@@ -559,8 +556,8 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(GemmArgs g) {
   da.init(g.a_sm, g.a_sk, m0, g.M, wave, lane);
   db.init(g.b_sn, g.b_sk, n0, g.N, wave, lane);
   // buffer descriptors over each operand's extent (raw, 32-bit records)
-  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)g.a_bytes, kRawBufferWord3);
-  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)Bm, (short)0, (int)g.b_bytes, kRawBufferWord3);
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(A, g.a_bytes);
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(Bm, g.b_bytes);
 
   floatx4 acc[4][MT];
 #pragma unroll

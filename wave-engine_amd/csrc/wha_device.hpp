@@ -333,6 +333,20 @@ __device__ __forceinline__ void prio_by_remaining(int remaining, int total) {
 // must hold exact zeros: a finite operand times a zero pad, never times data)
 static __device__ __align__(16) float g_zero_quad[4];
 
+// Raw buffer descriptors (gfx9 family: word 3 = 32-bit data format, no
+// swizzle; loads are range-checked against the record count in bytes).  A
+// buffer load takes a wave-uniform descriptor and offset from scalar registers
+// and only a 32-bit offset per lane, so a fixed per-lane offset plus a moving
+// uniform one costs no per-lane address arithmetic.
+constexpr int kRawBufferWord3 = 0x00020000;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRawBufferWord3);
+}
+__device__ __forceinline__ float4 buffer_load_quad(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  const floatx4 v = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
