@@ -10,10 +10,11 @@
 // with A and B given by strides, so the same kernel serves y = X W^T + b,
 // dX = dY W and dW = dY^T X.
 //
-// Tiling: 128 x 128 output tile per 256-thread block, 2 x 2 waves of 64 x 64,
-// 16-deep k stages staged through LDS with k contiguous (operands transposed on
-// the way in when the source is not k-contiguous), register prefetch of the
-// next stage.  MFMA rows are output columns n and MFMA columns are output rows m,
+// Tiling: 128 x 128 (or 64 x 128, 64 x 64) output tile per 256-thread block,
+// 2 x 2 waves; 32-deep k stages fetched straight into LDS by buffer loads
+// (gemm_dma_kernel), or, where alignment or size rule those out, 16-deep stages
+// staged through registers with the next stage prefetched (gemm_kernel).
+// MFMA rows are output columns n and MFMA columns are output rows m,
 // so each lane ends with 4 consecutive n of one row: 128-bit stores, bias added
 // as a float4.  Lane group g covers k = 4g..4g+3 of a stage, so one 128-bit LDS
 // read supplies four MFMA steps.  Split-K writes per-split partial tiles that a
@@ -437,8 +438,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 // needed).  Rows past the operand's extent read its last row (quad) and only
 // feed outputs that are never stored; k past the block's range reads a zero
 // quad.  Requires 16-byte aligned rows, K % 4 == 0 and, for a row-contiguous
-// operand, an extent that is a multiple of 4 (gemm_dma_ok).  Used for the
-// GEMMs with a k-contiguous A (no bias row sums to form).
+// operand, an extent that is a multiple of 4 (gemm_dma_ok).  Serves all three
+// projection GEMMs; for the weight gradient the bias row sums are read from
+// the staged A tiles.
 
 template <int KT>
 __device__ __forceinline__ int gemm_swz(int r) {
@@ -528,7 +530,6 @@ struct DmaStage {
 
 template <int BM, int KT, int WN, bool A_KC, bool B_KC, bool PARTIAL>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(GemmArgs g) {
-  static_assert(A_KC, "the weight-gradient GEMM (row-contiguous A, bias row sums) keeps gemm_kernel");
   constexpr int BN = 64 * WN;
   constexpr int MT = BM * WN / 64;  // 16-row m tiles per wave
   using DA = DmaStage<BM, KT, A_KC>;
@@ -571,10 +572,30 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(GemmArgs g) {
     da.issue(ra, A, g.a_sk, k0, k_end, Ad, wave);
     db.issue(rb, Bm, g.b_sk, k0, k_end, Bd, wave);
   };
+  // bias gradient (row-contiguous A, the weight-gradient GEMM): the blocks of
+  // the first column tile add up the staged A rows, each thread rows
+  // 4*(tid % (BM/4)) .. +3 over every (256/(BM/4))-th k row of a stage -- the
+  // per-thread sums gemm_rowsum_store reduces
+  const bool want_rs = !A_KC && n0 == 0 && (PARTIAL ? g.rowsum_part : g.rowsum) != nullptr;
+  float4 rs = make_float4(0.f, 0.f, 0.f, 0.f);
   auto step = [&](int s, const float* Ac, const float* Bc, float* An, float* Bn) {
     wait_vmem();
     __syncthreads();  // stage s is in LDS; every wave is done with stage s - 1
     if (s + 1 < nst) issue(s + 1, An, Bn);
+    if constexpr (!A_KC) {
+      if (want_rs) {
+        constexpr int R4 = BM / 4, KSTEP = 256 / R4;
+        const int tid = threadIdx.x;
+#pragma unroll
+        for (int kr = tid / R4; kr < KT; kr += KSTEP) {
+          const float4 x = *reinterpret_cast<const float4*>(&Ac[kr * BM + 4 * (tid % R4)]);
+          rs.x += x.x;
+          rs.y += x.y;
+          rs.z += x.z;
+          rs.w += x.w;
+        }
+      }
+    }
 #pragma unroll
     for (int ks = 0; ks < KT; ks += 16) {
       float bvals[4][4], avals[MT][4];
@@ -596,6 +617,8 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(GemmArgs g) {
     if (s + 1 < nst) step(s + 1, As1, Bs1, As0, Bs0);
   }
 
+  static_assert(BM * KT >= 4 * 256, "the row-sum exchange fits in an A stage");
+  if (!A_KC && n0 == 0) gemm_rowsum_store<BM, PARTIAL>(g, rs, m0, bt, As0);  // after its own barrier
   gemm_store<BM, WN, A_KC, B_KC, PARTIAL>(g, acc, m0, n0, bt);
 }
 
@@ -705,21 +728,23 @@ int gemm_splits(int M, int N, int K, int batch, int min_k = 256) {
 }
 
 
-// The direct-to-LDS kernel serves the GEMMs with a k-contiguous A (y = x W^T
-// + b and dx = dy W; measured at M = 8192 with per-lane global addresses:
-// layer step 1.477 vs 1.507 ms, the c_attn forward 106 vs 91 TFLOP/s; with
-// buffer loads: 768 x 768 forward 106 vs 95, dx 117 vs 107, layer step 1.401
-// vs 1.460 ms) when every row is 16-byte aligned along its operand's
-// contiguous direction (a_vec, b_vec), K % 4 == 0, a row-contiguous B has a
-// multiple-of-4 extent and each operand spans less than 2 GiB.  The weight
-// gradient (both operands row-contiguous) keeps the register-staged stages,
-// which measured faster there (dW 0.373 vs 0.385 ms per layer step).
+// The direct-to-LDS kernel serves y = x W^T + b, dx = dy W and dW = dy^T x
+// (measured at M = 8192 with per-lane global addresses: layer step 1.477 vs
+// 1.507 ms, the c_attn forward 106 vs 91 TFLOP/s, and the weight gradient
+// slower than register-staged stages; with buffer loads: 768 x 768 forward /
+// dx / dW 107 / 116 / 95 TFLOP/s against 95 / 107 / 91, 2304 x 768 dW 122
+// against 111, layer step 1.339 vs 1.460 ms) when every row is 16-byte aligned
+// along its operand's contiguous direction (a_vec, b_vec), K % 4 == 0, a
+// row-contiguous operand has a multiple-of-4 extent and each operand spans
+// less than 2 GiB.  Otherwise gemm_kernel (register-staged stages) runs.
 template <bool A_KC, bool B_KC>
 bool gemm_dma_ok(GemmArgs& g) {
-  if (!(WHA_GEMM_DMA && A_KC && g.a_vec && g.b_vec && g.K % 4 == 0 && (B_KC || g.N % 4 == 0))) return false;
+  if (!(WHA_GEMM_DMA && g.a_vec && g.b_vec && g.K % 4 == 0 && (A_KC || g.M % 4 == 0) &&
+        (B_KC || g.N % 4 == 0)))
+    return false;
   // DmaStage keeps 32-bit byte offsets and buffer extents: each operand's
   // reachable extent (one batch) must stay below 2 GiB
-  const int64_t a_ext = 4 * ((int64_t)(g.M - 1) * g.a_sm + g.K);
+  const int64_t a_ext = 4 * (A_KC ? (int64_t)(g.M - 1) * g.a_sm + g.K : (int64_t)(g.K - 1) * g.a_sk + g.M);
   const int64_t b_ext = 4 * (B_KC ? (int64_t)(g.N - 1) * g.b_sn + g.K : (int64_t)(g.K - 1) * g.b_sk + g.N);
   if (a_ext >= ((int64_t)1 << 31) || b_ext >= ((int64_t)1 << 31)) return false;
   g.a_bytes = (uint32_t)a_ext;
@@ -736,11 +761,9 @@ hipError_t gemm_launch(GemmArgs g, float* ws, int splits, const char* name, hipS
   TimingScope ts(name, stream);
   if (splits == 1) {
     g.k_chunk = dma ? ((g.K + KD - 1) / KD) * KD : ((g.K + KT - 1) / KT) * KT;
-    if constexpr (A_KC) {
-      if (dma) {
-        hipLaunchKernelGGL((gemm_dma_kernel<BM, KD, WN, A_KC, B_KC, false>), grid, dim3(256), 0, stream, g);
-        return hipGetLastError();
-      }
+    if (dma) {
+      hipLaunchKernelGGL((gemm_dma_kernel<BM, KD, WN, A_KC, B_KC, false>), grid, dim3(256), 0, stream, g);
+      return hipGetLastError();
     }
     hipLaunchKernelGGL((gemm_kernel<BM, KT, WN, A_KC, B_KC, false>), grid, dim3(256), 0, stream, g);
     return hipGetLastError();
@@ -750,14 +773,10 @@ hipError_t gemm_launch(GemmArgs g, float* ws, int splits, const char* name, hipS
   p.k_chunk = dma ? ((per + KD - 1) / KD) * KD : ((per + KT - 1) / KT) * KT;
   p.c = ws;
   p.bias = nullptr;
-  bool launched = false;
-  if constexpr (A_KC) {
-    if (dma) {
-      hipLaunchKernelGGL((gemm_dma_kernel<BM, KD, WN, A_KC, B_KC, true>), grid, dim3(256), 0, stream, p);
-      launched = true;
-    }
-  }
-  if (!launched) hipLaunchKernelGGL((gemm_kernel<BM, KT, WN, A_KC, B_KC, true>), grid, dim3(256), 0, stream, p);
+  if (dma)
+    hipLaunchKernelGGL((gemm_dma_kernel<BM, KD, WN, A_KC, B_KC, true>), grid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((gemm_kernel<BM, KT, WN, A_KC, B_KC, true>), grid, dim3(256), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t total = (int64_t)g.M * g.N * g.batch;
