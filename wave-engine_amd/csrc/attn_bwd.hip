@@ -637,6 +637,12 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
     if (wave == 0) dma_dword(stg + st * 64 + arow(lane), Sd);
   };
 
+  // this head's dS (and kept scores, same layout) as buffers (below 2 GiB: ds_head_fits)
+  const int64_t ds_head = (int64_t)bh * ds_rows(L.T) * 64;
+  const uint32_t ds_rec = (uint32_t)(ds_rows(L.T) * 256);
+  const __amdgpu_buffer_rsrc_t rds = buffer_rsrc(DS_OUT ? DS + ds_head : DS, DS_OUT ? ds_rec : 0u);
+  const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(SAVED && !PROBS ? SC + ds_head : SC, SAVED && !PROBS ? ds_rec : 0u);
+
   // key tiles pair and n_kt-1-pair: every block does n_kt+1 tiles of work.
   // One key tile: 64 keys, wave w owns keys 64kt + 16w .. +15.
   // paired: key tiles p and n_kt-1-p; unpaired: one tile per block, the longest first
@@ -662,7 +668,12 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
     // DP = 48 the keys of each 16-column group sit in tr16 order)
     const int64_t kcol = ((int64_t)bh * ds_rows(L.T) + ds_block_row(kt, L.T) - (int64_t)64 * kt) * 64 + wave * 16 +
                          arow(lq);
-    float* dsw = DS_OUT ? DS + kcol : nullptr;
+    // dS (and kept scores) of row q0 + arow(4g + i) (i < 4) of this key tile's
+    // block: buffer accesses with the uniform offset q0 * 256 and this lane's
+    // fixed offset -- no per-lane address arithmetic
+    int vrow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vrow[i] = (int)((kcol - ds_head) * 4) + arow(4 * g + i) * 256;
     // SAVED: a lane's scores of sub-tile st (rows 32st+16mt+arow(4g+i), this lane's key)
     auto load_sc = [&](int st, float (&dst)[8]) {
       if constexpr (PROBS) {
@@ -674,11 +685,11 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
             dst[4 * mt + i] = src[(int64_t)min(st * BSUB + 16 * mt + arow(4 * g + i), L.T - 1) * L.T];
         }
       } else {
-        const float* src = SC + kcol + (int64_t)(st * BSUB) * 64;
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) dst[4 * mt + i] = src[(16 * mt + arow(4 * g + i)) * 64];
+          for (int i = 0; i < 4; ++i)
+            dst[4 * mt + i] = buffer_load_float(rsc, vrow[i], (st * BSUB + 16 * mt) * 256);
         }
       }
     };
@@ -739,11 +750,10 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
       }
 
       if (DS_OUT) {
-        float* dsq = dsw + (int64_t)qb * 64;
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) dsq[(16 * mt + arow(4 * g + i)) * 64] = dp[mt][i];
+          for (int i = 0; i < 4; ++i) buffer_store_float(rds, dp[mt][i], vrow[i], (qb + 16 * mt) * 256);
         }
       }
 
@@ -883,10 +893,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __res
   };
 
   const float* dsh = DS + (int64_t)bh * ds_rows(L.T) * 64;
-  // buffer loads over this head's dS (below 2 GiB: every T up to about 30000)
-  const int64_t ds_head_bytes = ds_rows(L.T) * 256;
-  const bool ds_buf = ds_head_bytes < ((int64_t)1 << 31);
-  const __amdgpu_buffer_rsrc_t rds = buffer_rsrc(dsh, ds_buf ? (uint32_t)ds_head_bytes : 0u);
+  // buffer loads over this head's dS (below 2 GiB: ds_head_fits)
+  const __amdgpu_buffer_rsrc_t rds = buffer_rsrc(dsh, (uint32_t)(ds_rows(L.T) * 256));
   // paired: query tiles n_qt-1-p and p; unpaired: one tile per block, the longest first
   const int n_pass = (!unpaired && n_qt - 1 - pair != pair) ? 2 : 1;
   const int work = (n_qt - pair) + (n_pass == 2 ? pair + 1 : 0);  // key tiles this block sweeps
@@ -899,16 +907,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __res
     // dS of key tile kt for this lane: row qrow of column block kt, columns
     // 16c + 4g .. +3 (the block's first row is a uniform offset)
     auto load_ds = [&](int kt, float4* dsv) {
-      const int64_t blk = ds_block_row(kt, L.T) - (int64_t)64 * kt;
-      if (ds_buf) {
-        const int soff = (int)(blk * 256), voff = (qrow * 64 + 4 * g) * 4;
+      const int soff = (int)((ds_block_row(kt, L.T) - (int64_t)64 * kt) * 256), voff = (qrow * 64 + 4 * g) * 4;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) dsv[c] = buffer_load_quad(rds, voff + 64 * c, soff);
-      } else {
-        const float* src = dsh + (blk + qrow) * 64 + 4 * g;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) dsv[c] = *reinterpret_cast<const float4*>(src + 16 * c);
-      }
+      for (int c = 0; c < 4; ++c) dsv[c] = buffer_load_quad(rds, voff + 64 * c, soff);
     };
     floatx4 acc[NDT];
 #pragma unroll
@@ -1225,7 +1226,7 @@ hipError_t launch_attn_bwd(const float* q, const float* k, const float* v, const
   if (sc != nullptr && (ds == nullptr || !WHA_DKV_DMA || !scores_kept(L, vec))) return hipErrorInvalidValue;
   if (sc == nullptr && ds != nullptr && small_problem(L))
     return launch_attn_bwd_small(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
-  if (WHA_DKV_DMA && ds != nullptr && vec && (sc != nullptr ? kept_head_dim(L.D) : dma_head_dim(L.D))) {
+  if (WHA_DKV_DMA && ds != nullptr && vec && ds_head_fits(L) && (sc != nullptr ? kept_head_dim(L.D) : dma_head_dim(L.D))) {
     if (L.D == 48) return bwd_dma_t<48, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
     if (L.D < 48) return bwd_dma_t<48, true>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
     if (L.D == 64) return bwd_dma_t<64, false>(q, k, v, o, d_o, lse, dq, dk, dv, delta, ds, L, scale, stream, sc);
@@ -1282,7 +1283,7 @@ hipError_t launch_attn_bwd_probs(const float* d_o, const float* q, const float* 
   // 128-bit att loads need every row start 16-byte aligned (the non-VEC build
   // keeps scalar loads: it only serves unaligned operands)
   const bool av = vec && L.T % 4 == 0 && (reinterpret_cast<uintptr_t>(att) & 15) == 0;
-  if (WHA_DKV_DMA && vec && ds != nullptr && stats != nullptr && dma_head_dim(L.D)) {
+  if (WHA_DKV_DMA && vec && ds != nullptr && stats != nullptr && ds_head_fits(L) && dma_head_dim(L.D)) {
 #define WHA_BWDP_DMA(DP, PADQ)                                                                                \
   return av ? bwd_probs_dma_t<DP, PADQ, true>(d_o, q, k, v, att, dq, dk, dv, delta, stats, ds, L, scale, stream) \
             : bwd_probs_dma_t<DP, PADQ, false>(d_o, q, k, v, att, dq, dk, dv, delta, stats, ds, L, scale, stream)

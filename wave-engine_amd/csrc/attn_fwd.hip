@@ -513,7 +513,9 @@ void fwd_dma_t(const float* q, const float* k, const float* v, float* o, float* 
 }
 }  // namespace
 
-bool scores_kept(const View& L, bool vec) { return WHA_FWD_DMA && vec && kept_head_dim(L.D) && !small_problem(L); }
+bool scores_kept(const View& L, bool vec) {
+  return WHA_FWD_DMA && WHA_DKV_DMA && vec && kept_head_dim(L.D) && ds_head_fits(L) && !small_problem(L);
+}
 
 namespace {
 template <int DP, bool PADQ, bool AV>

@@ -346,6 +346,14 @@ __device__ __forceinline__ float4 buffer_load_quad(__amdgpu_buffer_rsrc_t r, int
   const floatx4 v = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
   return make_float4(v[0], v[1], v[2], v[3]);
 }
+__device__ __forceinline__ float buffer_load_float(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+// x by value: __builtin_bit_cast of a vector element (v[i]) miscompiles here
+// (it reads element 0), so callers pass plain floats
+__device__ __forceinline__ void buffer_store_float(__amdgpu_buffer_rsrc_t r, float x, int voff, int soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, voff, soff, 0);
+}
 
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }

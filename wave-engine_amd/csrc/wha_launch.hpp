@@ -32,6 +32,10 @@ inline bool dma_head_dim(int D) { return D % 4 == 0 && D > 32 && D <= 128; }
 // Head dims of the kept-scores pair: the same.
 inline bool kept_head_dim(int D) { return dma_head_dim(D); }
 
+// The direct-to-LDS backward reaches one head's dS (and kept scores) through
+// buffer descriptors, whose byte ranges are 31-bit here: up to T of about 30000.
+inline bool ds_head_fits(const View& L) { return ds_rows(L.T) * 256 < ((int64_t)1 << 31); }
+
 // Small problems -- fewer than kSmallBlocks 64-row tiles over all (b,h) heads
 // and rows of at most kSmallMaxT -- run the 16-row split-sweep kernels of
 // attn_small.hip (wha_attn_fwd / wha_attn_bwd; such layouts keep no scores).
