@@ -14,7 +14,8 @@
 - the wave attention's buckets at the 768-dim model shape against the
   reference's own f32 operations (atan2f, phase_to_bucket) on the device's
   projections;
-- unaligned tensors: the kept pair falls back to the recompute kernels.
+- unaligned tensors: the kept pair falls back to the recompute kernels;
+- a sequence whose dS passes 2 GiB per head takes the register-staged backward.
 """
 import numpy as np
 import pytest
@@ -298,6 +299,33 @@ def test_kept_pair_4096_preset_full(pkg, torch_dev):
         sl = lambda a: a[b:b + 1, h:h + 1]
         ref = threaded_ref(sl(q), sl(k), sl(v), sl(do), nthreads=1)
         report(f"kept 4096 b{b}h{h}", (sl(o), sl(dq), sl(dk), sl(dv)), ref)
+    check_identities(q, k, v, do, o, dq, dk, dv)
+
+
+def test_long_sequence_takes_the_register_staged_backward(pkg, torch_dev):
+    """T = 32768 on one head: its dS (2.15 GB) is past the 2 GiB a buffer
+    descriptor of the direct-to-LDS backward spans, so the pair keeps no scores
+    and the backward runs the register-staged kernels.  Causality pins the first
+    256 rows exactly (their O, LSE and dQ depend on those rows only: the oracle
+    on the prefix), the whole-output identities the rest."""
+    torch, dev = torch_dev
+    from test_gpu_parity import check_identities
+    B, H, T, D = 1, 1, 32768, 64
+    print("case long sequence T=32768", flush=True)
+    assert pkg.attn_scores_bytes(pkg.layout_bhtd(B, H, T, D)) == 0
+    q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=5)
+    tq, tk, tv, tdo = (torch.from_numpy(a).to(dev) for a in (q, k, v, do))
+    o, lse = pkg.attn_fwd(tq, tk, tv)
+    dq, dk, dv = pkg.attn_bwd(tq, tk, tv, o, tdo, lse)
+    torch.cuda.synchronize()
+    o, lse, dq, dk, dv = (x.cpu().numpy() for x in (o, lse, dq, dk, dv))
+    P = 256
+    prefix = [np.ascontiguousarray(a[:, :, :P]) for a in (q, k, v, do)]
+    r32 = oracle.fwd_bwd_bhtd(*prefix, "f32")
+    r64 = oracle.fwd_bwd_bhtd(*prefix, "f64")
+    assert_parity("O prefix", o[:, :, :P], r32[0])
+    assert_parity("dQ prefix", dq[:, :, :P], r32[1])
+    assert np.abs(lse[:, :, :P] - r64[4]).max() < 2e-5
     check_identities(q, k, v, do, o, dq, dk, dv)
 
 
