@@ -235,6 +235,9 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
   const char* kg = reinterpret_cast<const char*>(K + base);
   const char* vg = reinterpret_cast<const char*>(V + base);
   const int64_t sub_bytes = (int64_t)BSUB * L.st * 4;
+  // SAVE: this head's block of the score layout as a buffer
+  const __amdgpu_buffer_rsrc_t rsc =
+      buffer_rsrc(SAVE ? SC + (int64_t)bh * ds_rows(L.T) * 64 : SC, SAVE ? (uint32_t)(ds_rows(L.T) * 256) : 0u);
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -317,7 +320,8 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
     const int n_sub = (min(L.T, (qt + 1) * 64) + BSUB - 1) / BSUB;
     const int key_last = min(qrow, L.T - 1);  // keys above it are masked
     // SAVE: this lane's row of the score layout, less 64 rows per column block
-    float* sc_row = SAVE ? SC + ((int64_t)bh * ds_rows(L.T) + qrow) * 64 + 4 * g : nullptr;
+    // (through a buffer over this head's score blocks: below 2 GiB, scores_kept)
+    const int sc_lane = (qrow * 64 + 4 * g) * 4;
     // DELTA: this lane's att row (clamped into the tensor; rows past T are never stored)
     const float* att_row = DELTA ? ATT + ((int64_t)bh * L.T + min(qrow, L.T - 1)) * L.T : nullptr;
     float d_acc = 0.f;
@@ -369,9 +373,9 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
       // therefore holds the keys of each 16-column group in tr16 order
       if constexpr (SAVE) {
         const int kt = k0 >> 6;
-        float* dst = sc_row + (ds_block_row(kt, L.T) - (int64_t)64 * kt) * 64 + (k0 & 63);
+        const int sc_blk = (int)(((ds_block_row(kt, L.T) - (int64_t)64 * kt) * 64 + (k0 & 63)) * 4);
 #pragma unroll
-        for (int mt = 0; mt < NKT; ++mt) *reinterpret_cast<floatx4*>(dst + 16 * mt) = s[mt] - neg_m;
+        for (int mt = 0; mt < NKT; ++mt) buffer_store_quad(rsc, s[mt] - neg_m, sc_lane, sc_blk + 64 * mt);
       }
       if (MASKED) {
 #pragma unroll

@@ -354,6 +354,10 @@ __device__ __forceinline__ float buffer_load_float(__amdgpu_buffer_rsrc_t r, int
 __device__ __forceinline__ void buffer_store_float(__amdgpu_buffer_rsrc_t r, float x, int voff, int soff) {
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, voff, soff, 0);
 }
+__device__ __forceinline__ void buffer_store_quad(__amdgpu_buffer_rsrc_t r, floatx4 v, int voff, int soff) {
+  typedef unsigned uintx4 __attribute__((ext_vector_type(4)));
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4, v), r, voff, soff, 0);
+}
 
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
