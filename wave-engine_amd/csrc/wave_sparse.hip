@@ -341,11 +341,15 @@ __global__ __launch_bounds__(256) void wave_sfwd_kernel(const float* __restrict_
 #pragma unroll
     for (int e = 0; e < FG; ++e) {
       const int f = g * FG + e;
-      qf[e] = qok ? FSh[(int64_t)qrow * kFP + f] * (f < 2 ? kLog2e : w_cs) : 0.f;
+      // unconditional loads (row 0 stands in past T), so they issue together
+      qf[e] = FSh[(int64_t)(qok ? qrow : 0) * kFP + f] * (f < 2 ? kLog2e : w_cs);
+      qf[e] = qok ? qf[e] : 0.f;
     }
   }
   const int qb = qok ? BSh[qrow] : 0;
   const int qpos = qok ? PSh[qrow] : -1;
+  // bucket of the previous position, for the k = q - 1 term (fetched now, used last)
+  const int pb = qok && qpos >= 1 ? Bh[qpos - 1] : 0;
   const int nq = qok ? near_set(1 << qb) : 0;  // buckets this query admits
   const int4 ci = qc < NC ? CIh[qc] : empty_chunk();
 
@@ -358,13 +362,13 @@ __global__ __launch_bounds__(256) void wave_sfwd_kernel(const float* __restrict_
   StageInfo nxt, nxt2;
   ChunkRows<kFP, kLDF> fs;
   GatherRows<DP, LD, VEC> vs;
-  int kbit_r = 0, kp_r = -1;
+  int kb_r = 0, kp_r = -1;  // raw bucket: its bit is formed when stored, not beside the load
   auto load = [&](int kt) {
     fs.load(FSh, nxt.row0, T, tid);
     vs.load(V + vbase, Lv.st, Lv.D, tid);
     if (tid < 64) {
       const int j = sel4(nxt.row0, tid >> 4) + (tid & 15);
-      kbit_r = j < T ? 1 << BSh[j] : 0;
+      kb_r = j < T ? BSh[j] : 0;
       kp_r = j < T ? PSh[j] : -1;
     }
     if (kt + 1 < n_kt) {
@@ -392,7 +396,7 @@ __global__ __launch_bounds__(256) void wave_sfwd_kernel(const float* __restrict_
     fs.store(Fs, tid);
     vs.store(Vs, tid);
     if (tid < 64) {
-      Bs[tid] = kbit_r;
+      Bs[tid] = kp_r >= 0 ? 1 << kb_r : 0;
       Ps[tid] = kp_r;
     }
     __syncthreads();
@@ -471,7 +475,7 @@ __global__ __launch_bounds__(256) void wave_sfwd_kernel(const float* __restrict_
 
   // the previous position when its bucket is not near (outside every window)
   const int pp = qpos - 1;
-  const bool extra = qok && pp >= 0 && !wave_bucket_near(Bh[pp], qb);
+  const bool extra = qok && pp >= 0 && !wave_bucket_near(pb, qb);
   float part = 0.f;
   if (extra) {
 #pragma unroll
@@ -565,11 +569,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 128 ?
 #pragma unroll
     for (int e = 0; e < FG; ++e) {
       const int f = g * FG + e;
-      kf[e] = kok ? FSh[(int64_t)krow * kFP + f] * (f < 2 ? kLog2e : w_cs) : 0.f;
+      // unconditional loads (row 0 stands in past T), so they issue together
+      kf[e] = FSh[(int64_t)(kok ? krow : 0) * kFP + f] * (f < 2 ? kLog2e : w_cs);
+      kf[e] = kok ? kf[e] : 0.f;
     }
   }
   float vf[DG];
   load_row_frag<DP, VEC>(V + vbase, kok && kpos >= 0 ? kpos : T, T, Lv.D, Lv.st, g, 1.f, vf);
+  // bucket, LSE and Delta of the query at position kpos + 1, for the k = q - 1
+  // term (fetched now, used last)
+  const int qn = kpos + 1;
+  const bool has_qn = kok && kpos >= 0 && qn < T;
+  const int qn_b = has_qn ? Bh[qn] : 0;
+  const float qn_lse = has_qn ? LSE[rbase + qn] : 0.f;
+  const float qn_del = has_qn ? Delta[rbase + qn] : 0.f;
 
   floatx4 dfacc[NFT], dvacc[NDT];
 #pragma unroll
@@ -587,7 +600,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 128 ?
   ChunkRows<kFP, kLDF> fs;
   GatherRows<DP, LD, VEC> os;
   float lse_r = 0.f, del_r = 0.f;
-  int qb_r = 0, qp_r = -1;
+  int qb_r = 0, qp_r = -1;  // raw bucket: its bit is formed when stored, not beside the load
   auto load = [&](int qt) {
     fs.load(FSh, nxt.row0, T, tid);
     os.load(dO + vbase, Lv.st, Lv.D, tid);
@@ -596,7 +609,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 128 ?
       const bool ok = j < T;
       lse_r = ok ? LSh[j] : 0.f;
       del_r = ok ? DLh[j] : 0.f;
-      qb_r = ok ? 1 << BSh[j] : 0;
+      qb_r = ok ? BSh[j] : 0;
       qp_r = ok ? PSh[j] : -1;
     }
     if (qt + 1 < n_qt) {
@@ -626,7 +639,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 128 ?
     if (tid < 64) {
       lse_s[tid] = lse_r * kLog2e;
       del_s[tid] = del_r;
-      qb_s[tid] = qb_r;
+      qb_s[tid] = qp_r >= 0 ? 1 << qb_r : 0;
       qp_s[tid] = qp_r;
     }
     __syncthreads();
@@ -706,8 +719,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 128 ?
   }
 
   // the query at position kpos + 1 when its bucket is not near this key's
-  const int qn = kpos + 1;
-  const bool extra = kok && kpos >= 0 && qn < T && !wave_bucket_near(kb, Bh[qn]);
+  const bool extra = has_qn && !wave_bucket_near(kb, qn_b);
   float sp = 0.f, dpp = 0.f;
   float dof[DG];
   float fq[FG];
@@ -725,8 +737,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 128 ?
   dpp = pair_sum32(pair_sum16(dpp));
   float dsx = 0.f;
   if (extra) {
-    const float p = fast_exp2(sp - LSE[rbase + qn] * kLog2e);
-    dsx = p * (dpp - Delta[rbase + qn]);
+    const float p = fast_exp2(sp - qn_lse * kLog2e);
+    dsx = p * (dpp - qn_del);
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
@@ -738,7 +750,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 128 ?
       for (int i = 0; i < 4; ++i) dfacc[dt][i] += dsx * fq[NFT * i + dt];
     }
   }
-  if (kok && kpos >= 0 && qn < T && g == 0) DSP[rbase + qn] = dsx;
+  if (has_qn && g == 0) DSP[rbase + qn] = dsx;
 
   const int out_row = kok && kpos >= 0 ? kpos : T;
   store_row_frag<kFP, true>(dF + rbase * kFP, out_row, T, kFP, kFP, g, dfacc, 1.f);
