@@ -385,18 +385,21 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
             s[mt][i] = (k0 + 16 * mt + arow(4 * g + i) > key_last) ? -INFINITY : s[mt][i];
         }
       }
-      // largest shifted score of the query (its keys here, then the 4 lane groups)
+      // largest shifted score among this lane's keys; the query's maximum (over
+      // the 4 lane groups) is formed only where it is used -- the first
+      // sub-tile and a rescale -- since some lane's maximum passes kLazyMax
+      // exactly when some query's does
       float mx;
       if constexpr (NKT == 2)
         mx = vmax3(vmax3(s[0][0], s[0][1], s[0][2]), vmax3(s[0][3], s[1][0], s[1][1]), vmax2(s[1][2], s[1][3]));
       else
         mx = vmax3(vmax2(s[0][0], s[0][1]), s[0][2], s[0][3]);
-      mx = pair_max32(pair_max16(mx));
       if (fresh) {
         // first sub-tile: the running max is this one's (k0 <= every query here,
         // so every lane has a finite score)
         asm volatile("" ::: "memory");
         fresh = false;
+        mx = pair_max32(pair_max16(mx));
         m_i = mx;
 #pragma unroll
         for (int mt = 0; mt < NKT; ++mt) s[mt] -= mx;
@@ -404,6 +407,7 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
       } else if (__builtin_amdgcn_ballot_w64(mx > kLazyMax) != 0) {
         // a real branch (not if-converted): rescale to the new max
         asm volatile("" ::: "memory");
+        mx = pair_max32(pair_max16(mx));
         const float d = fmaxf(mx, 0.f);  // the max grows by d; scores shift down by d
         const float alpha = fast_exp2(-d);
         l_i *= alpha;
