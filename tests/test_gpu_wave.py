@@ -15,9 +15,9 @@ from conftest import assert_parity, make_wave_weights
 pytestmark = pytest.mark.gpu
 
 # (B, T, n_embd, n_head, content_dim): head_dim 12 (padded 48), 42, 64, 128, and the
-# 768-dim model shape
+# 768-dim model shape; 3 x 37 rows put a partial 16-row tile in the 64-wide per-head projections
 CONFIGS = [(2, 100, 48, 4, 16), (1, 77, 168, 4, 0), (2, 200, 128, 2, 16), (2, 130, 256, 2, 5),
-           (2, 1024, 768, 12, 16), (3, 1, 64, 2, 30), (1, 64, 64, 1, 3)]
+           (2, 1024, 768, 12, 16), (3, 1, 64, 2, 30), (1, 64, 64, 1, 3), (3, 37, 128, 2, 8)]
 
 
 @pytest.fixture(scope="module")

@@ -33,6 +33,10 @@
 #ifndef WHA_GEMM_DMA_KT
 #define WHA_GEMM_DMA_KT 32
 #endif
+// 64 x 64 per-head projections on head64_gemm_kernel
+#ifndef WHA_HEAD64
+#define WHA_HEAD64 1
+#endif
 
 namespace wha {
 
@@ -791,6 +795,144 @@ hipError_t gemm_launch(GemmArgs g, float* ws, int splits, const char* name, hipS
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// ---------------------------------------------------------------- 64 x 64 per-head projections
+// The per-head projections of 64-wide heads (the wave attention's value
+// projection and its input gradient): for head bt,
+//   out[m][j] (+)= sum_i A[m][i] Wop(i, j) (+ bias[j]),   i, j < 64,
+// with Wop(i, j) = W_bt[j][i] (TRANS_W: y = x W^T + b) or W_bt[i][j]
+// (dx += dy W).  K = N = 64 leaves the generic tiles two k stages, so their
+// time goes to prologues and epilogues.  Here each wave holds the head's
+// operand in registers -- lane (lq, g) keeps Wop(i, 4lq + nt) for its 16
+// contraction indices i = 16u + 4g + e, MFMA k-step 4u + e, so every MFMA sums
+// the same four products, in the same step order, as gemm_dma_kernel's
+// (results bit-identical to it); MFMA column lq of n-tile nt is output column
+// 4lq + nt; the block stages the operand once in LDS -- and streams 16-row tiles: four 128-bit loads of a row's floats
+// 16u + 4g .. +3 per lane (the next tile's issued before the current tile's 64
+// MFMAs), four 128-bit stores of whole 64-float rows per lane.  Memory-bound.
+constexpr int kHead64Waves = 4;
+constexpr int kHead64TilesPerWave = 2;
+
+template <bool TRANS_W, bool ACC>
+__global__ __launch_bounds__(256) void head64_gemm_kernel(const float* __restrict__ A, int64_t lda, int64_t a_sb,
+                                                          const float* __restrict__ W, int64_t w_sb,
+                                                          const float* __restrict__ bias, int64_t b_sb,
+                                                          float* __restrict__ C, int64_t ldc, int64_t c_sb, int M) {
+  const int bt = blockIdx.y;
+  const int lane = threadIdx.x & 63, lq = lane & 15, g = lane >> 4;
+  const int wave = threadIdx.x >> 6;
+  const float* Ab = A + (int64_t)bt * a_sb;
+  const float* Wb = W + (int64_t)bt * w_sb;
+  float* Cb = C + (int64_t)bt * c_sb;
+
+  // the head's operand through LDS (one 16 KB load per block): Ws[i * 64 + j] = Wop(i, j)
+  __shared__ __align__(16) float Ws[64 * 64];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int q = (int)threadIdx.x + 256 * p;  // quad q of W: row q / 16, floats 4 (q % 16) .. +3
+    const int r = q >> 4, c4 = 4 * (q & 15);
+    const float4 v = *reinterpret_cast<const float4*>(Wb + r * 64 + c4);
+    if constexpr (TRANS_W) {
+      Ws[(c4 + 0) * 64 + r] = v.x;
+      Ws[(c4 + 1) * 64 + r] = v.y;
+      Ws[(c4 + 2) * 64 + r] = v.z;
+      Ws[(c4 + 3) * 64 + r] = v.w;
+    } else {
+      *reinterpret_cast<float4*>(&Ws[r * 64 + c4]) = v;
+    }
+  }
+  __syncthreads();
+  // wop[nt][4u + e] = Wop(16u + 4g + e, 4lq + nt): one 128-bit read of quad lq of
+  // row 16u + 4g + e per k-step (each 16-lane set reads 16 different quads)
+  float wop[4][16];
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    const float4 v = *reinterpret_cast<const float4*>(&Ws[(16 * (s >> 2) + 4 * g + (s & 3)) * 64 + 4 * lq]);
+    wop[0][s] = v.x;
+    wop[1][s] = v.y;
+    wop[2][s] = v.z;
+    wop[3][s] = v.w;
+  }
+  const float4 bv = (!ACC && bias != nullptr) ? *reinterpret_cast<const float4*>(bias + (int64_t)bt * b_sb + 4 * lq)
+                                              : make_float4(0.f, 0.f, 0.f, 0.f);
+
+  const int n_tiles = (M + 15) / 16;
+  const int stride = (int)gridDim.x * kHead64Waves;
+  // this lane's part of tile t: a[4u + e] = float 16u + 4g + e of row 16t + lq (zeros past M)
+  auto load_a = [&](int t, float (&a)[16]) {
+    const int r = 16 * t + lq;
+    const bool ok = t < n_tiles && r < M;
+    const float* p = Ab + (int64_t)(ok ? r : 0) * lda + 4 * g;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float4 v = *reinterpret_cast<const float4*>(p + 16 * u);
+      a[4 * u + 0] = ok ? v.x : 0.f;
+      a[4 * u + 1] = ok ? v.y : 0.f;
+      a[4 * u + 2] = ok ? v.z : 0.f;
+      a[4 * u + 3] = ok ? v.w : 0.f;
+    }
+  };
+  int t = (int)blockIdx.x * kHead64Waves + wave;
+  float a_cur[16], a_nxt[16];
+  load_a(t, a_cur);
+  for (; t < n_tiles; t += stride) {
+    load_a(t + stride, a_nxt);
+    // lane results: rows 16t + 4g + i, columns 4lq .. 4lq + 3
+    float4 prev[4];
+    if constexpr (ACC) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * t + 4 * g + i;
+        prev[i] = r < M ? *reinterpret_cast<const float4*>(Cb + (int64_t)r * ldc + 4 * lq)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    floatx4 acc[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) acc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) acc[nt] = mfma4(a_cur[s], wop[nt][s], acc[nt]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * t + 4 * g + i;
+      if (r >= M) continue;
+      float4 o = make_float4(acc[0][i], acc[1][i], acc[2][i], acc[3][i]);
+      const float4 add = ACC ? prev[i] : bv;
+      o.x += add.x;
+      o.y += add.y;
+      o.z += add.z;
+      o.w += add.w;
+      *reinterpret_cast<float4*>(Cb + (int64_t)r * ldc + 4 * lq) = o;
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) a_cur[e] = a_nxt[e];
+  }
+}
+
+// Whether head64_gemm_kernel serves a batched projection: 64 x 64 per head,
+// every pointer, row stride and batch stride 16-byte aligned.
+bool head64_ok(const float* a, int64_t lda, int64_t a_sb, const float* w, int64_t w_sb, const float* b,
+               int64_t b_sb, const float* c, int64_t ldc, int64_t c_sb, int M, int N, int K, int batch) {
+  return WHA_HEAD64 && N == 64 && K == 64 && M > 0 && batch > 0 && batch <= 65535 && aligned16(a) && aligned16(w) &&
+         aligned16(c) && (b == nullptr || (aligned16(b) && b_sb % 4 == 0)) && lda % 4 == 0 && a_sb % 4 == 0 &&
+         w_sb % 4 == 0 && ldc % 4 == 0 && c_sb % 4 == 0;
+}
+
+template <bool TRANS_W, bool ACC>
+hipError_t head64_launch(const float* a, int64_t lda, int64_t a_sb, const float* w, int64_t w_sb, const float* b,
+                         int64_t b_sb, float* c, int64_t ldc, int64_t c_sb, int M, int batch, const char* name,
+                         hipStream_t stream) {
+  const int n_tiles = (M + 15) / 16;
+  const int per_block = kHead64Waves * kHead64TilesPerWave;
+  const int gx = std::min((n_tiles + per_block - 1) / per_block, 65535);
+  TimingScope ts(name, stream);
+  hipLaunchKernelGGL((head64_gemm_kernel<TRANS_W, ACC>), dim3((unsigned)gx, (unsigned)batch), dim3(256), 0, stream,
+                     a, lda, a_sb, w, w_sb, b, b_sb, c, ldc, c_sb, M);
+  return hipGetLastError();
+}
+
 template <bool A_KC, bool B_KC>
 hipError_t gemm_t(GemmArgs g, float* ws, const char* name, hipStream_t stream, int min_k = 256) {
   const int splits = ws ? gemm_splits(g.M, g.N, g.K, g.batch, min_k) : 1;
@@ -828,6 +970,8 @@ size_t linear_fwd_workspace_floats(int M, int N, int K, int batch) {
 hipError_t launch_linear_fwd_batched(const float* x, int64_t ldx, int64_t x_sb, const float* w, int64_t w_sb,
                                      const float* b, int64_t b_sb, float* y, int64_t ldy, int64_t y_sb, int M,
                                      int N, int K, int batch, hipStream_t stream, float* ws) {
+  if (head64_ok(x, ldx, x_sb, w, w_sb, b, b_sb, y, ldy, y_sb, M, N, K, batch))
+    return head64_launch<true, false>(x, ldx, x_sb, w, w_sb, b, b_sb, y, ldy, y_sb, M, batch, "linear_fwd", stream);
   GemmArgs g{x, ldx, 1, w, (int64_t)K, 1, y, ldy, b, M, N, K, 0,
              aligned16(y) && ldy % 4 == 0 && y_sb % 4 == 0, false};
   g.batch = batch;
@@ -842,6 +986,11 @@ hipError_t launch_linear_fwd_batched(const float* x, int64_t ldx, int64_t x_sb, 
 hipError_t launch_linear_bwd_dx_batched(const float* dy, int64_t lddy, int64_t dy_sb, const float* w,
                                         int64_t w_sb, float* dx, int64_t lddx, int64_t dx_sb, int M, int N,
                                         int K, int batch, bool accumulate, hipStream_t stream) {
+  if (head64_ok(dy, lddy, dy_sb, w, w_sb, nullptr, 0, dx, lddx, dx_sb, M, N, K, batch))
+    return accumulate ? head64_launch<false, true>(dy, lddy, dy_sb, w, w_sb, nullptr, 0, dx, lddx, dx_sb, M, batch,
+                                                   "linear_bwd_dx", stream)
+                      : head64_launch<false, false>(dy, lddy, dy_sb, w, w_sb, nullptr, 0, dx, lddx, dx_sb, M, batch,
+                                                    "linear_bwd_dx", stream);
   // dx[m][k] = sum_n dy[m][n] w[n][k]: GEMM with (M, N=K_in, K=N_out)
   GemmArgs g{dy, lddy, 1, w, 1, (int64_t)K, dx, lddx, nullptr, M, K, N, 0,
              aligned16(dx) && lddx % 4 == 0 && dx_sb % 4 == 0, accumulate};
