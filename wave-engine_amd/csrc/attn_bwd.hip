@@ -94,20 +94,25 @@ __global__ __launch_bounds__(256) void attn_bwd_stats_kernel(const float* __rest
                                                              const float* __restrict__ dO,
                                                              const float* __restrict__ LSE,
                                                              float* __restrict__ stats, View L) {
+  // block: rows t0 .. t0+63 of head bh (two 32-row stats blocks); 16 lanes per
+  // row, kDeltaRows consecutive rows per 16-lane group; no 64-bit divisions
   const int Tb = (L.T + 31) / 32 * 32;
-  const int64_t rows = (int64_t)L.B * L.H * Tb;
-  const int64_t rbase = ((int64_t)blockIdx.x * 16 + (threadIdx.x >> 4)) * kDeltaRows;
-  const int sub = threadIdx.x & 15;
+  const int nrb = (Tb + 63) / 64;
+  const int bh = (int)(blockIdx.x / nrb), t0 = 64 * (int)(blockIdx.x % nrb);
+  const int b = bh / L.H, h = bh % L.H;
+  const int64_t hoff = (int64_t)b * L.sb + (int64_t)h * L.sh;
+  const int sub = threadIdx.x & 15, rg = threadIdx.x >> 4;
+  __shared__ float lse_s[64], del_s[64];
+  // LSE of the block's rows, requested before the dot products
+  const int tl = t0 + (int)threadIdx.x;
+  const float lse = (threadIdx.x < 64 && tl < L.T) ? LSE[(int64_t)bh * L.T + tl] : 0.f;
   float acc[kDeltaRows];
 #pragma unroll
   for (int j = 0; j < kDeltaRows; ++j) {
     acc[j] = 0.f;
-    const int64_t r = rbase + j;
-    const int t = (int)(r % Tb);
-    if (r >= rows || t >= L.T) continue;
-    const int64_t bh = r / Tb;
-    const int b = (int)(bh / L.H), h = (int)(bh % L.H);
-    const int64_t off = (int64_t)b * L.sb + (int64_t)h * L.sh + (int64_t)t * L.st;
+    const int t = t0 + rg * kDeltaRows + j;
+    if (t >= L.T) continue;
+    const int64_t off = hoff + (int64_t)t * L.st;
     for (int d = 4 * sub; d < L.D; d += 64) {
       const float4 x = *reinterpret_cast<const float4*>(dO + off + d);
       const float4 y = *reinterpret_cast<const float4*>(O + off + d);
@@ -121,13 +126,18 @@ __global__ __launch_bounds__(256) void attn_bwd_stats_kernel(const float* __rest
     a += __shfl_xor(a, 4, 16);
     a += __shfl_xor(a, 2, 16);
     a += __shfl_xor(a, 1, 16);
-    const int64_t r = rbase + j;
-    if (r < rows && sub == 0) {
-      const int t = (int)(r % Tb);
-      const int64_t bh = r / Tb;
-      float* blk = stats + (bh * (Tb / 32) + t / 32) * 64 + (t % 32);
-      blk[0] = t < L.T ? -LSE[bh * L.T + t] * kLog2e : 0.f;
-      blk[32] = t < L.T ? -a : 0.f;
+    if (sub == 0) del_s[rg * kDeltaRows + j] = a;
+  }
+  if (threadIdx.x < 64) lse_s[threadIdx.x] = lse;
+  __syncthreads();
+  // stats blocks t0/32 and t0/32 + 1 (if inside Tb): 32 x -LSE*log2(e), then 32 x -Delta
+  if (threadIdx.x < 128) {
+    const int blk = (int)threadIdx.x >> 6, half = ((int)threadIdx.x >> 5) & 1, rr = (int)threadIdx.x & 31;
+    const int t = t0 + 32 * blk + rr;
+    if (t0 + 32 * blk < Tb) {
+      const int i = 32 * blk + rr;
+      const float v = t < L.T ? (half ? -del_s[i] : -lse_s[i] * kLog2e) : 0.f;
+      stats[((int64_t)bh * (Tb / 32) + t0 / 32 + blk) * 64 + 32 * half + rr] = v;
     }
   }
 }
@@ -1078,9 +1088,8 @@ hipError_t bwd_dma_t(const float* q, const float* k, const float* v, const float
   hipError_t e;
   {
     TimingScope ts("attn_bwd_delta", stream);
-    const int64_t rows = (int64_t)L.B * L.H * ((L.T + 31) / 32 * 32);
-    hipLaunchKernelGGL(attn_bwd_stats_kernel, dim3((unsigned)((rows + 16 * kDeltaRows - 1) / (16 * kDeltaRows))),
-                       dim3(256), 0, stream, o, d_o, lse, stats, L);
+    const int64_t blocks = (int64_t)L.B * L.H * (((L.T + 31) / 32 * 32 + 63) / 64);
+    hipLaunchKernelGGL(attn_bwd_stats_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, o, d_o, lse, stats, L);
     e = hipGetLastError();
   }
   if (e != hipSuccess) return e;
