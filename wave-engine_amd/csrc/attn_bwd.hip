@@ -41,28 +41,29 @@ namespace wha {
 enum DqMode { kFused = 0, kProbs = 1, kDeltaFromProbs = 2 };
 
 
-// Delta_t = sum_d dO[t][d] * O[t][d]; 16 lanes per row, 16 rows per block.
-// Delta[r] = sum_d dO[r][d] O[r][d]: 16 lanes per row, each 16-lane group
-// kDeltaRows rows (all loads issued before the sums).  VEC: 128-bit loads
-// (D, the strides and both bases 16-byte aligned, checked on the host).
+// Delta[r] = sum_d dO[r][d] O[r][d]: a block takes 64 rows of one (b,h), 16
+// lanes per row, each 16-lane group kDeltaRows consecutive rows (all loads
+// issued before the sums), no 64-bit divisions per row; the 64 results leave
+// through LDS as one contiguous store.  VEC: 128-bit loads (D, the strides and
+// both bases 16-byte aligned, checked on the host).
 constexpr int kDeltaRows = 4;
 template <bool VEC>
 __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const float* __restrict__ O,
                                                              const float* __restrict__ dO,
                                                              float* __restrict__ Delta, View L) {
-  const int64_t rows = (int64_t)L.B * L.H * L.T;
-  const int64_t rbase = ((int64_t)blockIdx.x * 16 + (threadIdx.x >> 4)) * kDeltaRows;
-  const int sub = threadIdx.x & 15;
+  const int nrb = (L.T + 63) / 64;
+  const int bh = (int)(blockIdx.x / nrb), t0 = 64 * (int)(blockIdx.x % nrb);
+  const int b = bh / L.H, h = bh % L.H;
+  const int64_t hoff = (int64_t)b * L.sb + (int64_t)h * L.sh;
+  const int sub = threadIdx.x & 15, rg = threadIdx.x >> 4;
+  __shared__ float del_s[64];
   float acc[kDeltaRows];
 #pragma unroll
   for (int j = 0; j < kDeltaRows; ++j) {
     acc[j] = 0.f;
-    const int64_t r = rbase + j;
-    if (r >= rows) continue;
-    const int t = (int)(r % L.T);
-    const int64_t bh = r / L.T;
-    const int b = (int)(bh / L.H), h = (int)(bh % L.H);
-    const int64_t off = (int64_t)b * L.sb + (int64_t)h * L.sh + (int64_t)t * L.st;
+    const int t = t0 + rg * kDeltaRows + j;
+    if (t >= L.T) continue;
+    const int64_t off = hoff + (int64_t)t * L.st;
     if (VEC) {
       for (int d = 4 * sub; d < L.D; d += 64) {
         const float4 x = *reinterpret_cast<const float4*>(dO + off + d);
@@ -80,8 +81,10 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const float* __rest
     a += __shfl_xor(a, 4, 16);
     a += __shfl_xor(a, 2, 16);
     a += __shfl_xor(a, 1, 16);
-    if (rbase + j < rows && sub == 0) Delta[rbase + j] = a;
+    if (sub == 0) del_s[rg * kDeltaRows + j] = a;
   }
+  __syncthreads();
+  if (threadIdx.x < 64 && t0 + (int)threadIdx.x < L.T) Delta[(int64_t)bh * L.T + t0 + threadIdx.x] = del_s[threadIdx.x];
 }
 
 // Row statistics for attn_bwd_dkv_dma_kernel, per (b,h) in blocks of 32 rows
@@ -150,8 +153,7 @@ bool delta_vec(const float* o, const float* d_o, const View& L) {
          L.st % 4 == 0 && L.sh % 4 == 0 && L.sb % 4 == 0;
 }
 hipError_t delta_launch(const float* o, const float* d_o, float* delta, const View& L, hipStream_t stream) {
-  const int64_t rows = (int64_t)L.B * L.H * L.T;
-  const dim3 grid((unsigned)((rows + 16 * kDeltaRows - 1) / (16 * kDeltaRows)));
+  const dim3 grid((unsigned)((int64_t)L.B * L.H * ((L.T + 63) / 64)));
   if (delta_vec(o, d_o, L))
     hipLaunchKernelGGL(attn_bwd_delta_kernel<true>, grid, dim3(256), 0, stream, o, d_o, delta, L);
   else
