@@ -1,4 +1,4 @@
-"""A vector-memory store of more than 8 bytes (buffer_/global_/flat_store_dwordx3,
+"""A vector-memory store of more than 8 bytes (buffer_/global_/flat_/scratch_store_dwordx3,
 _dwordx4) reads its data VGPRs after it issues, so a VALU instruction that
 overwrites those VGPRs must not follow it directly: the hardware needs one wait
 state between them.  The compiler does not always keep that gap.  A build of the
@@ -15,7 +15,7 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent.parent
 PKG = ROOT / "wave-engine_amd"
 
-STORE = re.compile(r"^\s*(buffer|global|flat)_store_(dwordx3|dwordx4|b96|b128)\s+(.*)$")
+STORE = re.compile(r"^\s*(buffer|global|flat|scratch)_store_(dwordx3|dwordx4|b96|b128)\s+(.*)$")
 SKIP = re.compile(r"^\s*($|;|\.|\S+:)")
 
 
@@ -45,7 +45,7 @@ def scan(text):
         if not m:
             continue
         ops = m.group(3).split(",")
-        # buffer stores name their data first; global/flat stores name the address first
+        # buffer stores name their data first; global/flat/scratch stores name the address first
         data = vgprs(ops[0]) if m.group(1) == "buffer" else vgprs(ops[1]) if len(ops) > 1 else set()
         j = i + 1
         while j < len(lines) and SKIP.match(lines[j]):
@@ -63,6 +63,8 @@ def test_scanner_finds_the_pattern():
     assert len(scan(bad_global)) == 1
     gap = "\tbuffer_store_dwordx4 v[100:103], v86, s[52:55], s16 offen\n\ts_nop 0\n\tv_sub_f32_e32 v103, v27, v15\n"
     other = "\tbuffer_store_dwordx4 v[100:103], v86, s[52:55], s16 offen\n\tv_sub_f32_e32 v104, v27, v15\n"
+    spill = "\tscratch_store_dwordx4 off, v[20:23], s33 offset:16\n\tv_mov_b32_e32 v21, 0\n"
+    assert len(scan(spill)) == 1
     small = "\tbuffer_store_dwordx2 v[100:101], v86, s[52:55], s16 offen\n\tv_sub_f32_e32 v101, v27, v15\n"
     assert scan(gap) == [] and scan(other) == [] and scan(small) == []
 
