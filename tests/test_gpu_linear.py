@@ -22,7 +22,10 @@ def rnd(shape, seed, scale=1.0):
     return (np.random.default_rng(seed).standard_normal(shape) * scale).astype(np.float32)
 
 
-SHAPES = [(1, 1, 1), (37, 45, 29), (300, 130, 70), (129, 257, 128), (1000, 768, 384), (64, 2304, 768)]
+# (333, 64, 64): the 64 x 64 projection kernel (head64_gemm_kernel) with a partial 16-row tile, forward with
+# and without bias and the non-accumulating input gradient
+SHAPES = [(1, 1, 1), (37, 45, 29), (300, 130, 70), (129, 257, 128), (1000, 768, 384), (64, 2304, 768),
+          (333, 64, 64)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
