@@ -984,172 +984,6 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const float* __res
   }
 }
 
-// dQ = scale * dS K at head dim 64 on the bf16 MFMA (v_mfma_f32_16x16x32_bf16)
-// with both operands split into three bf16 parts (split3_pair) and the six
-// cross products of parts i + j <= 2 summed in the fp32 accumulators: the
-// accuracy of an fp32 product at 6/16 of the fp32 MFMA's time.  Same grid,
-// pairing, sweep order, dS workspace and output layout as
-// attn_bwd_dq_dma_kernel; per 64-key tile:
-//   - each thread loads one head-dim column d = lane of 16 keys 16w .. 16w+15
-//     (w = wave) into registers one tile ahead, splits it and writes the
-//     three parts to LDS planes, row 16(d & 3) + d/4 (the A-operand row m of
-//     d-tile dt for d = 4m + dt), 64 key slots and 8 pad per row (144 bytes,
-//     so the 16 rows a ds_read_b128 serves together fall in distinct banks);
-//   - key slot 32kb + 8g + e holds key 32kb + 16(e >> 2) + 4g + (e & 3): the
-//     keys of lane group g's 16 dS values (loaded as in the fp32 kernel,
-//     columns 16c + 4g .. +3) in the order the MFMA's k index takes them;
-//   - one barrier before the planes are written (every wave is done with the
-//     last tile) and an LDS-only barrier after, so the next tile's loads stay
-//     in flight across it.
-// Diagonal tile: key blocks after every query of the wave are skipped, and
-// within a block the 16-key chunk that follows every query of the wave has its
-// K parts zeroed, so those keys contribute exactly nothing (as the fp32 kernel,
-// which skips the chunk).
-template <int DP>
-__global__ __launch_bounds__(256) void attn_bwd_dq_bf16s_kernel(const float* __restrict__ K,
-                                                                const float* __restrict__ DS,
-                                                                float* __restrict__ dQ, View L, int unpaired,
-                                                                float scale) {
-  static_assert(DP == 64, "64-wide heads only");
-  constexpr int NDT = 4;
-  constexpr int PW = 36;            // plane row pitch in 32-bit words (64 bf16 slots + 8 pad)
-  constexpr int PLANE = 64 * PW;    // words per plane
-  __shared__ __align__(16) uint32_t Pl[3 * PLANE];
-
-  const int BH = L.B * L.H;
-  const int bh = blockIdx.x % BH;
-  const int pair = (int)(blockIdx.x / BH);
-  const int n_qt = (L.T + 63) / 64;
-  const int b = bh / L.H, h = bh % L.H;
-  const int64_t base = (int64_t)b * L.sb + (int64_t)h * L.sh;
-
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int lq = lane & 15, g = lane >> 4;
-
-  // this thread's share of a K tile: column d = lane, keys 16*wave + i
-  const float* kcol = K + base + lane;
-  const int wrow = (16 * (lane & 3) + (lane >> 2)) * PW + 16 * (wave >> 1) + 2 * (wave & 1);
-  auto load_k = [&](int kt, float* kr) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = min(kt * 64 + 16 * wave + i, L.T - 1);  // rows past T read row T-1 (their dS is zero)
-      kr[i] = kcol[(int64_t)r * L.st];
-    }
-  };
-  auto write_planes = [&](const float* kr) {
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {  // keys 16w + 4q4 + e' -> slots 32(w >> 1) + 8q4 + 4(w & 1) + e'
-      uint32_t h0, m0, l0, h1, m1, l1;
-      split3_pair(kr[4 * q4], kr[4 * q4 + 1], h0, m0, l0);
-      split3_pair(kr[4 * q4 + 2], kr[4 * q4 + 3], h1, m1, l1);
-      const int w = wrow + 4 * q4;
-      *reinterpret_cast<uint2*>(&Pl[w]) = make_uint2(h0, h1);
-      *reinterpret_cast<uint2*>(&Pl[PLANE + w]) = make_uint2(m0, m1);
-      *reinterpret_cast<uint2*>(&Pl[2 * PLANE + w]) = make_uint2(l0, l1);
-    }
-  };
-
-  const float* dsh = DS + (int64_t)bh * ds_rows(L.T) * 64;
-  const __amdgpu_buffer_rsrc_t rds = buffer_rsrc(dsh, (uint32_t)(ds_rows(L.T) * 256));
-  const int n_pass = (!unpaired && n_qt - 1 - pair != pair) ? 2 : 1;
-  const int work = (n_qt - pair) + (n_pass == 2 ? pair + 1 : 0);
-  int left = work;
-  float kA[16], kB[16];
-  float4 dA[4], dB[4];
-  for (int pass = 0; pass < n_pass; ++pass) {
-    const int qt = pass == 0 ? n_qt - 1 - pair : pair;
-    const int qrow = qt * 64 + wave * 16 + lq;
-    const int n_kt = qt + 1;
-    auto load_ds = [&](int kt, float4* dsv) {
-      const int soff = (int)((ds_block_row(kt, L.T) - (int64_t)64 * kt) * 256), voff = (qrow * 64 + 4 * g) * 4;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) dsv[c] = buffer_load_quad(rds, voff + 64 * c, soff);
-    };
-    floatx4 acc[NDT];
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    auto compute = [&](int kt, const float4* dc) {
-      const bool diag = kt == qt;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        if (diag && 2 * kb > wave) break;  // every key of the block follows every query of the wave
-        WHA_FENCE();
-        uint32_t bh4[4], bm4[4], bl4[4];
-        split3_pair(dc[2 * kb].x, dc[2 * kb].y, bh4[0], bm4[0], bl4[0]);
-        split3_pair(dc[2 * kb].z, dc[2 * kb].w, bh4[1], bm4[1], bl4[1]);
-        split3_pair(dc[2 * kb + 1].x, dc[2 * kb + 1].y, bh4[2], bm4[2], bl4[2]);
-        split3_pair(dc[2 * kb + 1].z, dc[2 * kb + 1].w, bh4[3], bm4[3], bl4[3]);
-        const wha_bf16x8 Bh = __builtin_bit_cast(wha_bf16x8, make_uint4(bh4[0], bh4[1], bh4[2], bh4[3]));
-        const wha_bf16x8 Bm = __builtin_bit_cast(wha_bf16x8, make_uint4(bm4[0], bm4[1], bm4[2], bm4[3]));
-        const wha_bf16x8 Bl = __builtin_bit_cast(wha_bf16x8, make_uint4(bl4[0], bl4[1], bl4[2], bl4[3]));
-        const bool cut = diag && 2 * kb + 1 > wave;  // chunk 2kb+1 follows every query of the wave
-        wha_bf16x8 Ah[NDT], Am[NDT], Al[NDT];
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          const int w = (16 * dt + lq) * PW + 16 * kb + 4 * g;
-          uint4 vh = *reinterpret_cast<const uint4*>(&Pl[w]);
-          uint4 vm = *reinterpret_cast<const uint4*>(&Pl[PLANE + w]);
-          uint4 vl = *reinterpret_cast<const uint4*>(&Pl[2 * PLANE + w]);
-          if (cut) {
-            vh.z = vh.w = 0u;
-            vm.z = vm.w = 0u;
-            vl.z = vl.w = 0u;
-          }
-          Ah[dt] = __builtin_bit_cast(wha_bf16x8, vh);
-          Am[dt] = __builtin_bit_cast(wha_bf16x8, vm);
-          Al[dt] = __builtin_bit_cast(wha_bf16x8, vl);
-        }
-        // the small terms first, four independent accumulator chains per term
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al[dt], Bh, acc[dt], 0, 0, 0);
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Am[dt], Bm, acc[dt], 0, 0, 0);
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah[dt], Bl, acc[dt], 0, 0, 0);
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Am[dt], Bh, acc[dt], 0, 0, 0);
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah[dt], Bm, acc[dt], 0, 0, 0);
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah[dt], Bh, acc[dt], 0, 0, 0);
-      }
-    };
-
-    auto step = [&](int kt, int nx, const float* kc, float* kn, const float4* dc, float4* dn) {
-      wait_vmem();
-      __syncthreads();  // this tile's K columns are in registers; every wave is done with the planes
-      write_planes(kc);
-      if (nx >= 0) {  // the next tile of the sweep
-        load_k(nx, kn);
-        load_ds(nx, dn);
-      }
-      lds_barrier();  // the planes are written; the next tile's loads stay in flight
-      prio_by_remaining(left--, work);
-      compute(kt, dc);
-    };
-
-    auto kt_at = [&](int j) { return pass == 0 ? j : n_kt - 1 - j; };
-    load_k(kt_at(0), kA);
-    load_ds(kt_at(0), dA);
-    for (int j = 0; j < n_kt; j += 2) {
-      step(kt_at(j), j + 1 < n_kt ? kt_at(j + 1) : -1, kA, kB, dA, dB);
-      if (j + 1 < n_kt) step(kt_at(j + 1), j + 2 < n_kt ? kt_at(j + 2) : -1, kB, kA, dB, dA);
-    }
-    store_row_frag_split<DP>(dQ + base, qrow, L.T, L.D, L.st, g, acc, scale);
-  }
-}
-
-// dQ on the bf16-split kernel: 64-wide heads (no padding), when enabled at build time
-#ifndef WHA_DQ_BF16
-#define WHA_DQ_BF16 0
-#endif
-template <int DP, bool PADQ>
-bool dq_bf16s(const View& L) {
-  return WHA_DQ_BF16 && DP == 64 && !PADQ && L.D == 64;
-}
-
 // Query-stationary dQ from stored dS: dQ^T[d][q] += K^T[d][key] dS^T[key][q] over
 // the causal 64-key tiles; K tiles staged through LDS (A operand, d = NDT*m + dt
 // on MFMA rows; the swizzled layout at head dim 64, where it keeps that d
@@ -1273,12 +1107,8 @@ hipError_t bwd_dma_t(const float* q, const float* k, const float* v, const float
   }
   if (e != hipSuccess) return e;
   TimingScope ts("attn_bwd_dq", stream);
-  if (dq_bf16s<DP, PADQ>(L))
-    hipLaunchKernelGGL((attn_bwd_dq_bf16s_kernel<64>), grid, dim3(256), 0, stream, k, (const float*)ds, dq, L, unp,
-                       scale);
-  else
-    hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<DP, PADQ>), grid, dim3(256), 0, stream, k, (const float*)ds, dq, L,
-                       unp, scale);
+  hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<DP, PADQ>), grid, dim3(256), 0, stream, k, (const float*)ds, dq, L, unp,
+                     scale);
   return hipGetLastError();
 }
 
@@ -1452,12 +1282,8 @@ hipError_t bwd_probs_dma_t(const float* d_o, const float* q, const float* k, con
   }
   if (e != hipSuccess) return e;
   TimingScope ts("attn_bwd_probs_dq", stream);
-  if (dq_bf16s<DP, PADQ>(L))
-    hipLaunchKernelGGL((attn_bwd_dq_bf16s_kernel<64>), grid, dim3(256), 0, stream, k, (const float*)ds, dq, L, unp,
-                       scale);
-  else
-    hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<DP, PADQ>), grid, dim3(256), 0, stream, k, (const float*)ds, dq, L,
-                       unp, scale);
+  hipLaunchKernelGGL((attn_bwd_dq_dma_kernel<DP, PADQ>), grid, dim3(256), 0, stream, k, (const float*)ds, dq, L,
+                     unp, scale);
   return hipGetLastError();
 }
 }  // namespace

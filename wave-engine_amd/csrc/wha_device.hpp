@@ -361,35 +361,6 @@ __device__ __forceinline__ void buffer_store_quad(__amdgpu_buffer_rsrc_t r, floa
 
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-// s_waitcnt lgkmcnt(0), then s_barrier: the block's LDS writes are complete
-// and visible, while vector-memory requests stay in flight (vmcnt and expcnt
-// left at their maxima); the signal fences keep the compiler from moving
-// memory accesses across it
-__device__ __forceinline__ void lds_barrier() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-// Three-part bf16 split of an fp32 pair: hi is the bf16 rounding (to nearest
-// even) of (a, b), mid that of what hi leaves, lo that of what hi + mid leave.
-// Each subtraction is exact, so hi + mid + lo keeps the 24-bit significand,
-// and the six products of parts i, j with i + j <= 2 (hi = 0) give an fp32
-// product to within about 2^-24 of it (Henry, Tang and Heinecke, 2019).  Part
-// pairs are packed as two bf16 in a 32-bit word, element 0 in the low half.
-typedef float wha_float2 __attribute__((ext_vector_type(2)));
-typedef __bf16 wha_bf16x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 wha_bf16x8 __attribute__((ext_vector_type(8)));
-__device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((wha_float2){a, b}, wha_bf16x2));
-}
-__device__ __forceinline__ void split3_pair(float a, float b, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
-  hi = bf16_pair(a, b);
-  const float ra = a - __uint_as_float(hi << 16), rb = b - __uint_as_float(hi & 0xffff0000u);
-  mid = bf16_pair(ra, rb);
-  lo = bf16_pair(ra - __uint_as_float(mid << 16), rb - __uint_as_float(mid & 0xffff0000u));
-}
 
 // Index m = 4a + b of a 16-row group -> 4b + a (an involution).
 __host__ __device__ __forceinline__ int tr16(int m) { return ((m & 3) << 2) | ((m >> 2) & 3) | (m & ~15); }
