@@ -111,9 +111,12 @@ int wha_attn_bwd(const float* q, const float* k, const float* v,
  * 8 GiB) scores may be NULL and the pair
  * behaves exactly as wha_attn_fwd / wha_attn_bwd.  The pair also runs as
  * wha_attn_fwd / wha_attn_bwd when a tensor is not 16-byte aligned (the
- * forward then leaves scores untouched, and the backward, whose check covers
- * the same q, k, v, o, recomputes); scores itself, when used, must be non-NULL
- * and 16-byte aligned (WHA_ERR_INVALID if not). */
+ * forward then leaves scores untouched).  The library records, per score
+ * buffer, whether the last wha_attn_fwd_keep into it wrote scores and for
+ * which B, H, T, D; wha_attn_bwd_kept reads scores only when that record says
+ * so (and its own tensors are aligned), and otherwise recomputes them, so a
+ * backward never reads scores the forward did not write.  scores itself, when
+ * used, must be non-NULL and 16-byte aligned (WHA_ERR_INVALID if not). */
 size_t wha_attn_scores_size(const wha_layout* layout);
 int wha_attn_fwd_keep(const float* q, const float* k, const float* v, float* o,
                       float* lse, float* scores, const wha_layout* layout,
@@ -290,11 +293,24 @@ typedef struct wha_wave_cache {
   float* lse;
 } wha_wave_cache;
 
+/* Workspace bytes of wha_wave_fwd: the bucket-sparse family's sorted operand
+ * copies, whenever the shape can take that family whatever the mode set by
+ * wha_wave_set_bucket_sparse (0 for an invalid shape, or one that only runs
+ * the all-pairs family). */
+size_t wha_wave_fwd_workspace_size(const wha_wave_shape* shape);
+
 /* wave_attention_forward (attn.rs:90-305): out [B][T][n_embd] and the cache.
  * The reference's att_weights_all is not materialised; wha_wave_probs_rows
- * recomputes any rows of it from the cache. */
+ * recomputes any rows of it from the cache.  workspace: at least
+ * wha_wave_fwd_workspace_size bytes, 16-byte aligned, scratch for this call
+ * only.  With workspace NULL the bucket-sparse family (the default from
+ * T = 1024) takes a library-cached buffer per (host thread, device, stream),
+ * as wha_attn_bwd does: growing it synchronises the stream and calls
+ * hipFree / hipMalloc, so callers that cannot allocate (HIP graph capture,
+ * allocation-free loops) must pass a workspace.  The all-pairs family needs
+ * none and never allocates. */
 int wha_wave_fwd(const float* x, const wha_wave_weights* w, const wha_wave_shape* shape, float* out,
-                 const wha_wave_cache* cache, void* stream);
+                 const wha_wave_cache* cache, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Gradients.  d_x [B][T][n_embd] (d_normed) is required; the weight
  * gradients (same layouts as wha_wave_weights, summed over the B sequences)

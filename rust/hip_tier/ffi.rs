@@ -64,8 +64,10 @@ extern "C" {
                                        v: *const f32, att: *const f32, t: i32, e: i32, n_head: i32,
                                        dq: *mut f32, dk: *mut f32, dv: *mut f32) -> c_int;
     // wave attention (src/common/attn.rs) and its KV cache (src/common/kv_cache.rs)
+    pub fn wha_wave_fwd_workspace_size(shape: *const WhaWaveShape) -> usize;
     pub fn wha_wave_fwd(x: *const f32, w: *const WhaWaveWeights, shape: *const WhaWaveShape, out: *mut f32,
-                        cache: *const WhaWaveCache, stream: *mut c_void) -> c_int;
+                        cache: *const WhaWaveCache, workspace: *mut c_void, workspace_bytes: usize,
+                        stream: *mut c_void) -> c_int;
     pub fn wha_wave_bwd_workspace_size(shape: *const WhaWaveShape) -> usize;
     pub fn wha_wave_bwd(x: *const f32, d_out: *const f32, w: *const WhaWaveWeights, shape: *const WhaWaveShape,
                         cache: *const WhaWaveCache, grads: *const WhaWaveGrads, workspace: *mut c_void,

@@ -120,7 +120,11 @@ int main() {
   wha_wave_cache c{p, p, p, p, reinterpret_cast<int32_t*>(p), p, p};
   wha_wave_shape wsh[] = {{1, 8, 63, 2, 16}, {1, 8, 64, 2, 31}, {1, 8, 258, 1, 16}, {1, 0, 64, 2, 16},
                           {1, 8, 258, 129, 0}};
-  for (auto& s : wsh) expect(wha_wave_fwd(cp, &w, &s, p, &c, nullptr) != WHA_OK, "wave shape");
+  for (auto& s : wsh) expect(wha_wave_fwd(cp, &w, &s, p, &c, nullptr, 0, nullptr) != WHA_OK, "wave shape");
+  wha_wave_shape wbig{2, 1024, 768, 12, 16};
+  expect(wha_wave_fwd(cp, &w, &wbig, p, &c, p, wha_wave_fwd_workspace_size(&wbig) - 16, nullptr) ==
+             WHA_ERR_WORKSPACE,
+         "wave forward workspace too small");
   wha_wave_shape ok{1, 8, 64, 2, 16};
   wha_wave_grads some{p, p, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
   expect(wha_wave_bwd(cp, cp, &w, &ok, &c, &some, nullptr, 0, nullptr) == WHA_ERR_INVALID, "wave grads mix");

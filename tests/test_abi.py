@@ -10,7 +10,7 @@ import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
 
-WHA_ERR_INVALID, WHA_ERR_UNSUPPORTED = -1, -2
+WHA_ERR_INVALID, WHA_ERR_UNSUPPORTED, WHA_ERR_WORKSPACE = -1, -2, -4
 
 # Several checks below pass made-up device addresses (1 << 20, 0x100000) that
 # validation must reject before any launch.  On a machine with a visible GPU a
@@ -166,12 +166,23 @@ def test_wave_entry_points_validate_before_device_use(pkg):
     for bad, msg in ((dict(E=63), b"divisible"), (dict(C=31), b"content_dim"), (dict(E=258, H=1), b"128"),
                      (dict(E=258, H=129), b"n_head"), (dict(T=0), b"positive")):
         s2, _, _ = _wave_structs(pkg, **bad)
-        rc = L.wha_wave_fwd(p, ctypes.byref(w), ctypes.byref(s2), p, ctypes.byref(cache), None)
+        rc = L.wha_wave_fwd(p, ctypes.byref(w), ctypes.byref(s2), p, ctypes.byref(cache), None, 0, None)
         assert rc in (WHA_ERR_INVALID, WHA_ERR_UNSUPPORTED) and msg in L.wha_last_error(), L.wha_last_error()
     nw = pkg._WaveWeightsC(*([1 << 20] * 6 + [None]))
-    assert L.wha_wave_fwd(p, ctypes.byref(nw), ctypes.byref(sh), p, ctypes.byref(cache), None) == WHA_ERR_INVALID
+    assert L.wha_wave_fwd(p, ctypes.byref(nw), ctypes.byref(sh), p, ctypes.byref(cache), None, 0,
+                          None) == WHA_ERR_INVALID
     nc = pkg._WaveCacheC(*([1 << 20] * 6 + [None]))
-    assert L.wha_wave_fwd(p, ctypes.byref(w), ctypes.byref(sh), p, ctypes.byref(nc), None) == WHA_ERR_INVALID
+    assert L.wha_wave_fwd(p, ctypes.byref(w), ctypes.byref(sh), p, ctypes.byref(nc), None, 0,
+                          None) == WHA_ERR_INVALID
+    # the bucket-sparse family (default from T = 1024) needs its workspace; a
+    # short one is refused before anything is enqueued
+    big, _, _ = _wave_structs(pkg, B=2, T=1024, E=768, H=12)
+    need = L.wha_wave_fwd_workspace_size(ctypes.byref(big))
+    assert need > 0
+    rc = L.wha_wave_fwd(p, ctypes.byref(w), ctypes.byref(big), p, ctypes.byref(cache), p, need - 16, None)
+    assert rc == WHA_ERR_WORKSPACE and b"workspace" in L.wha_last_error(), L.wha_last_error()
+    # shapes that only take the all-pairs family need none
+    assert L.wha_wave_fwd_workspace_size(ctypes.byref(sh)) >= 0
     some = pkg._WaveGradsC(1 << 20, 1 << 20, None, None, None, None, None, None)  # neither all nor none
     rc = L.wha_wave_bwd(p, p, ctypes.byref(w), ctypes.byref(sh), ctypes.byref(cache), ctypes.byref(some), None, 0,
                         None)

@@ -154,3 +154,47 @@ def test_kept_pair_fused_qkv_layout_is_bit_identical(pkg, torch_dev):
         got = [x.contiguous().cpu().numpy() for x in (o, lse, dq, dk, dv)]
         for a, b_ in zip(got, base):
             np.testing.assert_array_equal(a, b_)
+
+
+def test_kept_backward_reads_only_scores_the_forward_wrote(pkg, torch_dev):
+    """wha_attn_fwd_keep on tensors that are not 16-byte aligned falls back to
+    the recompute forward and leaves the score buffer untouched.  A backward
+    that then gets aligned copies of the same tensors must recompute the
+    scores, not read the buffer: here it holds NaN (never written) in the
+    first case, and scores of other inputs (a kept forward before the
+    fallback) in the second.  Both backwards must meet the bar against the
+    oracle."""
+    torch, dev = torch_dev
+    B, H, T, D = widen_b(1, 4, 200), 4, 200, 64
+    L = pkg.layout_bhtd(B, H, T, D)
+    assert pkg.attn_scores_bytes(L) > 0
+
+    def unaligned(a):
+        buf = torch.empty(a.size + 1, dtype=torch.float32, device=dev)
+        t = buf[1:].view(a.shape)
+        t.copy_(torch.from_numpy(np.ascontiguousarray(a)))
+        assert t.data_ptr() % 16 != 0
+        return t
+
+    q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=77)
+    q2, k2, v2, _ = pkg.synth_inputs(B, H, T, D, seed=78)
+    sel = [0, B - 1]
+    ref = oracle.fwd_bwd_bhtd(*(a[sel] for a in (q, k, v, do)), "f32")
+    for case in ("never written", "other inputs"):
+        print(f"case kept fallback: {case}", flush=True)
+        sc = pkg.attn_scores_buffer(L, dev)
+        sc.fill_(float("nan"))
+        if case == "other inputs":
+            # a kept forward of other inputs fills the buffer with their scores
+            t2 = [torch.from_numpy(a).to(dev) for a in (q2, k2, v2)]
+            pkg.attn_fwd(*t2, scores=sc)
+        uq, uk, uv = (unaligned(a) for a in (q, k, v))
+        uo = unaligned(np.zeros_like(q))
+        _, lse = pkg.attn_fwd(uq, uk, uv, out=uo, scores=sc)
+        tq, tk, tv, tdo = (torch.from_numpy(np.ascontiguousarray(a)).to(dev) for a in (q, k, v, do))
+        o = uo.clone()  # fresh (aligned) storage
+        assert o.data_ptr() % 16 == 0
+        dq, dk, dv = pkg.attn_bwd(tq, tk, tv, o, tdo, lse, scores=sc)
+        torch.cuda.synchronize()
+        for n, g, r in zip(("O", "dQ", "dK", "dV"), (o, dq, dk, dv), ref):
+            assert_parity(f"kept fallback ({case}) {n}", g.cpu().numpy()[sel], r)

@@ -15,7 +15,20 @@ d_harmonic_raw is a sum over positions of phi * dphi / n; with every phase
 near zero (the wrap pattern) its terms cancel, and the f32 oracle itself is
 1.1e-5 from the f64 oracle in relative L2 at T = 1024.  That gradient is
 therefore checked against the f64 oracle, within the bar or twice the f32
-oracle's own distance from f64, whichever is larger."""
+oracle's own distance from f64, whichever is larger (as is every other
+weight gradient, a sum over all positions).  At T = 2500 the f32
+oracle's distance (its sum runs over ~3.1M admitted pairs in order) measured
+3.0e-5 (wrap), 2.1e-5 (natural) and 1.0e-6 (far): which pattern it happens to
+sum well says nothing of the kernels, so above 2048 positions the bar is at
+least 4e-5 for it and for d_proj_b.  The far pattern is the hard case for the
+kernels: its phases take exactly two values, so every pair within a bucket has
+sin(n delta) = 0, and the oracle's pair terms -sin(n delta) delta dS vanish
+there, while the kernels form a position's share u_t = cos(n phi_t) G1 -
+sin(n phi_t) G0 from feature sums G over the keys (the MFMA form of the
+score), a difference of equal fp32 sums that leaves only rounding; d_r, d_s
+and the harmonic partial phi_t u_t carry it.  Measured at T = 2500 (far,
+bucket-sparse): d_harmonic_raw 2.4e-5 and d_proj_b 1.4e-5 from f64, every
+other gradient and pattern within 6.4e-6."""
 import math
 
 import numpy as np
@@ -50,17 +63,28 @@ def _weights(H, C, E, pattern, seed):
     elif pattern == "wrap":
         pb[:, 0] = 1.0      # (r, s) = (1, 0.3 x0): bucket 0 for x0 >= 0, 7 for x0 < 0 (|x0| < 3.3)
         pw[:, 1, 0] = 0.3
+    elif pattern == "natural":
+        return make_wave_weights(H, C, E, seed)
     return w
 
 
 def _expected_buckets(pattern):
-    return {"one": {3}, "far": {2, 6}, "wrap": {0, 7}}[pattern]
+    return {"one": {3}, "far": {2, 6}, "wrap": {0, 7}, "natural": None}[pattern]
 
 
-@pytest.mark.parametrize("pattern", ["one", "far", "wrap"])
-@pytest.mark.parametrize("sparse", [True, False])
-@pytest.mark.parametrize("B,T,E,H,C", [(2, 300, 128, 2, 16), (1, 1024, 256, 4, 5)])
-def test_bucket_patterns_match_oracle(pkg, torch_dev, pattern, sparse, B, T, E, H, C):
+CASES = [(p, s, sh) for sh in ((2, 300, 128, 2, 16), (1, 1024, 256, 4, 5)) for s in (True, False)
+         for p in ("one", "far", "wrap")]
+# A ragged sequence above 1024 positions: the stable bucket sort then takes
+# several passes of its 1024 threads, adding each pass's counts to the bucket
+# bases, and the bucket windows are longer; the phases of the default weights
+# give every bucket ("natural"), the adversarial patterns gaps and wrap-around.
+CASES += [(p, True, (1, 2500, 256, 4, 16)) for p in ("natural", "far", "wrap")]
+CASES += [("natural", False, (1, 2500, 256, 4, 16))]
+
+
+@pytest.mark.parametrize("pattern,sparse,shape", CASES)
+def test_bucket_patterns_match_oracle(pkg, torch_dev, pattern, sparse, shape):
+    B, T, E, H, C = shape
     torch, dev = torch_dev
     print(f"wave pattern {pattern} sparse={sparse} B{B} T{T} E{E} H{H} C{C}", flush=True)
     prev = pkg.wave_set_bucket_sparse(sparse)
@@ -77,7 +101,8 @@ def test_bucket_patterns_match_oracle(pkg, torch_dev, pattern, sparse, B, T, E, 
         grads = pkg.wave_attention_backward_full(W, cache, t(dy))
         torch.cuda.synchronize()
         bk = cache.bucket.cpu().numpy()
-        assert set(np.unique(bk)) == _expected_buckets(pattern)
+        want = _expected_buckets(pattern)
+        assert set(np.unique(bk)) == (want if want is not None else set(range(8)))
         phase = cache.phase.cpu().numpy()
         merged, lse = cache.merged.cpu().numpy(), cache.lse.cpu().numpy()
         refs = []
@@ -86,21 +111,24 @@ def test_bucket_patterns_match_oracle(pkg, torch_dev, pattern, sparse, B, T, E, 
             assert_parity(f"merged b{b}", merged[b], ref["merged"])
             assert_parity(f"lse b{b}", lse[b], ref["lse"])
             assert_parity(f"out b{b}", out[b].cpu().numpy(), ref["out"])
-            refs.append(oracle.wave_bwd(x[b], w, dy[b], "f32", phase_in=phase[b]))
-            refs[-1]["d_hraw64"] = oracle.wave_bwd(x[b], w, dy[b], "f64", phase_in=phase[b])["d_hraw"]
+            refs.append((oracle.wave_bwd(x[b], w, dy[b], "f32", phase_in=phase[b]),
+                         oracle.wave_bwd(x[b], w, dy[b], "f64", phase_in=phase[b])))
         got_dx = grads.d_normed.cpu().numpy()
         for b in range(B):
-            assert_parity(f"d_x b{b}", got_dx[b], refs[b]["d_x"])
-        s = lambda k: np.sum([r[k] for r in refs], axis=0, dtype=np.float64)
-        h32, h64 = s("d_hraw"), s("d_hraw64")
-        _, cond = errors(h32, h64)
-        assert_parity("d_harmonic_raw vs f64", grads.d_harmonic_raw.cpu().numpy(), h64, rel_l2=max(REL_L2, 2 * cond))
-        assert_parity("d_proj_w", grads.d_proj_w.cpu().numpy(), s("d_proj_w"))
-        assert_parity("d_proj_b", grads.d_proj_b.cpu().numpy(), s("d_proj_b"))
-        assert_parity("d_v_w", grads.d_v_w.cpu().numpy(), s("d_v_w"))
-        assert_parity("d_v_b", grads.d_v_b.cpu().numpy(), s("d_v_b"))
-        assert_parity("d_out_w", grads.out_proj_w.cpu().numpy(), s("d_out_w"))
-        assert_parity("d_out_b", grads.out_proj_b.cpu().numpy(), s("d_out_b"))
+            assert_parity(f"d_x b{b}", got_dx[b], refs[b][0]["d_x"])
+        # weight gradients: sums over every position of the batch, against the
+        # f64 oracle within the bar or twice the f32 oracle's own distance
+        for k, g in (("d_hraw", grads.d_harmonic_raw), ("d_proj_w", grads.d_proj_w), ("d_proj_b", grads.d_proj_b),
+                     ("d_v_w", grads.d_v_w), ("d_v_b", grads.d_v_b), ("d_out_w", grads.out_proj_w),
+                     ("d_out_b", grads.out_proj_b)):
+            r32 = np.sum([r[0][k] for r in refs], axis=0, dtype=np.float64)
+            r64 = np.sum([r[1][k] for r in refs], axis=0)
+            _, cond = errors(r32, r64)
+            floor = 4e-5 if (k in ("d_hraw", "d_proj_b") and T > 2048) else REL_L2
+            got = g.cpu().numpy()
+            print(f"{k} vs f64: rel_l2 {errors(got, r64)[1]:.2e} (f32 oracle {cond:.2e}); vs f32 oracle "
+                  f"{errors(got, r32)[1]:.2e}", flush=True)
+            assert_parity(f"{k} vs f64", got, r64, rel_l2=max(floor, 2 * cond))
     finally:
         pkg.wave_set_bucket_sparse(prev)
 
@@ -136,3 +164,39 @@ def test_families_agree_at_model_shape(pkg, torch_dev):
         pkg.wave_set_bucket_sparse(prev)
     for k in res[True]:
         assert_parity(f"sparse vs dense {k}", res[True][k], res[False][k])
+
+
+def test_forward_workspace_forms_agree(pkg, torch_dev):
+    """wha_wave_fwd with a caller workspace (exactly wha_wave_fwd_workspace_size
+    bytes) and with workspace NULL (the library-cached buffer) give the same
+    bits on the bucket-sparse family at a ragged T above 1024."""
+    import ctypes
+    torch, dev = torch_dev
+    B, T, E, H, C = 2, 1100, 256, 4, 16
+    print("wave forward workspace forms", flush=True)
+    w = make_wave_weights(H, C, E, seed=31)
+    x = np.random.default_rng(32).normal(size=(B, T, E)).astype(np.float32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    W = pkg.WaveAttnWeights(t(w["hraw"]), t(w["proj_w"]), t(w["proj_b"]), t(w["v_w"]), t(w["v_b"]), t(w["out_w"]),
+                            t(w["out_b"]))
+    tx = t(x)
+    shape = pkg.WaveShape(B, T, E, H, C)
+    need = pkg.wave_fwd_workspace_bytes(shape)
+    assert need > 0 and need % 4 == 0
+    prev = pkg.wave_set_bucket_sparse(True)
+    try:
+        res = []
+        for ws in (torch.empty(need // 4, dtype=torch.float32, device=dev), None):
+            cache = pkg.WaveAttnCache(shape, dev)
+            out = torch.empty_like(tx)
+            rc = pkg.lib().wha_wave_fwd(ctypes.c_void_p(tx.data_ptr()), ctypes.byref(W._c()), ctypes.byref(shape),
+                                        ctypes.c_void_p(out.data_ptr()), ctypes.byref(cache._c()),
+                                        None if ws is None else ctypes.c_void_p(ws.data_ptr()),
+                                        0 if ws is None else need, None)
+            assert rc == 0, pkg.lib().wha_last_error()
+            torch.cuda.synchronize()
+            res.append((out.cpu().numpy(), cache.merged.cpu().numpy(), cache.lse.cpu().numpy()))
+    finally:
+        pkg.wave_set_bucket_sparse(prev)
+    for a, b in zip(*res):
+        np.testing.assert_array_equal(a, b)

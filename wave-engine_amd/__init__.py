@@ -41,7 +41,7 @@ EXPORTED_SYMBOLS = (
     "wha_attn_bwd_from_probs_workspace_size", "wha_attn_bwd_from_probs",
     "wha_attn_scores_size", "wha_attn_fwd_keep", "wha_attn_bwd_kept",
     "wha_decode_workspace_size", "wha_decode_fwd", "wha_decode_fwd_noalloc", "wha_attn_probs_rows",
-    "wha_wave_fwd", "wha_wave_bwd_workspace_size", "wha_wave_bwd", "wha_wave_probs_rows",
+    "wha_wave_fwd_workspace_size", "wha_wave_fwd", "wha_wave_bwd_workspace_size", "wha_wave_bwd", "wha_wave_probs_rows",
     "wha_wave_set_bucket_sparse",
     "wha_wave_kv_prefill_workspace_size", "wha_wave_kv_prefill", "wha_wave_kv_decode_workspace_size",
     "wha_wave_kv_decode", "wha_host_wave_attention_forward", "wha_host_wave_attention_backward",
@@ -155,7 +155,9 @@ def lib():
         L.wha_attn_probs_rows.argtypes = [vp, vp, vp, ctypes.POINTER(ctypes.c_int32), i32, vp, lp, ctypes.c_float, vp]
         wsp, wwp = ctypes.POINTER(WaveShape), ctypes.POINTER(_WaveWeightsC)
         wcp, wgp = ctypes.POINTER(_WaveCacheC), ctypes.POINTER(_WaveGradsC)
-        L.wha_wave_fwd.argtypes = [vp, wwp, wsp, vp, wcp, vp]
+        L.wha_wave_fwd_workspace_size.argtypes = [wsp]
+        L.wha_wave_fwd_workspace_size.restype = sz
+        L.wha_wave_fwd.argtypes = [vp, wwp, wsp, vp, wcp, vp, sz, vp]
         L.wha_wave_bwd_workspace_size.argtypes = [wsp]
         L.wha_wave_bwd_workspace_size.restype = sz
         L.wha_wave_bwd.argtypes = [vp, vp, wwp, wsp, wcp, wgp, vp, sz, vp]
@@ -766,10 +768,17 @@ def _wave_x(x, weights: WaveAttnWeights):
     return x
 
 
-def wave_attention_forward(weights: WaveAttnWeights, x, n_bands=None, return_pathway_cache=True, out=None):
+def wave_fwd_workspace_bytes(shape: WaveShape) -> int:
+    return int(lib().wha_wave_fwd_workspace_size(ctypes.byref(shape)))
+
+
+def wave_attention_forward(weights: WaveAttnWeights, x, n_bands=None, return_pathway_cache=True, out=None,
+                           workspace=None):
     """wave_attention_forward (src/common/attn.rs:90-305) on x [B][T][n_embd]
     (or one sequence [T][n_embd]).  Returns (out, att_weights, cache): att_weights
-    is a WaveAttnRows view; cache is None unless return_pathway_cache."""
+    is a WaveAttnRows view; cache is None unless return_pathway_cache.
+    workspace: a float32 device tensor of at least wave_fwd_workspace_bytes
+    (allocated here when None)."""
     torch = _torch()
     x = _wave_x(x, weights)
     if n_bands is not None and 2 * n_bands != weights.n_embd:
@@ -780,8 +789,12 @@ def wave_attention_forward(weights: WaveAttnWeights, x, n_bands=None, return_pat
     cache.normed = x
     if out is None:
         out = torch.empty_like(x)
+    ws = workspace
+    if ws is None:
+        ws = torch.empty(wave_fwd_workspace_bytes(shape) // 4 + 64, dtype=torch.float32, device=x.device)
     _check("wha_wave_fwd", lib().wha_wave_fwd(_ptr(x), ctypes.byref(weights._c()), ctypes.byref(shape), _ptr(out),
-                                               ctypes.byref(cache._c()), _stream_ptr(x)))
+                                               ctypes.byref(cache._c()), _ptr(ws), ws.numel() * 4,
+                                               _stream_ptr(x)))
     return out, WaveAttnRows(cache), (cache if return_pathway_cache else None)
 
 

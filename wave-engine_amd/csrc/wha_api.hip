@@ -388,6 +388,40 @@ size_t wha_attn_scores_size(const wha_layout* layout) {
   return ds_bytes(layout);
 }
 
+// What the last wha_attn_fwd_keep into each score buffer did: whether it
+// wrote scores, and for which shape.  wha_attn_bwd_kept reads the scores only
+// when this record says they were written for its shape; otherwise it
+// recomputes them (always valid, since it has q, k and lse).  This keeps a
+// backward from reading scores the forward never wrote, e.g. when the forward
+// fell back on unaligned tensors and the backward gets aligned copies of them.
+namespace {
+struct ScoresRecord {
+  bool kept;
+  int32_t B, H, T, D;
+};
+std::mutex g_scores_mu;
+std::map<const void*, ScoresRecord> g_scores_rec;
+constexpr size_t kMaxScoresRecords = 4096;
+
+void record_scores(const float* scores, bool kept, const wha_layout* L) {
+  if (!scores) return;
+  std::lock_guard<std::mutex> lk(g_scores_mu);
+  // a dropped record only makes a backward recompute, so the table is simply
+  // reset when it grows past its bound
+  if (g_scores_rec.size() >= kMaxScoresRecords && !g_scores_rec.count(scores)) g_scores_rec.clear();
+  g_scores_rec[scores] = ScoresRecord{kept, L->B, L->H, L->T, L->D};
+}
+
+bool scores_recorded(const float* scores, const wha_layout* L) {
+  if (!scores) return false;
+  std::lock_guard<std::mutex> lk(g_scores_mu);
+  auto it = g_scores_rec.find(scores);
+  if (it == g_scores_rec.end()) return false;
+  const ScoresRecord& r = it->second;
+  return r.kept && r.B == L->B && r.H == L->H && r.T == L->T && r.D == L->D;
+}
+}  // namespace
+
 int wha_attn_fwd_keep(const float* q, const float* k, const float* v, float* o, float* lse, float* scores,
                       const wha_layout* layout, float scale, void* stream) {
   static const char* fn = "wha_attn_fwd_keep";
@@ -408,6 +442,7 @@ int wha_attn_fwd_keep(const float* q, const float* k, const float* v, float* o, 
   }
   hipError_t e = wha::launch_attn_fwd(q, k, v, o, lse, V, vec, scale, static_cast<hipStream_t>(stream),
                                       keep ? scores : nullptr);
+  record_scores(scores, keep && e == hipSuccess, layout);
   if (e != hipSuccess) return hip_fail(e, "wha_attn_fwd_keep launch");
   g_err[0] = 0;
   return WHA_OK;
@@ -425,11 +460,13 @@ int wha_attn_bwd_kept(const float* q, const float* k, const float* v, const floa
     return fail(WHA_ERR_INVALID, "%s: every tensor pointer must be non-NULL", fn);
   // Unaligned tensors: the recompute backward (the kept scores are not needed).
   const bool vec = vec_ok(V, {q, k, v, o, d_o, dq, dk, dv});
-  const bool keep = wha_attn_scores_size(layout) > 0 && vec;
+  bool keep = wha_attn_scores_size(layout) > 0 && vec;
   if (keep) {
     if (!scores) return fail(WHA_ERR_INVALID, "%s: scores must be non-NULL (wha_attn_scores_size > 0)", fn);
     if (reinterpret_cast<uintptr_t>(scores) & 15)
       return fail(WHA_ERR_INVALID, "%s: scores must be 16-byte aligned", fn);
+    // only scores the forward actually wrote for this shape are read
+    keep = scores_recorded(scores, layout);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   void* ws = nullptr;
@@ -661,14 +698,32 @@ static bool wave_sparse_on(const wha_wave_shape* sh) {
   return (mode == 1 || (mode == 2 && sh->T >= kWaveSparseMinT)) && wave_sparse_fits(sh);
 }
 
+// Scratch of the bucket-sparse forward (sorted operand copies), in bytes; 0
+// when the shape never takes that family.
+static size_t wave_fwd_sparse_bytes(const wha_wave_shape* sh) {
+  if (!wave_sparse_fits(sh)) return 0;
+  return round256(wha::wave_sparse_fwd_floats(sh->B, sh->n_head, sh->T, sh->n_embd / sh->n_head) * sizeof(float));
+}
+
+size_t wha_wave_fwd_workspace_size(const wha_wave_shape* shape) {
+  if (check_wave_shape(shape, "wha_wave_fwd_workspace_size") != WHA_OK) return 0;
+  return wave_fwd_sparse_bytes(shape);
+}
+
 int wha_wave_fwd(const float* x, const wha_wave_weights* w, const wha_wave_shape* shape, float* out,
-                 const wha_wave_cache* cache, void* stream) {
+                 const wha_wave_cache* cache, void* workspace, size_t workspace_bytes, void* stream) {
   static const char* fn = "wha_wave_fwd";
   int rc;
   if ((rc = check_wave_shape(shape, fn)) || (rc = check_wave_weights(w, fn)) || (rc = check_wave_cache(cache, fn)))
     return rc;
   if (!x || !out) return fail(WHA_ERR_INVALID, "%s: x and out must be non-NULL", fn);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // The scratch is resolved before anything is enqueued, so a too-small
+  // workspace leaves every output untouched.
+  const bool sparse = wave_sparse_on(shape);
+  void* ws = nullptr;
+  if (sparse && (rc = resolve_workspace(workspace, workspace_bytes, wave_fwd_sparse_bytes(shape), s, fn, &ws)))
+    return rc;
   const int B = shape->B, T = shape->T, E = shape->n_embd, H = shape->n_head, C = shape->content_dim;
   const int hd = E / H, HP = H * (2 + C), M = B * T;
   const wha::View Lv = wave_view(shape);
@@ -681,10 +736,8 @@ int wha_wave_fwd(const float* x, const wha_wave_weights* w, const wha_wave_shape
     e = wha::launch_wave_features(cache->proj, w->harmonic_raw, cache->feat, cache->phase, cache->bucket, B, H, T,
                                   C, C, s);
   const bool vec = vec_ok(Lv, {cache->values, cache->merged});
-  if (e == hipSuccess && wave_sparse_on(shape)) {
-    // sorted copies of the operands: library scratch (the backward sorts again)
-    void* ws = nullptr;
-    if ((rc = cached_workspace(wha::wave_sparse_fwd_floats(B, H, T, hd) * sizeof(float), s, &ws))) return rc;
+  if (e == hipSuccess && sparse) {
+    // sorted copies of the operands (the backward sorts again)
     e = wha::launch_wave_fwd_sparse(cache->feat, cache->bucket, cache->values, cache->merged, cache->lse,
                                     static_cast<float*>(ws), Lv, vec, cs, s);
   } else if (e == hipSuccess) {
@@ -906,7 +959,8 @@ int wha_host_wave_attention_forward(const float* x, const wha_wave_weights* w, i
   const WaveHostSizes z = wave_host_sizes(T, E, H, C);
   float* base = nullptr;
   hipStream_t s = nullptr;
-  if ((rc = host_stage(wave_host_weight_bytes(z) + wave_host_cache_bytes(z) + 2 * seg(z.te), &base, &s)))
+  const size_t fws_bytes = wha_wave_fwd_workspace_size(&sh);
+  if ((rc = host_stage(wave_host_weight_bytes(z) + wave_host_cache_bytes(z) + 2 * seg(z.te) + fws_bytes, &base, &s)))
     return rc;
   Carve cv{base, 0};
   wha_wave_weights dw;
@@ -914,9 +968,10 @@ int wha_host_wave_attention_forward(const float* x, const wha_wave_weights* w, i
   float* dx = cv.take(z.te);
   float* dout = cv.take(z.te);
   const wha_wave_cache dc = carve_wave_cache(cv, z);
+  void* fws = fws_bytes ? cv.take(fws_bytes / sizeof(float)) : nullptr;
   if (e == hipSuccess) e = hipMemcpyAsync(dx, x, z.te * sizeof(float), hipMemcpyHostToDevice, s);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync H2D");
-  if ((rc = wha_wave_fwd(dx, &dw, &sh, dout, &dc, s))) return rc;
+  if ((rc = wha_wave_fwd(dx, &dw, &sh, dout, &dc, fws, fws_bytes, s))) return rc;
   e = hipMemcpyAsync(out, dout, z.te * sizeof(float), hipMemcpyDeviceToHost, s);
   if (e == hipSuccess && phase_out)
     e = hipMemcpyAsync(phase_out, dc.phase, z.ht * sizeof(float), hipMemcpyDeviceToHost, s);
@@ -942,10 +997,13 @@ int wha_host_wave_attention_backward(const float* x, const float* d_attn_out, co
   const bool full = n_set == 7;
   const WaveHostSizes z = wave_host_sizes(T, E, H, C);
   const size_t ws_bytes = wha_wave_bwd_workspace_size(&sh);
+  // the forward's scratch is dead by the time the backward runs: both share it
+  const size_t shared_bytes = std::max(ws_bytes, wha_wave_fwd_workspace_size(&sh));
   const size_t grad_bytes = full ? wave_host_weight_bytes(z) : 0;
   float* base = nullptr;
   hipStream_t s = nullptr;
-  if ((rc = host_stage(wave_host_weight_bytes(z) + wave_host_cache_bytes(z) + 4 * seg(z.te) + grad_bytes + ws_bytes,
+  if ((rc = host_stage(wave_host_weight_bytes(z) + wave_host_cache_bytes(z) + 4 * seg(z.te) + grad_bytes +
+                           shared_bytes,
                        &base, &s)))
     return rc;
   Carve cv{base, 0};
@@ -960,11 +1018,11 @@ int wha_host_wave_attention_backward(const float* x, const float* d_attn_out, co
   float* dg[7] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
   if (full)
     for (int i = 0; i < 7; ++i) dg[i] = cv.take(n[i]);
-  void* ws = cv.take(ws_bytes / sizeof(float));
+  void* ws = cv.take(shared_bytes / sizeof(float));
   if (e == hipSuccess) e = hipMemcpyAsync(dx_in, x, z.te * sizeof(float), hipMemcpyHostToDevice, s);
   if (e == hipSuccess) e = hipMemcpyAsync(dout_in, d_attn_out, z.te * sizeof(float), hipMemcpyHostToDevice, s);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync H2D");
-  if ((rc = wha_wave_fwd(dx_in, &dw, &sh, fwd_out, &dc, s))) return rc;
+  if ((rc = wha_wave_fwd(dx_in, &dw, &sh, fwd_out, &dc, ws, shared_bytes, s))) return rc;
   const wha_wave_grads dgr{d_x, dg[0], dg[1], dg[2], dg[3], dg[4], dg[5], dg[6]};
   if ((rc = wha_wave_bwd(dx_in, dout_in, &dw, &sh, &dc, &dgr, ws, ws_bytes, s))) return rc;
   e = hipMemcpyAsync(g->d_x, d_x, z.te * sizeof(float), hipMemcpyDeviceToHost, s);
