@@ -7,7 +7,16 @@ right after `buffer_store_dwordx4 v[100:103]` (and `v_or_b32 v100, ...` after th
 last store).  The stored scores then came out wrong in exactly those elements,
 only in blocks that shared a CU with another block.  Every kernel of the library
 is compiled to device assembly here and scanned for a store whose next
-instruction writes one of its data VGPRs.  No GPU needed."""
+instruction writes one of its data VGPRs.
+
+The compiler inserts the wait states an MFMA result needs before a VALU
+instruction reads it (about a dozen for v_mfma_f32_16x16x4_f32), and before an
+instruction overwrites a register an MFMA still reads, only for instructions it
+generates itself: inline assembly is invisible to that bookkeeping.  An
+inline-asm v_max3_f32 over a score chain's accumulators once came directly
+after the chain's last MFMA and read stale values (the running maximum of
+whole waves came out wrong).  The kernels therefore contain no inline
+assembly; the second check keeps it that way.  No GPU needed."""
 import re
 import subprocess
 from pathlib import Path
@@ -75,3 +84,34 @@ def test_no_store_data_overwritten_by_the_next_instruction():
     assert len(files) >= 10
     hits = [(f.name, *h) for f in files for h in scan(f.read_text())]
     assert hits == [], "\n".join(f"{f}:{n}: {s} / {nx}" for f, n, s, nx in hits)
+
+
+def asm_instructions(text):
+    """(line number, instruction) of every instruction inside an inline-asm
+    block; empty blocks (compiler barriers, asm volatile("" ::: "memory"))
+    emit nothing and are not reported."""
+    found, inside = [], False
+    for n, line in enumerate(text.splitlines()):
+        if ";;#ASMSTART" in line:
+            inside = True
+        elif ";;#ASMEND" in line:
+            inside = False
+        elif inside and not SKIP.match(line):
+            found.append((n + 1, line.strip()))
+    return found
+
+
+def test_asm_scanner():
+    barrier = "\t;;#ASMSTART\n\t;;#ASMEND\n\tv_add_f32_e32 v1, v2, v3\n"
+    asm_max = "\tv_mfma_f32_16x16x4_f32 v[48:51], v51, v121, v[44:47]\n\t;;#ASMSTART\n\tv_max_f32 v4, v48, v49\n\t;;#ASMEND\n"
+    assert asm_instructions(barrier) == []
+    assert asm_instructions(asm_max) == [(3, "v_max_f32 v4, v48, v49")]
+
+
+def test_no_inline_assembly_in_kernels():
+    """Inline asm bypasses the compiler's MFMA hazard handling (module docstring)."""
+    subprocess.run(["make", "-s", "-C", str(PKG), "-j8", "isa"], check=True, timeout=900)
+    files = sorted((PKG / "_build" / "isa").glob("*.s"))
+    assert len(files) >= 10
+    hits = [(f.name, *h) for f in files for h in asm_instructions(f.read_text())]
+    assert hits == [], f"inline assembly in device code: {hits[:10]}"

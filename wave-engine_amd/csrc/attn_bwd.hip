@@ -88,15 +88,17 @@ __global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const float* __rest
 }
 
 // Row statistics for attn_bwd_dkv_dma_kernel, per (b,h) in blocks of 32 rows
-// (Tb = T rounded up to 32): block j holds -LSE_t*log2(e) for t = 32j..32j+31,
+// (Tb = T rounded up to 32): block j holds -LSE_t*lse_mult for t = 32j..32j+31,
 // then -Delta_t for the same rows (rows past T hold 0).  The key-stationary
 // kernel fetches a block with one 256-byte load and starts its S and dP
-// accumulators from it, so p = exp2(acc) and dS = p * acc need no further
-// arithmetic.  Same 16-lanes-per-row dot product as attn_bwd_delta_kernel.
+// accumulators from it.  lse_mult is log2(e) when S comes in log2 units (the
+// kept scores: p = exp2(acc)) and 1/scale when S is recomputed from raw Q and
+// K (acc is then in dot-product units and p = exp2(acc * scale*log2(e))).
+// Same 16-lanes-per-row dot product as attn_bwd_delta_kernel.
 __global__ __launch_bounds__(256) void attn_bwd_stats_kernel(const float* __restrict__ O,
                                                              const float* __restrict__ dO,
                                                              const float* __restrict__ LSE,
-                                                             float* __restrict__ stats, View L) {
+                                                             float* __restrict__ stats, View L, float lse_mult) {
   // block: rows t0 .. t0+63 of head bh (two 32-row stats blocks); 16 lanes per
   // row, kDeltaRows consecutive rows per 16-lane group; no 64-bit divisions
   const int Tb = (L.T + 31) / 32 * 32;
@@ -139,7 +141,7 @@ __global__ __launch_bounds__(256) void attn_bwd_stats_kernel(const float* __rest
     const int t = t0 + 32 * blk + rr;
     if (t0 + 32 * blk < Tb) {
       const int i = 32 * blk + rr;
-      const float v = t < L.T ? (half ? -del_s[i] : -lse_s[i] * kLog2e) : 0.f;
+      const float v = t < L.T ? (half ? -del_s[i] : -lse_s[i] * lse_mult) : 0.f;
       stats[((int64_t)bh * (Tb / 32) + t0 / 32 + blk) * 64 + 32 * half + rr] = v;
     }
   }
@@ -256,11 +258,14 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
     const int key0 = kt * BN;
     if (key0 > q0 + 15) continue;
 
+    // S starts from -LSE*log2(e) and dP from -Delta of this lane's query, so
+    // the large partial sums of S cancel in the first steps (Delta is 0 in the
+    // kDeltaFromProbs pass, which needs dP itself)
     floatx4 s[NKT], dp[NKT];
 #pragma unroll
     for (int mt = 0; mt < NKT; ++mt) {
-      s[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      dp[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      s[mt] = floatx4{-lse2, -lse2, -lse2, -lse2};
+      dp[mt] = floatx4{-delta, -delta, -delta, -delta};
     }
 #pragma unroll
     for (int j = 0; j < DG / 4; ++j) {
@@ -291,7 +296,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
         const bool valid = 16 * mt + 4 * g + i <= key_lim;
         float p;
         if (MODE == kFused) {
-          p = fast_exp2(s[mt][i] - lse2);
+          p = fast_exp2(s[mt][i]);
           p = valid ? p : 0.f;
         } else {
           p = valid ? acur[4 * mt + i] : 0.f;
@@ -299,7 +304,7 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dq_kernel(
         if (MODE == kDeltaFromProbs) {
           dsum += p * dp[mt][i];
         } else {
-          dp[mt][i] = p * (dp[mt][i] - delta);
+          dp[mt][i] = p * dp[mt][i];
         }
       }
     }
@@ -360,8 +365,12 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
   const int k0w = kt * BNK + wave * 16;  // first key of this wave
   const int krow = k0w + lq;             // this lane's key
 
+  // K unscaled: S is the plain dot product started from -LSE/scale, and
+  // scale*log2(e) is applied per score in the exponent (the forward's rounding
+  // of q*scale*log2(e) is common to a row's keys; a per-key rounding here
+  // would not be, and dQ = dS K amplifies that mismatch by the size of K)
   float kf[PROBS ? 1 : DG];
-  if (!PROBS) load_row_frag<DP, VEC>(K + base, krow, L.T, L.D, L.st, g, scale_log2, kf);
+  if (!PROBS) load_row_frag<DP, VEC>(K + base, krow, L.T, L.D, L.st, g, 1.f, kf);
   float vf[DG];
   load_row_frag<DP, VEC>(V + base, krow, L.T, L.D, L.st, g, 1.f, vf);
 
@@ -410,8 +419,8 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
     qs.store_tile(Qs, tid);
     os.store_tile(Os, tid);
     if (tid < BMQ) {
-      lse_s[tid] = lse_r * kLog2e;
-      del_s[tid] = del_r;
+      lse_s[tid] = -lse_r / scale;
+      del_s[tid] = -del_r;
     }
     if (PROBS) {
 #pragma unroll
@@ -423,11 +432,14 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
     if (qb + BMQ - 1 < k0w) continue;  // every query of the tile precedes every key of the wave
     const int q_end = krow < L.T ? L.T : 0;  // valid queries: krow <= q < q_end
 
+    // S and dP start from -LSE/scale and -Delta of their rows (lane element
+    // (mt,i): query qb+16mt+4g+i), so the large partial sums of S cancel in
+    // the first steps and dS = P * dP needs no subtraction
     floatx4 s[NQT], dp[NQT];
 #pragma unroll
     for (int mt = 0; mt < NQT; ++mt) {
-      s[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      dp[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      s[mt] = *reinterpret_cast<const floatx4*>(&lse_s[16 * mt + 4 * g]);
+      dp[mt] = *reinterpret_cast<const floatx4*>(&del_s[16 * mt + 4 * g]);
     }
     // S and dP: 2*NQT independent accumulator chains, interleaved step by step
 #pragma unroll
@@ -452,28 +464,23 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
       }
     }
 
-    // lane element (mt,i): query qb+16mt+4g+i, key krow.  The row statistics of
-    // the four queries 16mt+4g+0..3 come in one 128-bit LDS broadcast read; masking
-    // is a select, so no branch sits between the MFMA blocks.
+    // lane element (mt,i): query qb+16mt+4g+i, key krow; masking is a select,
+    // so no branch sits between the MFMA blocks.
 #pragma unroll
     for (int mt = 0; mt < NQT; ++mt) {
-      const float4 l4 = *reinterpret_cast<const float4*>(&lse_s[16 * mt + 4 * g]);
-      const float4 d4 = *reinterpret_cast<const float4*>(&del_s[16 * mt + 4 * g]);
-      const float lq4[4] = {l4.x, l4.y, l4.z, l4.w};
-      const float dq4[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int q = qb + 16 * mt + 4 * g + i;
         const bool valid = (q >= krow) & (q < q_end);
         float p;
         if (!PROBS) {
-          p = fast_exp2(s[mt][i] - lq4[i]);
+          p = fast_exp2(s[mt][i] * scale_log2);
           p = valid ? p : 0.f;
         } else {
           p = valid ? acur[4 * mt + i] : 0.f;
         }
         s[mt][i] = p;
-        dp[mt][i] = p * (dp[mt][i] - dq4[i]);
+        dp[mt][i] = p * dp[mt][i];
       }
     }
 
@@ -527,8 +534,9 @@ __global__ __launch_bounds__(NW * 64) void attn_bwd_dkv_kernel(
 //     one slot from the loads into the other and does not wait for those loads
 //     before reading;
 //   - the row statistics arrive as one 256-byte block per sub-tile
-//     (attn_bwd_stats_kernel: -LSE*log2(e), then -Delta) and initialise the S
-//     and dP accumulators, so P = exp2(S) and dS = P * dP;
+//     (attn_bwd_stats_kernel: -LSE*log2(e) or -LSE/scale, then -Delta) and
+//     initialise the S and dP accumulators, so P = exp2(S) (kept scores) or
+//     exp2(S * scale*log2(e)) (recomputed) and dS = P * dP;
 //   - masking runs only on sub-tiles that touch the diagonal or the end of the
 //     sequence (a wave-uniform test);
 //   - Q and dO sit in the swizzled Lds<DP> layout (a DMA instruction fills 64
@@ -666,8 +674,15 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
     const int kt = pass == 0 ? pair : n_kt - 1 - pair;
     const int k0w = kt * 64 + wave * 16;
     const int krow = k0w + lq;
+    // K unscaled: the recomputed S is the plain dot product q.k (started from
+    // -LSE/scale), and scale*log2(e) is applied once per score in the
+    // exponent.  The forward forms q*(scale*log2(e)) . k, whose rounding is
+    // common to every key of a row and cancels against its LSE; scaling K
+    // here instead would round each key's scores differently from the
+    // forward's, and dQ = dS K amplifies such a per-key mismatch by the size
+    // of K wherever large scores come from a large shared key component.
     float kf[SAVED ? 1 : DG], vf[DG];
-    if constexpr (!SAVED) load_row_frag_dma<DP>(K + base, krow, L.T, L.D, L.st, g, scale_log2, kf);
+    if constexpr (!SAVED) load_row_frag_dma<DP>(K + base, krow, L.T, L.D, L.st, g, 1.f, kf);
     load_row_frag_dma<DP>(V + base, krow, L.T, L.D, L.st, g, 1.f, vf);
     floatx4 dkacc[NDT], dvacc[NDT];
 #pragma unroll
@@ -712,7 +727,8 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
     auto compute = [&](auto masked, int qb, const float* Qs, const float* Os, const float* Sts,
                        const float (&sc)[8]) {
       constexpr bool MASKED = decltype(masked)::value;
-      // S (log2 units) and dP, started from -LSE*log2(e) and -Delta of their rows
+      // S and dP, started from the rows' -LSE*log2(e) (kept scores) or
+      // -LSE/scale (recompute) and -Delta
       floatx4 s[2], dp[2];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
@@ -748,7 +764,7 @@ __global__ __launch_bounds__(256) WHA_DMA_WPE(DP) void attn_bwd_dkv_dma_kernel(
       for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p = PROBS ? s[mt][i] : fast_exp2(s[mt][i]);
+          const float p = PROBS ? s[mt][i] : fast_exp2(SAVED ? s[mt][i] : s[mt][i] * scale_log2);
           if (MASKED) {
             const int q = qb + 16 * mt + arow(4 * g + i);
             const bool valid = (q >= krow) & (q < q_end);
@@ -1091,7 +1107,10 @@ hipError_t bwd_dma_t(const float* q, const float* k, const float* v, const float
   {
     TimingScope ts("attn_bwd_delta", stream);
     const int64_t blocks = (int64_t)L.B * L.H * (((L.T + 31) / 32 * 32 + 63) / 64);
-    hipLaunchKernelGGL(attn_bwd_stats_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, o, d_o, lse, stats, L);
+    // kept scores are in log2 units; the recompute works in dot-product units
+    const float lse_mult = sc != nullptr ? kLog2e : (float)(1.0 / (double)scale);
+    hipLaunchKernelGGL(attn_bwd_stats_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, o, d_o, lse, stats, L,
+                       lse_mult);
     e = hipGetLastError();
   }
   if (e != hipSuccess) return e;

@@ -56,7 +56,9 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
   const int64_t base = (int64_t)b * L.sb + (int64_t)h * L.sh;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  // wave index as a scalar: conditions derived from it compile to scalar
+  // branches, never to EXEC-masked blocks (which MFMAs would not respect)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lq = lane & 15, g = lane >> 4;
   const int q0 = qt * BM + wave * 16;  // first query of this wave
   const int qrow = q0 + lq;            // this lane's query
@@ -71,7 +73,21 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
   ks.load(K + base, 0, L.T, L.D, L.st, tid);
   vs.load(V + base, 0, L.T, L.D, L.st, tid);
 
-  float m_i = -INFINITY, l_i = 0.f;
+  // Running max m_i, started from an anchor (this query's score against key
+  // 0, the first key of the sweep) and moved only by exact steps.  Every
+  // tile's S accumulators start from -m_i, so the fused multiply-add chain of
+  // the MFMA keeps its partial sums near 0 instead of rounding scores of tens
+  // of units at every step (the backward, started from -LSE, then sees the
+  // probabilities this forward normalised).
+  float m_i, l_i = 0.f;
+  {
+    float kfa[DG];
+    load_row_frag<DP, VEC>(K + base, 0, L.T, L.D, L.st, g, 1.f, kfa);
+    float a = 0.f;
+#pragma unroll
+    for (int t = 0; t < DG; ++t) a = fmaf(qf[t], kfa[t], a);
+    m_i = pair_sum32(pair_sum16(a));  // identical in the query's four lane groups
+  }
   floatx4 oacc[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) oacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -88,49 +104,66 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
     const int key0 = kt * BN;
     if (key0 > q0 + 15) continue;  // every key of the tile is after every query of the wave
 
-    // S^T[key][query] (already in log2 units); four independent accumulator chains
+    // S^T[key][query] - m_i (log2 units); four independent accumulator chains
     floatx4 s[NKT];
-#pragma unroll
-    for (int mt = 0; mt < NKT; ++mt) s[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < DG / 4; ++j) {
-      float4 a[NKT];
-#pragma unroll
-      for (int mt = 0; mt < NKT; ++mt)
-        a[mt] = lds_read_quad<DP>(Ks, 16 * mt + lq, g * (DG / 4) + j);
-#pragma unroll
-      for (int mt = 0; mt < NKT; ++mt) s[mt] = mfma4(a[mt].x, qf[4 * j + 0], s[mt]);
-#pragma unroll
-      for (int mt = 0; mt < NKT; ++mt) s[mt] = mfma4(a[mt].y, qf[4 * j + 1], s[mt]);
-#pragma unroll
-      for (int mt = 0; mt < NKT; ++mt) s[mt] = mfma4(a[mt].z, qf[4 * j + 2], s[mt]);
-#pragma unroll
-      for (int mt = 0; mt < NKT; ++mt) s[mt] = mfma4(a[mt].w, qf[4 * j + 3], s[mt]);
-    }
-
-    // causal / tail mask, running max (one query per lane; keys over 16 values
-    // in the lane and the 4 lane groups)
-    // keys above key_lim are masked: one compare and a select per score, no branch
+    // causal / tail mask: keys above key_lim, one compare and a select per
+    // score, no branch
     const int key_lim = min(qrow, L.T - 1) - key0;
-    float mx = -INFINITY;
+    auto scores = [&]() {
 #pragma unroll
-    for (int mt = 0; mt < NKT; ++mt) {
+      for (int mt = 0; mt < NKT; ++mt) s[mt] = floatx4{-m_i, -m_i, -m_i, -m_i};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float x = (16 * mt + 4 * g + i > key_lim) ? -INFINITY : s[mt][i];
-        s[mt][i] = x;
-        mx = fmaxf(mx, x);
+      for (int j = 0; j < DG / 4; ++j) {
+        float4 a[NKT];
+#pragma unroll
+        for (int mt = 0; mt < NKT; ++mt)
+          a[mt] = lds_read_quad<DP>(Ks, 16 * mt + lq, g * (DG / 4) + j);
+#pragma unroll
+        for (int mt = 0; mt < NKT; ++mt) s[mt] = mfma4(a[mt].x, qf[4 * j + 0], s[mt]);
+#pragma unroll
+        for (int mt = 0; mt < NKT; ++mt) s[mt] = mfma4(a[mt].y, qf[4 * j + 1], s[mt]);
+#pragma unroll
+        for (int mt = 0; mt < NKT; ++mt) s[mt] = mfma4(a[mt].z, qf[4 * j + 2], s[mt]);
+#pragma unroll
+        for (int mt = 0; mt < NKT; ++mt) s[mt] = mfma4(a[mt].w, qf[4 * j + 3], s[mt]);
       }
+#pragma unroll
+      for (int mt = 0; mt < NKT; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[mt][i] = (16 * mt + 4 * g + i > key_lim) ? -INFINITY : s[mt][i];
+      }
+    };
+    // Running max (one query per lane; keys over 16 values in the lane and
+    // the 4 lane groups).  Every lane has a valid key here (key0 <= q0), so
+    // mx is finite; the first tile holds the anchor's key, so there mx >= 0.
+    // Scores far above the maximum they started from were summed at their
+    // own size: then the tile's scores are formed again from the new maximum
+    // (a second trip, whose scores are all <= 0; a loop rather than a second
+    // copy of the contraction, which would hold more registers).
+    float alpha = 1.f, dd;
+    for (;;) {
+      scores();
+      float mx = -INFINITY;
+#pragma unroll
+      for (int mt = 0; mt < NKT; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[mt][i]);
+      }
+      const bool redo = __builtin_amdgcn_ballot_w64(mx > kRedoMax) != 0;
+      mx = pair_max32(pair_max16(mx));
+      const float m_new = m_i + fmaxf(mx, 0.f);
+      dd = m_new - m_i;  // exact step of the float maximum
+      alpha *= fast_exp2(-dd);
+      if (!redo) break;
+      m_i = m_new;
     }
-    mx = pair_max32(pair_max16(mx));
-    const float m_new = fmaxf(m_i, mx);
-    const float alpha = fast_exp2(m_i - m_new);
+    const float m_new = m_i + dd;
     float rs = 0.f;
 #pragma unroll
     for (int mt = 0; mt < NKT; ++mt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = fast_exp2(s[mt][i] - m_new);
+        const float p = fast_exp2(s[mt][i] - dd);
         s[mt][i] = p;
         rs += p;
       }
@@ -188,7 +221,9 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(const float* __restri
 // (src/common/compute.rs:391-399 -> :286-314): the key-stationary backward then
 // reads them instead of recomputing Q K^T.  Entries after the diagonal hold
 // whatever the key tile gave (the backward masks them); rows past T are
-// written too (the layout pads every block to a multiple of 64 rows).
+// written too (the layout pads every block to a multiple of 64 rows).  A
+// sub-tile whose scores are formed again (see the rescale below) is stored
+// again.
 // DELTA: the Delta pass of the from-probabilities backward on the same tiles:
 // Q is dO, K is V (scale 1), so the score contraction forms dP^T; each lane
 // takes sum_j att[q][j] dP[q][j] over its keys (att given, read one sub-tile
@@ -310,7 +345,15 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
     load_row_frag_dma<DP>(Q + base, qrow, L.T, L.D, L.st, g, scale_log2, qf);
     // running max m_i (log2 units) and row sum; -m_i in every element of neg_m,
     // from which the S accumulators start (MFMA srcC), so the scores come out
-    // already shifted by the running max.  The first sub-tile sets m_i exactly.
+    // already shifted by the running max.  The MFMA accumulates as a chain of
+    // fused multiply-adds, so starting near the row's scores keeps every
+    // partial sum small and its rounding fine; summed from 0, scores of tens
+    // of units pick up an ulp of their own size at every step, and the
+    // backward, which starts from -LSE, would then see different
+    // probabilities than the forward normalised (dQ = dS K amplifies that by
+    // the size of K).  The first sub-tile starts from 0 and sets m_i; when
+    // its maximum is more than kRedoMax from 0 its scores are formed again
+    // from that maximum.  m_i then moves only by exact steps.
     float m_i = 0.f, l_i = 0.f;
     bool fresh = true;
     floatx4 neg_m = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -341,22 +384,44 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
 
     auto compute = [&](auto masked, int k0, const float* Ks, const float* Vs, const floatx4 (&at)[NKT]) {
       constexpr bool MASKED = decltype(masked)::value;
-      // S^T[key][query] in log2 units: MFMA rows are keys 16mt + arow(lq), columns the wave's queries
+      // S^T[key][query] - m_i in log2 units: MFMA rows are keys 16mt + arow(lq), columns the wave's queries
       floatx4 s[NKT];
+      auto scores = [&]() {
 #pragma unroll
-      for (int mt = 0; mt < NKT; ++mt) {
-        WHA_FENCE();
+        for (int mt = 0; mt < NKT; ++mt) {
+          WHA_FENCE();
 #pragma unroll
-        for (int j = 0; j < DG / 4; ++j) {
-          const float4 a = lds_read_quad<DP, true>(Ks, 16 * mt + arow(lq), dma48_quad<DP>(g, j));
-          s[mt] = mfma4(a.x, qf[4 * j + 0], j == 0 ? neg_m : s[mt]);
-          s[mt] = mfma4(a.y, qf[4 * j + 1], s[mt]);
-          s[mt] = mfma4(a.z, qf[4 * j + 2], s[mt]);
-          s[mt] = mfma4(a.w, qf[4 * j + 3], s[mt]);
+          for (int j = 0; j < DG / 4; ++j) {
+            const float4 a = lds_read_quad<DP, true>(Ks, 16 * mt + arow(lq), dma48_quad<DP>(g, j));
+            s[mt] = mfma4(a.x, qf[4 * j + 0], j == 0 ? neg_m : s[mt]);
+            s[mt] = mfma4(a.y, qf[4 * j + 1], s[mt]);
+            s[mt] = mfma4(a.z, qf[4 * j + 2], s[mt]);
+            s[mt] = mfma4(a.w, qf[4 * j + 3], s[mt]);
+          }
         }
-      }
-      WHA_FENCE();
+        WHA_FENCE();
+      };
+      // SAVE: the raw scores (s + m_i, before masking) of this sub-tile
+      auto keep = [&]() {
+        if constexpr (SAVE) {
+          const int kt = k0 >> 6;
+          const int sc_blk = (int)(((ds_block_row(kt, L.T) - (int64_t)64 * kt) * 64 + (k0 & 63)) * 4);
+#pragma unroll
+          for (int mt = 0; mt < NKT; ++mt) buffer_store_quad(rsc, s[mt] - neg_m, sc_lane, sc_blk + 64 * mt);
+        }
+      };
+      auto mask = [&]() {
+        if (MASKED) {
+#pragma unroll
+          for (int mt = 0; mt < NKT; ++mt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              s[mt][i] = (k0 + 16 * mt + arow(4 * g + i) > key_last) ? -INFINITY : s[mt][i];
+          }
+        }
+      };
       if constexpr (DELTA) {
+        scores();
         // lane element (mt,i): dP of key k0 + 16mt + 4g + i and query qrow
 #pragma unroll
         for (int mt = 0; mt < NKT; ++mt) {
@@ -368,55 +433,61 @@ __global__ __launch_bounds__(256) WHA_FWD_WPE void attn_fwd_dma_kernel(const flo
         }
         return;
       }
-      // lane element (mt,i): key k0 + 16mt + arow(4g+i) of query qrow, as s - m_i;
-      // kept at column 16mt + 4g + i of the score layout, which at DP = 48
-      // therefore holds the keys of each 16-column group in tr16 order
-      if constexpr (SAVE) {
-        const int kt = k0 >> 6;
-        const int sc_blk = (int)(((ds_block_row(kt, L.T) - (int64_t)64 * kt) * 64 + (k0 & 63)) * 4);
+      // Scores more than kLazyMax above the value the accumulators started
+      // from (more than kRedoMax from 0 in the first sub-tile) were summed at
+      // their own size; in that (rare) case the sub-tile's scores are formed
+      // again from the new maximum, so every score that carries weight comes
+      // out of a chain of small partial sums.  A loop of at most two trips
+      // (the second trip's scores lie at or below the new maximum) keeps one
+      // copy of the contraction.  The branches are wave-uniform scalars
+      // (readfirstlane of a value every lane shares, or a ballot): the MFMAs
+      // they hold ignore the EXEC mask, so these blocks must never run under
+      // a partial or empty one.
+      for (;;) {
+        scores();
+        // lane element (mt,i): key k0 + 16mt + arow(4g+i) of query qrow, as s - m_i;
+        // kept at column 16mt + 4g + i of the score layout, which at DP = 48
+        // therefore holds the keys of each 16-column group in tr16 order
+        keep();
+        mask();
+        // largest shifted score among this lane's keys; the query's maximum
+        // (over the 4 lane groups) is formed only where it is used -- the
+        // first sub-tile and a rescale -- since some lane's maximum passes
+        // kLazyMax exactly when some query's does (three-input maxima only: a
+        // two-input max quiets its operands first)
+        float mx;
+        if constexpr (NKT == 2)
+          mx = vmax3(vmax3(s[0][0], s[0][1], s[0][2]), vmax3(s[0][3], s[1][0], s[1][1]),
+                     vmax3(s[1][2], s[1][3], s[0][0]));
+        else
+          mx = vmax3(vmax3(s[0][0], s[0][1], s[0][2]), s[0][3], s[0][0]);
+        if (__builtin_amdgcn_readfirstlane((int)fresh)) {
+          // first sub-tile: the running max is this one's (k0 <= every query
+          // here, so every lane has a finite score)
+          asm volatile("" ::: "memory");
+          fresh = false;
+          mx = pair_max32(pair_max16(mx));
+          m_i = mx;
+          neg_m = floatx4{-m_i, -m_i, -m_i, -m_i};
+          if (__builtin_amdgcn_ballot_w64(fabsf(mx) > kRedoMax) != 0) continue;
 #pragma unroll
-        for (int mt = 0; mt < NKT; ++mt) buffer_store_quad(rsc, s[mt] - neg_m, sc_lane, sc_blk + 64 * mt);
-      }
-      if (MASKED) {
+          for (int mt = 0; mt < NKT; ++mt) s[mt] -= mx;
+        } else if (__builtin_amdgcn_ballot_w64(mx > kLazyMax) != 0) {
+          // a real branch (not if-converted): rescale to the new max, by the
+          // exact step between the old and the new float maximum, and form
+          // the scores again from it
+          asm volatile("" ::: "memory");
+          mx = pair_max32(pair_max16(mx));
+          const float m_new = m_i + fmaxf(mx, 0.f);
+          const float alpha = fast_exp2(-(m_new - m_i));  // the max grows by this exact step
+          l_i *= alpha;
 #pragma unroll
-        for (int mt = 0; mt < NKT; ++mt) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            s[mt][i] = (k0 + 16 * mt + arow(4 * g + i) > key_last) ? -INFINITY : s[mt][i];
+          for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
+          m_i = m_new;
+          neg_m = floatx4{-m_i, -m_i, -m_i, -m_i};
+          continue;
         }
-      }
-      // largest shifted score among this lane's keys; the query's maximum (over
-      // the 4 lane groups) is formed only where it is used -- the first
-      // sub-tile and a rescale -- since some lane's maximum passes kLazyMax
-      // exactly when some query's does
-      float mx;
-      if constexpr (NKT == 2)
-        mx = vmax3(vmax3(s[0][0], s[0][1], s[0][2]), vmax3(s[0][3], s[1][0], s[1][1]), vmax2(s[1][2], s[1][3]));
-      else
-        mx = vmax3(vmax2(s[0][0], s[0][1]), s[0][2], s[0][3]);
-      if (fresh) {
-        // first sub-tile: the running max is this one's (k0 <= every query here,
-        // so every lane has a finite score)
-        asm volatile("" ::: "memory");
-        fresh = false;
-        mx = pair_max32(pair_max16(mx));
-        m_i = mx;
-#pragma unroll
-        for (int mt = 0; mt < NKT; ++mt) s[mt] -= mx;
-        neg_m = floatx4{-m_i, -m_i, -m_i, -m_i};
-      } else if (__builtin_amdgcn_ballot_w64(mx > kLazyMax) != 0) {
-        // a real branch (not if-converted): rescale to the new max
-        asm volatile("" ::: "memory");
-        mx = pair_max32(pair_max16(mx));
-        const float d = fmaxf(mx, 0.f);  // the max grows by d; scores shift down by d
-        const float alpha = fast_exp2(-d);
-        l_i *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
-        m_i += d;
-#pragma unroll
-        for (int mt = 0; mt < NKT; ++mt) s[mt] -= d;
-        neg_m = floatx4{-m_i, -m_i, -m_i, -m_i};
+        break;
       }
 #pragma unroll
       for (int mt = 0; mt < NKT; ++mt) {

@@ -36,7 +36,7 @@ __global__ __launch_bounds__(256) void attn_probs_rows_kernel(const float* __res
       const float* kr = K + base + (int64_t)j * L.st;
       float dot = 0.f;
       for (int d = 0; d < L.D; ++d) dot += qs[d] * kr[d];
-      p = expf(dot * scale - lse);
+      p = expf(fmaf(dot, scale, -lse));  // fused: the score is not rounded before the subtraction
     }
     dst[j] = p;
   }

@@ -155,7 +155,9 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
   const int b = bh / L.H, h = bh % L.H;
   const int64_t base = (int64_t)b * L.sb + (int64_t)h * L.sh;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  // wave index as a scalar: conditions derived from it compile to scalar
+  // branches, never to EXEC-masked blocks (which MFMAs would not respect)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lq = lane & 15, g = lane >> 4;
   const int qrow = 16 * qg + lq;            // this lane's query (MFMA column)
   const int key_last = min(qrow, L.T - 1);  // keys after it are masked
@@ -177,6 +179,12 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
   float qf[DG];
   row_frag<DP>(qs, lq, g, scale_log2, qf);
 
+  // Running max m of this wave's chunks: started at its first chunk from an
+  // anchor (the query's score against the chunk's first key) and moved only
+  // by exact steps; every chunk's S accumulators start from -m, so the fused
+  // multiply-add chain of the MFMA keeps its partial sums near 0 instead of
+  // rounding scores of tens of units at every step.  A wave with no chunk
+  // keeps m = -inf.
   float m = -INFINITY, l = 0.f;
   floatx4 oacc[NDT];
 #pragma unroll
@@ -186,32 +194,57 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
     kr.store(ks, lane);
     vr.store(vs, lane);
     wave_lds_sync();
+    if (c == wave) {
+      float kfa[DG];
+      row_frag<DP>(ks, 0, g, 1.f, kfa);
+      float a = 0.f;
+#pragma unroll
+      for (int j = 0; j < DG; ++j) a = fmaf(qf[j], kfa[j], a);
+      m = pair_sum32(pair_sum16(a));  // identical in the query's four lane groups
+    }
     if (c + kSW <= qg) {  // the next chunk's loads in flight during this one
       kr.load(K + base, 16 * (c + kSW), L.T, L.D, L.st, lane);
       vr.load(V + base, 16 * (c + kSW), L.T, L.D, L.st, lane);
     }
     const int key0 = 16 * c;  // <= 16*qg <= T-1: the chunk's first key is valid for every query here
-    float kf[DG], vv[4][NDT];
-    row_frag<DP>(ks, lq, g, 1.f, kf);
-    col_frag<DP>(vs, lq, g, vv);
-    // S^T[key][query] (log2 units): lane element i = key key0+4g+i, query qrow
-    floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+    // S^T[key][query] - m (log2 units): lane element i = key key0+4g+i, query
+    // qrow; the K fragment is read inside, so it is not held across the trips
+    floatx4 s;
+    auto scores = [&]() {
+      float kf[DG];
+      row_frag<DP>(ks, lq, g, 1.f, kf);
+      s = floatx4{-m, -m, -m, -m};
 #pragma unroll
-    for (int j = 0; j < DG; ++j) s = mfma4(kf[j], qf[j], s);
-    float mx = -INFINITY;
+      for (int j = 0; j < DG; ++j) s = mfma4(kf[j], qf[j], s);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float x = (key0 + 4 * g + i > key_last) ? -INFINITY : s[i];
-      s[i] = x;
-      mx = fmaxf(mx, x);
+      for (int i = 0; i < 4; ++i) s[i] = (key0 + 4 * g + i > key_last) ? -INFINITY : s[i];
+    };
+    // The chunk's first key is valid for every query here, so mx is finite,
+    // and >= 0 in the first chunk (the anchor's key).  Scores far above the
+    // maximum they started from were summed at their own size: then the
+    // chunk's scores are formed again from the new maximum (a second trip,
+    // whose scores are all <= 0).
+    float alpha = 1.f, dd;
+    for (;;) {
+      scores();
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[i]);
+      const bool redo = __builtin_amdgcn_ballot_w64(mx > kRedoMax) != 0;
+      mx = pair_max32(pair_max16(mx));
+      const float m_new = m + fmaxf(mx, 0.f);
+      dd = m_new - m;  // exact step of the float maximum
+      alpha *= fast_exp2(-dd);
+      if (!redo) break;
+      m = m_new;
     }
-    mx = pair_max32(pair_max16(mx));
-    const float m_new = fmaxf(m, mx);
-    const float alpha = fast_exp2(m - m_new);
+    const float m_new = m + dd;
+    float vv[4][NDT];
+    col_frag<DP>(vs, lq, g, vv);
     float rs = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float p = fast_exp2(s[i] - m_new);
+      const float p = fast_exp2(s[i] - dd);
       s[i] = p;
       rs += p;
     }
@@ -272,9 +305,10 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
 // The backward in one launch.  Block kg owns keys 16kg .. 16kg+15 (dK, dV)
 // and queries 16kg .. 16kg+15 (dQ); its tasks are
 //   - query chunks kg .. n_g-1 of a key-stationary pass (lane column lq = key):
-//     S = Q K^T and dP = dO V^T (contractions over d, queries on MFMA rows),
-//     P = exp2(S - LSE), dS = P (dP - Delta) with Delta = dO.O of the chunk's
-//     rows formed in place, then dV^T += dO^T P and dK^T += Q^T dS
+//     S = Q K^T and dP = dO V^T (contractions over d, queries on MFMA rows,
+//     the accumulators started from -LSE/scale and -Delta), P =
+//     exp2(S scale log2(e)), dS = P dP with Delta = dO.O of the chunk's rows
+//     formed in place, then dV^T += dO^T P and dK^T += Q^T dS
 //     (contractions over the chunk's rows);
 //   - key chunks 0 .. kg of a query-stationary pass (lane column lq = query)
 //     that forms S^T and dP^T the same way (P from the saved LSE, Delta of the
@@ -302,7 +336,9 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
   const int b = bh / L.H, h = bh % L.H;
   const int64_t base = (int64_t)b * L.sb + (int64_t)h * L.sh;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  // wave index as a scalar: conditions derived from it compile to scalar
+  // branches, never to EXEC-masked blocks (which MFMAs would not respect)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lq = lane & 15, g = lane >> 4;
   const int row = 16 * kg + lq;  // this lane's key (first pass) and query (second pass)
   const int n_kv = n_g - kg;     // key-stationary tasks
@@ -329,9 +365,15 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
     float* qs = stage[0][wave];
     float* os = stage[1][wave];  // dO
     float* ys = stage[2][wave];  // O
+    // K unscaled: S is the plain dot product started from -LSE/scale, and
+    // scale*log2(e) is applied per score in the exponent.  The forward's
+    // rounding of q*scale*log2(e) is common to a row's keys; a per-key
+    // rounding of K here would not be, and dQ = dS K amplifies such a
+    // mismatch by the size of K.
     float kf[DG], vf[DG];
-    row_frag<DP>(own[0], lq, g, scale_log2, kf);
+    row_frag<DP>(own[0], lq, g, 1.f, kf);
     row_frag<DP>(own[1], lq, g, 1.f, vf);
+    const float inv_scale = 1.f / scale;
     ChunkRaw<DP> qr, dr, orr;
     float lsv[4];
     auto load = [&](int c) {
@@ -341,7 +383,7 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int q = 16 * c + 4 * g + i;
-        lsv[i] = q < L.T ? lse[q] * kLog2e : 0.f;
+        lsv[i] = q < L.T ? -lse[q] * inv_scale : 0.f;
       }
     };
     load(kg + wave);
@@ -374,8 +416,11 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
       float dlt[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) dlt[i] = __shfl(delta_lq, 4 * g + i, 64);
-      // S[query][key] (log2 units) and dP: lane element i = query q0+4g+i, key row
-      floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f}, dp = floatx4{0.f, 0.f, 0.f, 0.f};
+      // S[query][key] - LSE/scale (dot-product units) and dP - Delta: lane
+      // element i = query q0+4g+i, key row; started from the rows' -LSE/scale
+      // and -Delta, so the large partial sums of S cancel in the first steps
+      floatx4 s = floatx4{lse2[0], lse2[1], lse2[2], lse2[3]};
+      floatx4 dp = floatx4{-dlt[0], -dlt[1], -dlt[2], -dlt[3]};
 #pragma unroll
       for (int j = 0; j < DG; ++j) {
         s = mfma4(qf[j], kf[j], s);
@@ -385,8 +430,8 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
       for (int i = 0; i < 4; ++i) {
         const int q = q0 + 4 * g + i;
         const bool valid = (q >= row) & (q < L.T) & (row < L.T);
-        const float p = valid ? fast_exp2(s[i] - lse2[i]) : 0.f;
-        dp[i] = valid ? p * (dp[i] - dlt[i]) : 0.f;
+        const float p = valid ? fast_exp2(s[i] * scale_log2) : 0.f;
+        dp[i] = valid ? p * dp[i] : 0.f;
         s[i] = p;
       }
       // dV^T[d][key] += dO^T[d][query] P[query][key]; dK^T[d][key] += Q^T[d][query] dS[query][key]
@@ -435,8 +480,10 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
       row_frag<DP>(ks, lq, g, 1.f, kf);
       row_frag<DP>(vs, lq, g, 1.f, vf);
       col_frag<DP>(ks, lq, g, kc);
-      // S^T[key][query] (log2 units) and dP^T: lane element i = key key0+4g+i, query row
-      floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f}, dp = floatx4{0.f, 0.f, 0.f, 0.f};
+      // S^T[key][query] - LSE (log2 units) and dP^T - Delta: lane element i =
+      // key key0+4g+i, query row; started from -LSE*log2(e) and -Delta (Q
+      // carries the forward's scale*log2(e), as in the forward)
+      floatx4 s = floatx4{-lse2, -lse2, -lse2, -lse2}, dp = floatx4{-delta, -delta, -delta, -delta};
 #pragma unroll
       for (int j = 0; j < DG; ++j) {
         s = mfma4(kf[j], qf[j], s);
@@ -445,8 +492,8 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const bool valid = (key0 + 4 * g + i <= row) & (row < L.T);
-        const float p = valid ? fast_exp2(s[i] - lse2) : 0.f;
-        dp[i] = valid ? p * (dp[i] - delta) : 0.f;
+        const float p = valid ? fast_exp2(s[i]) : 0.f;
+        dp[i] = valid ? p * dp[i] : 0.f;
       }
       // dQ^T[d][query] += K^T[d][key] dS^T[key][query], k-index g <-> key key0+4g+i
 #pragma unroll

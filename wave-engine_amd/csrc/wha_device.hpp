@@ -47,6 +47,13 @@ namespace wha {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
+// The MFMA accumulates a chain of fused multiply-adds, so scores are formed
+// from accumulators started near the row's running maximum (partial sums stay
+// small).  A tile or chunk whose scores pass the maximum it started from by
+// more than this (log2 units) is formed again from the new maximum (the
+// register-staged and small-problem forwards; the direct-to-LDS forward does
+// so in its rescale branch, whose threshold is the same).
+constexpr float kRedoMax = 8.f;
 constexpr float kLn2 = 0.69314718055994531f;
 
 // Strided [B,H,T,D] view (unit stride on d), shared by every [T][D] tensor of a call.
@@ -97,22 +104,17 @@ __device__ __forceinline__ bool wave_bucket_near(int kb, int qb) { return ((kb -
 // v_permlane16_swap leaves lane l holding {x[l], x[l^16]} (in some order) and
 // v_permlane32_swap {x[l], x[l^32]}; max and + are commutative, so both lanes of
 // a pair get bit-identical results.
-// max(a, b, c) in one VALU instruction.  fmaxf lowers to v_max_f32 with every
-// operand first quieted (IEEE mode), doubling the instruction count of a max
-// reduction; a NaN operand here only ever comes from a NaN input, which the
-// exp of the scores propagates anyway (a quiet NaN operand yields the other
-// operand, as fmaxf does).
-__device__ __forceinline__ float vmax3(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
-// max(a, b) in one VALU instruction
-__device__ __forceinline__ float vmax2(float a, float b) {
-  float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
+// max(a, b, c) and max(a, b) as compiler-visible operations (v_max3_f32 /
+// v_max_f32, with an operand quieted where IEEE mode needs it).  These read
+// MFMA results, and the compiler only inserts the wait states an MFMA result
+// needs before a VALU read when it sees the read: an inline-asm v_max3_f32
+// here once read a score chain's last accumulators with no wait at all and got
+// stale values (a wrong running maximum, whole waves' rows shifted into
+// underflow), and an asm output could also land on a register an MFMA still
+// reads.  A NaN operand yields the other operand, as fmaxf does; a NaN score
+// only ever comes from a NaN input, which the exp of the scores propagates.
+__device__ __forceinline__ float vmax3(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+__device__ __forceinline__ float vmax2(float a, float b) { return fmaxf(a, b); }
 __device__ __forceinline__ float pair_max16(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return vmax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -354,9 +356,18 @@ __device__ __forceinline__ float buffer_load_float(__amdgpu_buffer_rsrc_t r, int
 __device__ __forceinline__ void buffer_store_float(__amdgpu_buffer_rsrc_t r, float x, int voff, int soff) {
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, voff, soff, 0);
 }
+// Four floats as two 64-bit stores.  A store of more than 8 bytes reads its
+// data VGPRs after it issues and needs a wait state before a VALU instruction
+// overwrites them, which this compiler does not always leave: a 128-bit store
+// here came out followed directly by a v_max3_f32 into one of its data
+// registers (the 128-wide kept-scores forward), and the stored scores were
+// wrong in that element.  Stores of 8 bytes have no such hazard.
 __device__ __forceinline__ void buffer_store_quad(__amdgpu_buffer_rsrc_t r, floatx4 v, int voff, int soff) {
-  typedef unsigned uintx4 __attribute__((ext_vector_type(4)));
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4, v), r, voff, soff, 0);
+  typedef unsigned uintx2 __attribute__((ext_vector_type(2)));
+  typedef float floatx2 __attribute__((ext_vector_type(2)));
+  const floatx2 lo = v.xy, hi = v.zw;
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(uintx2, lo), r, voff, soff, 0);
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(uintx2, hi), r, voff + 8, soff, 0);
 }
 
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
