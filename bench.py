@@ -217,7 +217,7 @@ def attn_pair(args, cfg, pkg, torch, keep, inputs=None, settle_s=None):
         "warmup_s": round(warm_s, 3), "warmup_steps": warm_n,
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS,
-                     "traffic": load_traffic(f"{dom}[{variant}]", cfg),
+                     **traffic_fields(f"{dom}[{variant}]", cfg),
                      "algorithmic_flops_per_launch": flops[dom], "avg_launch_ms": kern[dom]["avg_ms"]},
     }
     return res, (o, dq, dk, dv), plan
@@ -298,6 +298,8 @@ def run_attention(args, cfg, pkg, torch):
             torch.cuda.empty_cache()
         res["configs"]["decode"] = run_decode(args, CONFIGS["decode"], pkg, torch, sub=True)
         torch.cuda.empty_cache()
+        res["configs"]["probs"] = run_probs(args, CONFIGS["probs"], pkg, torch, sub=True)
+        torch.cuda.empty_cache()
     return res
 
 
@@ -364,7 +366,7 @@ def run_decode(args, cfg, pkg, torch, sub=False):
            "warmup_s": round(warm_s, 3),
            "roofline": {"kernel": "decode_split", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                         "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                        "traffic": load_traffic("decode_split", cfg), "algorithmic_bytes_per_launch": bytes_kv,
+                        **traffic_fields("decode_split", cfg), "algorithmic_bytes_per_launch": bytes_kv,
                         "avg_launch_ms": split}}
     del q, kc, vc, ws
     torch.cuda.empty_cache()
@@ -377,7 +379,7 @@ def run_decode(args, cfg, pkg, torch, sub=False):
     return res
 
 
-def run_probs(args, cfg, pkg, torch):
+def run_probs(args, cfg, pkg, torch, sub=False):
     """Fused forward plus the exact-contract backward (wha_attn_bwd_from_probs:
     att [B,H,T,T] read as given, never recomputed).  att is built once, outside
     the timed region, from the forward's LSE (wha_attn_probs_rows, 256 rows per
@@ -400,7 +402,7 @@ def run_probs(args, cfg, pkg, torch):
         pkg.attn_fwd(q, k, v, out=o, lse=lse_o)
         pkg.attn_bwd_from_probs(do, q, k, v, att, workspace=ws)
 
-    warm_s, _ = settle(step, args, torch)
+    warm_s, _ = settle(step, args, torch, min(0.5, args.settle) if sub else None)
     names = ("attn_fwd", "attn_bwd_probs_delta", "attn_bwd_probs_dq", "attn_bwd_probs_dkv")
     pkg.timing_reset()
     pkg.timing_enable(True)
@@ -427,6 +429,16 @@ def run_probs(args, cfg, pkg, torch):
     dom = max(alg, key=lambda n: avg[n])
     achieved = alg[dom] / (avg[dom] * 1e-3) / 1e9
     flops = credited_flops(B, H, T, D)["total"]
+    del q, k, v, do, o, lse, att, ws, lse_o
+    torch.cuda.empty_cache()
+    if sub:
+        return {"workload": cfg["name"], "pair": "wha_attn_fwd + wha_attn_bwd_from_probs (att given)",
+                "ms_per_step": ms, "tokens_per_s": B * T / (ms * 1e-3), "tflops": flops / (ms * 1e-3) / 1e12,
+                "kernel_ms": {n: round(avg[n], 5) for n in names},
+                "bwd_ms": sum(avg[n] for n in names[1:]),
+                "roofline": {"kernel": dom, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                             "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, **traffic_fields(dom, cfg),
+                             "algorithmic_bytes_per_launch": alg[dom], "avg_launch_ms": avg[dom]}}
     return {"metric": "causal attn fwd + exact-contract bwd (att given) tokens/s, 768-dim seq1024",
             "value": B * T / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "warmup_s": round(warm_s, 3), "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
@@ -437,7 +449,7 @@ def run_probs(args, cfg, pkg, torch):
             "kernel_ms": {n: round(avg[n], 5) for n in names},
             "bwd_ms": sum(avg[n] for n in names[1:]),
             "roofline": {"kernel": dom, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": achieved / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes_per_launch": alg[dom],
+                         "frac": achieved / HBM_PEAK_GBS, **traffic_fields(dom, cfg), "algorithmic_bytes_per_launch": alg[dom],
                          "avg_launch_ms": avg[dom]}}
 
 
@@ -570,7 +582,7 @@ def run_wave(args, cfg, pkg, torch):
         "ms_per_step_with_events": wall / args.steps * 1e3,
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS,
-                     "traffic": load_traffic(dom, cfg), "algorithmic_flops_per_launch": fl[dom],
+                     **traffic_fields(dom, cfg), "algorithmic_flops_per_launch": fl[dom],
                      "executed_pair_flops_per_launch": fl_exec[dom],
                      "avg_launch_ms": kern[dom]["avg_ms"]},
     }
@@ -640,7 +652,7 @@ def run_wave_decode(args, cfg, pkg, torch):
             "mask_fraction": n_valid / (B * H * L),
             "roofline": {"kernel": "wave_kv_split", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                         "traffic": load_traffic("wave_kv_split", cfg), "algorithmic_bytes_per_launch": alg_bytes,
+                         **traffic_fields("wave_kv_split", cfg), "algorithmic_bytes_per_launch": alg_bytes,
                          "avg_launch_ms": kern["wave_kv_split"]["avg_ms"]}}
 
 
@@ -809,6 +821,12 @@ def wave_cpu_baseline(cfg, seed=42, max_threads=None, min_seconds=10.0):
             "sample": f"{nthreads} of the {B} sequences ({nthreads}x{T} tokens), wave_attention_forward + "
                       f"wave_attention_backward_full, one thread per sequence, repeated {reps}x",
             "seconds_per_rep": dt}
+
+
+def traffic_fields(kernel, cfg):
+    """The roofline's traffic entry and, when it is measured, where it comes from."""
+    t = load_traffic(kernel, cfg)
+    return {"traffic": t, "traffic_source": "profiles/traffic.json" if t is not None else None}
 
 
 def load_traffic(kernel, cfg):

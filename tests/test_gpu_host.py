@@ -41,6 +41,34 @@ def test_python_host_mirror(pkg, T, E, H):
     assert_parity("d_v", dv, rv)
 
 
+@pytest.mark.parametrize("T,E,H", [(200, 384, 8), (300, 768, 12), (257, 1024, 8), (64, 224, 4)])
+def test_host_backward_takes_the_direct_to_lds_kernels(pkg, T, E, H):
+    """wha_host_attention_backward at head dims 48, 64, 128 and 56 (padded):
+    the staged [T][E] operands are 16-byte aligned, so the exact-contract
+    backward runs the direct-to-LDS kernels (Delta pass on the forward's tiles,
+    key-stationary dK/dV/dS, dQ from dS), not the register-staged ones (timed
+    as attn_bwd_probs_*_rs); results against the oracle."""
+    g = oracle.Xorshift64(3 * T + E)
+    D = E // H
+    q, k, v = (g.normal(T * E, 1.0 / np.sqrt(D)).reshape(T, E) for _ in range(3))
+    d = g.normal(T * E, 1.0).reshape(T, E)
+    _, att = oracle.core_fwd(q, k, v, H, "f32", want_att=True)
+    be = pkg.HipBackend()
+    pkg.timing_enable(True)
+    pkg.timing_reset()
+    try:
+        dq, dk, dv = be.attention_backward(d, q, k, v, att, H)
+        fast = [pkg.timing_read(f"attn_bwd_probs_{n}")[1] for n in ("delta", "dkv", "dq")]
+        slow = [pkg.timing_read(f"attn_bwd_probs_{n}_rs")[1] for n in ("delta", "dkv", "dq")]
+    finally:
+        pkg.timing_enable(False)
+    assert fast == [1, 1, 1] and slow == [0, 0, 0], (fast, slow)
+    rq, rk, rv = oracle.attention_backward(d, q, k, v, att, H, "f32")
+    assert_parity("d_q", dq, rq)
+    assert_parity("d_k", dk, rk)
+    assert_parity("d_v", dv, rv)
+
+
 @pytest.mark.parametrize("T,E,H,C", [(90, 64, 4, 16), (33, 168, 4, 0)])
 def test_python_host_wave_mirror(pkg, T, E, H, C):
     """HipBackend's host-array wave attention (attn.rs:90-511) against the oracle

@@ -1178,6 +1178,8 @@ hipError_t bwd_fused_t(const float* q, const float* k, const float* v, const flo
   return hipGetLastError();
 }
 
+// (timed as attn_bwd_probs_*_rs: register-staged, told apart from the
+// direct-to-LDS path below)
 template <int DP, bool VEC, bool AV>
 hipError_t bwd_probs_t(const float* d_o, const float* q, const float* k, const float* v,
                        const float* att, float* dq, float* dk, float* dv, float* delta, float* ds,
@@ -1186,7 +1188,7 @@ hipError_t bwd_probs_t(const float* d_o, const float* q, const float* k, const f
   const int n_qt = (L.T + NWQ * 16 - 1) / (NWQ * 16);
   const int n_kt = (L.T + NWK * 16 - 1) / (NWK * 16);
   {
-    TimingScope ts("attn_bwd_probs_delta", stream);
+    TimingScope ts("attn_bwd_probs_delta_rs", stream);
     hipLaunchKernelGGL((attn_bwd_dq_kernel<DP, NWQ, VEC, kDeltaFromProbs, AV>),
                        dim3((unsigned)(n_qt * L.B * L.H)), dim3(NWQ * 64), 0, stream, q, k, v, d_o,
                        (const float*)nullptr, delta, att, (float*)nullptr, L, scale, 0.f);
@@ -1196,14 +1198,14 @@ hipError_t bwd_probs_t(const float* d_o, const float* q, const float* k, const f
   if (ds != nullptr) {
     // dK, dV and the dS tiles in one key-stationary pass; dQ = scale * dS K from them
     {
-      TimingScope ts("attn_bwd_probs_dkv", stream);
+      TimingScope ts("attn_bwd_probs_dkv_rs", stream);
       hipLaunchKernelGGL((attn_bwd_dkv_kernel<DP, NWK, VEC, true, true>), dim3((unsigned)(n_kt * L.B * L.H)),
                          dim3(NWK * 64), 0, stream, q, k, v, d_o, (const float*)nullptr,
                          (const float*)delta, att, dk, dv, ds, L, scale, 0.f);
     }
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    TimingScope ts("attn_bwd_probs_dq", stream);
+    TimingScope ts("attn_bwd_probs_dq_rs", stream);
     constexpr int NWD = WHA_DQ_NW;
     const int n_qt_d = (L.T + NWD * 16 - 1) / (NWD * 16);
     hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<DP, NWD, VEC>), dim3((unsigned)(n_qt_d * L.B * L.H)),
@@ -1211,7 +1213,7 @@ hipError_t bwd_probs_t(const float* d_o, const float* q, const float* k, const f
     return hipGetLastError();
   }
   {
-    TimingScope ts("attn_bwd_probs_dq", stream);
+    TimingScope ts("attn_bwd_probs_dq_rs", stream);
     hipLaunchKernelGGL((attn_bwd_dq_kernel<DP, NWQ, VEC, kProbs, AV>), dim3((unsigned)(n_qt * L.B * L.H)),
                        dim3(NWQ * 64), 0, stream, q, k, v, d_o, (const float*)nullptr, delta, att, dq, L,
                        scale, 0.f);
@@ -1219,7 +1221,7 @@ hipError_t bwd_probs_t(const float* d_o, const float* q, const float* k, const f
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   {
-    TimingScope ts("attn_bwd_probs_dkv", stream);
+    TimingScope ts("attn_bwd_probs_dkv_rs", stream);
     hipLaunchKernelGGL((attn_bwd_dkv_kernel<DP, NWK, VEC, true, false>), dim3((unsigned)(n_kt * L.B * L.H)),
                        dim3(NWK * 64), 0, stream, q, k, v, d_o, (const float*)nullptr,
                        (const float*)delta, att, dk, dv, (float*)nullptr, L, scale, 0.f);

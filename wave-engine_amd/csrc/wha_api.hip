@@ -1240,10 +1240,13 @@ int wha_host_attention_backward(const float* d_pre_proj, const float* q, const f
   const size_t n = (size_t)T * E;
   const size_t nb = round256(n * sizeof(float)) / sizeof(float);
   const size_t na = round256((size_t)n_head * T * T * sizeof(float)) / sizeof(float);
-  const size_t nd = round256((size_t)n_head * T * sizeof(float)) / sizeof(float);
+  // the device entry's workspace (Delta, the statistics blocks and dS of the
+  // direct-to-LDS kernels) for the staged [T][E] sequence
+  const wha_layout sl{1, n_head, T, E / n_head, (int64_t)T * E, (int64_t)(E / n_head), (int64_t)E};
+  const size_t ws_bytes = wha_attn_bwd_from_probs_workspace_size(&sl);
   float* base = nullptr;
   hipStream_t s = nullptr;
-  if ((rc = host_stage((7 * nb + na + nd) * sizeof(float), &base, &s))) return rc;
+  if ((rc = host_stage((7 * nb + na) * sizeof(float) + ws_bytes, &base, &s))) return rc;
   float* d_do = base;
   float* d_q = base + nb;
   float* d_k = base + 2 * nb;
@@ -1253,6 +1256,9 @@ int wha_host_attention_backward(const float* d_pre_proj, const float* q, const f
   float* d_dv = base + 6 * nb;
   float* d_att = base + 7 * nb;
   float* d_delta = d_att + na;
+  float* d_stats = reinterpret_cast<float*>(reinterpret_cast<char*>(d_delta) + delta_bytes(&sl));
+  float* d_ds = ds_bytes(&sl) ? reinterpret_cast<float*>(reinterpret_cast<char*>(d_stats) + stats_bytes(&sl))
+                              : nullptr;
   hipError_t e = hipSuccess;
   const float* srcs[4] = {d_pre_proj, q, k, v};
   float* dsts[4] = {d_do, d_q, d_k, d_v};
@@ -1262,7 +1268,7 @@ int wha_host_attention_backward(const float* d_pre_proj, const float* q, const f
     e = hipMemcpyAsync(d_att, att, (size_t)n_head * T * T * sizeof(float), hipMemcpyHostToDevice, s);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync H2D");
   const float scale = 1.0f / sqrtf((float)(E / n_head));  // src/cpu/backward.rs:326
-  e = wha::launch_attn_bwd_probs(d_do, d_q, d_k, d_v, d_att, d_dq, d_dk, d_dv, d_delta, nullptr, nullptr, V,
+  e = wha::launch_attn_bwd_probs(d_do, d_q, d_k, d_v, d_att, d_dq, d_dk, d_dv, d_delta, d_stats, d_ds, V,
                                  vec_ok(V, {d_do, d_q, d_k, d_v, d_dq, d_dk, d_dv}), scale, s);
   if (e != hipSuccess) return hip_fail(e, "attention backward launch");
   float* outs[3] = {dq, dk, dv};
