@@ -305,37 +305,54 @@ def run_attention(args, cfg, pkg, torch):
 
 def hbm_read_ceiling(torch, gib=4):
     """Read-only stream rate (GB/s): a calibration kernel (wave-engine_amd/
-    libwha_hbm_probe.so, 16-byte loads grid-stride, one float written per
-    thread) over a `gib` GiB buffer, best of a few grid sizes -- the practical
-    ceiling for kernels that only read, such as the decode split kernel."""
+    libwha_hbm_probe.so: 16-byte loads grid-stride, U of them in flight per
+    thread, one float written per thread) over a `gib` GiB buffer, timed with
+    HIP events over 10 launches on the launch stream.  The best of a sweep of
+    one or two concurrent streams, unrolls (4, 8, 16), plain or non-temporal
+    loads, and grids of 4 to 64 blocks per CU is the practical ceiling for
+    kernels that only read, such as the decode split kernel.  A device copy (torch copy_, read + write
+    bytes) of the same buffer is timed beside it."""
     probe = ctypes.CDLL(str(ROOT / "wave-engine_amd" / "libwha_hbm_probe.so"))
-    probe.whp_read_stream.restype = ctypes.c_int
-    probe.whp_read_stream.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
-                                      ctypes.c_void_p]
+    probe.whp_read_stream_v.restype = ctypes.c_int
+    probe.whp_read_stream_v.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     x = torch.ones(gib * (1 << 28), dtype=torch.float32, device="cuda:0")
-    best = (0.0, 0)
-    for blocks in (1024, 2048, 4096, 8192):
-        out = torch.empty(blocks * 256, dtype=torch.float32, device="cuda:0")
-        st = torch.cuda.current_stream().cuda_stream
+    out = torch.empty(16384 * 256, dtype=torch.float32, device="cuda:0")
+    st = torch.cuda.current_stream().cuda_stream
+    n = 10
 
-        def run():
-            rc = probe.whp_read_stream(x.data_ptr(), x.numel() // 4, out.data_ptr(), blocks, st)
-            if rc:
-                raise RuntimeError(f"whp_read_stream failed ({rc})")
-
+    def timed(fn):
         for _ in range(3):
-            run()
-        torch.cuda.synchronize()
-        n = 10
-        t0 = time.perf_counter()
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
         for _ in range(n):
-            run()
+            fn()
+        e1.record()
         torch.cuda.synchronize()
-        gbs = x.numel() * 4 / ((time.perf_counter() - t0) / n) / 1e9
-        best = max(best, (gbs, blocks))
-    del x
+        return e0.elapsed_time(e1) / n * 1e-3
+
+    best = (0.0, None)
+    for streams in (1, 2):
+        for unroll in (4, 8, 16):
+            for nt in (0, 1):
+                for blocks in (1024, 2048, 4096, 8192, 16384):
+                    def run():
+                        rc = probe.whp_read_stream_v(x.data_ptr(), x.numel() // 4, out.data_ptr(), blocks, unroll,
+                                                     nt, streams, st)
+                        if rc:
+                            raise RuntimeError(f"whp_read_stream_v failed ({rc})")
+
+                    gbs = x.numel() * 4 / timed(run) / 1e9
+                    if gbs > best[0]:
+                        best = (gbs, {"streams": streams, "unroll": unroll, "nontemporal": bool(nt),
+                                      "blocks": blocks})
+    y = torch.empty_like(x)
+    copy_gbs = 2 * x.numel() * 4 / timed(lambda: y.copy_(x)) / 1e9
+    del x, y, out
     torch.cuda.empty_cache()
-    return {"gbs": best[0], "blocks": best[1], "buffer_gib": gib}
+    return {"gbs": best[0], **best[1], "buffer_gib": gib, "timing": "hip events, 10 launches",
+            "copy_gbs": copy_gbs}
 
 
 def run_decode(args, cfg, pkg, torch, sub=False):

@@ -137,7 +137,11 @@ __global__ __launch_bounds__(kKvThreads) void wave_kv_split_kernel(const float4*
 #pragma unroll
         for (int e4 = 0; e4 < NPL / 4; ++e4) {
           float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-          if (in && d0 + 4 * e4 < hd) a = *reinterpret_cast<const float4*>(vp + 4 * e4);
+          if (in && d0 + 4 * e4 < hd) {
+            // read once: non-temporal (5.7 -> 6.7 TB/s at the 768-dim wave decode)
+            const floatx4 t = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(vp + 4 * e4));
+            a = make_float4(t[0], t[1], t[2], t[3]);
+          }
           vv[u][4 * e4 + 0] = a.x;
           vv[u][4 * e4 + 1] = a.y;
           vv[u][4 * e4 + 2] = a.z;
