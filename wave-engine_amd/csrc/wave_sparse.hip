@@ -107,16 +107,16 @@ __device__ __forceinline__ void stage_info(const int4* __restrict__ CIh, int c0,
 
 // 64 rows of W floats (W % 4 == 0) of a sorted [T16][W] array: row r of the
 // stage is sorted row row0[r / 16] + r % 16 (zeros at and past T), staged
-// through registers into an LDS tile of pitch LD.
-template <int W, int LD>
+// through registers into an LDS tile of pitch LD by NT threads.
+template <int W, int LD, int NT = 256>
 struct ChunkRows {
   static constexpr int Q = W / 4;
-  static constexpr int PER = (64 * Q + 255) / 256;
+  static constexpr int PER = (64 * Q + NT - 1) / NT;
   float4 r[PER];
   __device__ __forceinline__ void load(const float* __restrict__ base, const int (&row0)[4], int T, int tid) {
 #pragma unroll
     for (int p = 0; p < PER; ++p) {
-      const int idx = tid + 256 * p;
+      const int idx = tid + NT * p;
       const int row = idx / Q, q = idx % Q;
       const int j = sel4(row0, row >> 4) + (row & 15);
       r[p] = (idx < 64 * Q && j < T) ? *reinterpret_cast<const float4*>(base + (unsigned)(j * W + 4 * q))
@@ -126,7 +126,7 @@ struct ChunkRows {
   __device__ __forceinline__ void store(float* lds, int tid) const {
 #pragma unroll
     for (int p = 0; p < PER; ++p) {
-      const int idx = tid + 256 * p;
+      const int idx = tid + NT * p;
       if (idx < 64 * Q) *reinterpret_cast<float4*>(lds + (idx / Q) * LD + 4 * (idx % Q)) = r[p];
     }
   }
@@ -137,16 +137,16 @@ struct ChunkRows {
 // row0[r / 16] + r % 16, zero padded past D and for rows at and past T.  The
 // positions are fetched one stage ahead (load_pos), so the row loads of a
 // stage do not wait on them.
-template <int DP, int LD, bool VEC>
+template <int DP, int LD, bool VEC, int NT = 256>
 struct GatherRows {
   static constexpr int Q = DP / 4;
-  static constexpr int PER = (64 * Q + 255) / 256;
+  static constexpr int PER = (64 * Q + NT - 1) / NT;
   float4 r[PER];
   int pos[PER];
   __device__ __forceinline__ void load_pos(const int* __restrict__ PSh, const int (&row0)[4], int T, int tid) {
 #pragma unroll
     for (int p = 0; p < PER; ++p) {
-      const int idx = tid + 256 * p;
+      const int idx = tid + NT * p;
       const int row = idx / Q;
       const int j = sel4(row0, row >> 4) + (row & 15);
       pos[p] = (idx < 64 * Q && j < T) ? PSh[j] : -1;
@@ -155,7 +155,7 @@ struct GatherRows {
   __device__ __forceinline__ void load(const float* __restrict__ Xh, int64_t st, int D, int tid) {
 #pragma unroll
     for (int p = 0; p < PER; ++p) {
-      const int q = (tid + 256 * p) % Q;
+      const int q = (tid + NT * p) % Q;
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       if (pos[p] >= 0) {
         const float* src = Xh + (int64_t)pos[p] * st + 4 * q;
@@ -174,7 +174,7 @@ struct GatherRows {
   __device__ __forceinline__ void store(float* lds, int tid) const {
 #pragma unroll
     for (int p = 0; p < PER; ++p) {
-      const int idx = tid + 256 * p;
+      const int idx = tid + NT * p;
       if (idx < 64 * Q) *reinterpret_cast<float4*>(lds + (idx / Q) * LD + 4 * (idx % Q)) = r[p];
     }
   }
@@ -300,8 +300,8 @@ __global__ __launch_bounds__(256) void wave_gather_kernel(const int* __restrict_
 // rows) and O^T += V^T P^T as in wave_fwd_kernel, per 16-key chunk only where
 // block_live().  The k = q - 1 term (buckets not near) is one more online
 // softmax step per lane before the output is scattered to the query's position.
-template <int DP, bool VEC>
-__global__ __launch_bounds__(256) void wave_sfwd_kernel(const float* __restrict__ FS, const int* __restrict__ PS,
+template <int DP, bool VEC, int NW>
+__global__ __launch_bounds__(NW * 64) void wave_sfwd_kernel(const float* __restrict__ FS, const int* __restrict__ PS,
                                                         const int* __restrict__ BSs,
                                                         const int4* __restrict__ CI, const int* __restrict__ BST,
                                                         const float* __restrict__ F, const int* __restrict__ BK,
@@ -314,9 +314,10 @@ __global__ __launch_bounds__(256) void wave_sfwd_kernel(const float* __restrict_
   __shared__ __align__(16) int Bs[64];  // bucket bit 1 << bucket of each key (0 past T)
   __shared__ __align__(16) int Ps[64];  // position of each key
 
+  constexpr int QT = 16 * NW;  // sorted queries per block
   const int T = Lv.T, BH = Lv.B * Lv.H;
   const int NC = (T + 15) >> 4, T16 = 16 * NC;
-  const int n_qt = (T + 63) >> 6;
+  const int n_qt = (T + QT - 1) / QT;
   const int bh = blockIdx.x % BH;
   const int qt = n_qt - 1 - (int)(blockIdx.x / BH);
   const int b = bh / Lv.H, h = bh % Lv.H;
@@ -331,7 +332,7 @@ __global__ __launch_bounds__(256) void wave_sfwd_kernel(const float* __restrict_
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lq = lane & 15, g = lane >> 4;
-  const int qc = 4 * qt + wave;
+  const int qc = NW * qt + wave;
   const int qrow = 16 * qc + lq;
   const bool qok = qrow < T;
 
@@ -354,14 +355,14 @@ __global__ __launch_bounds__(256) void wave_sfwd_kernel(const float* __restrict_
   const int4 ci = qc < NC ? CIh[qc] : empty_chunk();
 
   int c0, n_ch;
-  bucket_window(BST + bh * 16, BSh[64 * qt], BSh[min(64 * qt + 63, T - 1)], NC, c0, n_ch);
+  bucket_window(BST + bh * 16, BSh[QT * qt], BSh[min(QT * qt + QT - 1, T - 1)], NC, c0, n_ch);
   const int n_kt = (n_ch + 3) >> 2;
 
   // nxt: the stage whose rows load() fetches (its value-row positions already
   // in vs.pos); nxt2: the stage after it, whose positions load() requests
   StageInfo nxt, nxt2;
-  ChunkRows<kFP, kLDF> fs;
-  GatherRows<DP, LD, VEC> vs;
+  ChunkRows<kFP, kLDF, NW * 64> fs;
+  GatherRows<DP, LD, VEC, NW * 64> vs;
   int kb_r = 0, kp_r = -1;  // raw bucket: its bit is formed when stored, not beside the load
   auto load = [&](int kt) {
     fs.load(FSh, nxt.row0, T, tid);
@@ -927,12 +928,16 @@ hipError_t sort_and_gather(const float* feat, const int* bucket, const float* ls
   return hipGetLastError();
 }
 
+#ifndef WHA_SFWD_NW
+#define WHA_SFWD_NW 4
+#endif
 template <int DP, bool VEC>
 hipError_t sfwd_t(const SparseBufs& sb, const float* feat, const int* bucket, const float* v, float* merged,
                   float* lse, const View& Lv, float cs, hipStream_t stream) {
-  const int n_qt = (Lv.T + 63) / 64;
+  constexpr int NW = WHA_SFWD_NW;
+  const int n_qt = (Lv.T + 16 * NW - 1) / (16 * NW);
   TimingScope ts("wave_fwd", stream);
-  hipLaunchKernelGGL((wave_sfwd_kernel<DP, VEC>), dim3((unsigned)(n_qt * Lv.B * Lv.H)), dim3(256), 0, stream,
+  hipLaunchKernelGGL((wave_sfwd_kernel<DP, VEC, NW>), dim3((unsigned)(n_qt * Lv.B * Lv.H)), dim3(NW * 64), 0, stream,
                      (const float*)sb.fs, (const int*)sb.perm, (const int*)sb.bsort, (const int4*)sb.ci,
                      (const int*)sb.bstart, feat, bucket, v, merged, lse, Lv, cs);
   return hipGetLastError();
