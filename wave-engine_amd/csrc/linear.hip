@@ -698,7 +698,9 @@ namespace {
 // Output tile: the largest of 128 x 128, 64 x 128 that gives at least eight
 // blocks per CU; 64-column tiles when N <= 64, and for N <= 256 when 64 x 128
 // tiles would leave CUs with fewer (same padding, twice the blocks).  Split-K
-// then aims for 1024 blocks.  Both thresholds were swept on the layer and wave
+// then picks its factor by rounds of resident blocks (gemm_splits; it once
+// aimed for 1024 blocks in powers of two: weight gradients of the layer step
+// 343 -> 328 us, of the wave step 174 -> 166 us with the rounds model).  Both thresholds were swept on the layer and wave
 // steps (tile 256/512/1024 blocks x split 512/1024/2048: 1024/1024 best, layer
 // 1.465 vs 1.501 ms at 512/512, wave 0.865 vs 0.877 ms); with the buffer-load
 // stages the tile threshold moved to 2048 (the 2304 x 768 c_attn forward in
@@ -707,9 +709,6 @@ namespace {
 constexpr int kCUs = 256;
 #ifndef WHA_GEMM_TILE_BLOCKS
 #define WHA_GEMM_TILE_BLOCKS (8 * kCUs)
-#endif
-#ifndef WHA_GEMM_SPLIT_BLOCKS
-#define WHA_GEMM_SPLIT_BLOCKS 1024
 #endif
 struct GemmTile {
   int bm, bn;
@@ -722,13 +721,29 @@ GemmTile gemm_tile(int M, int N, int batch) {
   return {64, 64};
 }
 
-// Split-K factor: aim for >= WHA_GEMM_SPLIT_BLOCKS blocks while keeping >= min_k k per split.
+#ifndef WHA_GEMM_FIXK
+#define WHA_GEMM_FIXK 128
+#endif
+// Split-K factor: the split count that minimises rounds x (k per split + a fixed
+// per-block cost), where a round is one block per slot (blocks a CU holds at
+// once: 2 for 128 x 128 tiles, 3 for 64 x 128, 5 for 64 x 64, by their VGPRs
+// and LDS), keeping >= min_k k per split.
 int gemm_splits(int M, int N, int K, int batch, int min_k = 256) {
   const GemmTile t = gemm_tile(M, N, batch);
-  const int tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) * batch;
-  int splits = 1;
-  while (tiles * splits < WHA_GEMM_SPLIT_BLOCKS && (K / (splits * 2)) >= min_k) splits *= 2;
-  return splits;
+  const int64_t tiles = (int64_t)((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn) * batch;
+  const int64_t slots = (int64_t)kCUs * (t.bn == 64 ? 5 : t.bm == 128 ? 2 : 3);
+  int best = 1;
+  int64_t best_cost = INT64_MAX;
+  for (int s = 1; s <= 32; ++s) {
+    if (s > 1 && K / s < min_k) break;
+    const int64_t rounds = (tiles * s + slots - 1) / slots;
+    const int64_t cost = rounds * ((K + s - 1) / s + WHA_GEMM_FIXK);
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = s;
+    }
+  }
+  return best;
 }
 
 
