@@ -15,9 +15,11 @@ from conftest import assert_parity, make_wave_weights
 pytestmark = pytest.mark.gpu
 
 # (B, T, n_embd, n_head, content_dim): head_dim 12 (padded 48), 42, 64, 128, and the
-# 768-dim model shape; 3 x 37 rows put a partial 16-row tile in the 64-wide per-head projections
+# 768-dim model shape; 3 x 37 rows put a partial 16-row tile in the 64-wide per-head projections;
+# head_dim 56 runs the 64-wide kernels with pad quads
 CONFIGS = [(2, 100, 48, 4, 16), (1, 77, 168, 4, 0), (2, 200, 128, 2, 16), (2, 130, 256, 2, 5),
-           (2, 1024, 768, 12, 16), (3, 1, 64, 2, 30), (1, 64, 64, 1, 3), (3, 37, 128, 2, 8)]
+           (2, 1024, 768, 12, 16), (3, 1, 64, 2, 30), (1, 64, 64, 1, 3), (3, 37, 128, 2, 8),
+           (2, 150, 112, 2, 16)]
 
 
 @pytest.fixture(scope="module")

@@ -509,6 +509,281 @@ __global__ __launch_bounds__(NW * 64) void wave_sfwd_kernel(const float* __restr
   if (LSE != nullptr && g == 0 && qok) LSE[(int64_t)bh * T + qpos] = (m_i + log2f(l_sum)) * kLn2;
 }
 
+// The same forward with one wave per workgroup (16 sorted queries), no LDS
+// staging and no workgroup barrier.  The wave lists the live key chunks of its
+// own query chunk (the bucket window of its own buckets, block_live per
+// 16-key chunk) in LDS, then walks them with every operand loaded straight
+// into the MFMA operand registers, two chunks ahead of the one it computes
+// (three register sets; the key positions, which address the value rows, one
+// step before the rows).  A wave's time is then the sum of its own live
+// chunks rather than, per 64-key stage, the most any wave of a block had, and
+// a CU holds as many chunks in flight as its waves have registers.  Lane
+// (lq, g) loads features 8g .. 8g+7 of key row lq (the S = F_k F_q^T A
+// operand: two 16-byte loads; the 16 rows of a chunk are contiguous in sorted
+// order) and, for keys 4g + i, value quad lq of the key's row (the O += V^T
+// P^T A operand, gathered through the permutation), with the positions and
+// buckets of keys 4g .. 4g+3 for the mask; buffer loads, so a chunk's offset
+// is one scalar.  Every step issues the same loads (past the last live chunk,
+// repeats of it that are never used), so the compiler's count of loads in
+// flight stays exact.  Chunks the mask admits whole (flagged in the list) skip
+// the element mask, and the running max moves only when a query's maximum
+// passes it by more than kSparseLazy.  D padded to 64, 16-byte aligned value
+// rows (vec).
+#ifndef WHA_SFWD_NS
+#define WHA_SFWD_NS 3
+#endif
+constexpr float kSparseLazy = 8.f;  // log2 units
+template <bool PADQ, int NS = WHA_SFWD_NS>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NS <= 3 ? 3 : 2))) void wave_sfwd_reg_kernel(
+    const float* __restrict__ FS, const int* __restrict__ PS, const int* __restrict__ BSs,
+    const int4* __restrict__ CI, const int* __restrict__ BST, const float* __restrict__ F,
+    const int* __restrict__ BK, const float* __restrict__ V, float* __restrict__ O, float* __restrict__ LSE, View Lv,
+    float cs) {
+  constexpr int DP = 64;
+  constexpr int NDT = DP / 16, FG = kFP / 4;
+  static_assert(FG == 8, "32 features: two 16-byte loads per lane");
+  extern __shared__ int live_list[];  // NC entries
+
+  const int T = Lv.T, BH = Lv.B * Lv.H;
+  const int NC = (T + 15) >> 4, T16 = 16 * NC;
+  // workgroup -> (head, query chunk).  Workgroups are dealt to the 8 XCDs in
+  // turn; with BH % 8 == 0 every chunk of a head lands on one XCD, whose L2
+  // then serves the head's gathered rows to all of them.
+  const int wg = (int)blockIdx.x;
+  int bh, qc;
+  if (BH % 8 == 0) {
+    bh = (wg & 7) + 8 * ((wg >> 3) / NC);
+    qc = (wg >> 3) % NC;
+  } else {
+    bh = wg % BH;
+    qc = wg / BH;
+  }
+  const int b = bh / Lv.H, h = bh % Lv.H;
+  const int64_t vbase = (int64_t)b * Lv.sb + (int64_t)h * Lv.sh;
+  const float* FSh = FS + (int64_t)bh * T16 * kFP;
+  const int* PSh = PS + (int64_t)bh * T16;
+  const int* BSh = BSs + (int64_t)bh * T16;
+  const int4* CIh = CI + (int64_t)bh * NC;
+  const float* Fh = F + (int64_t)bh * T * kFP;
+  const int* Bh = BK + (int64_t)bh * T;
+
+  const int lane = (int)threadIdx.x;
+  const int lq = lane & 15, g = lane >> 4;
+  const int qrow = 16 * qc + lq;
+  const bool qok = qrow < T;
+
+  float qf[FG];
+  {
+    const float w_cs = cs * kLog2e;
+#pragma unroll
+    for (int e = 0; e < FG; ++e) {
+      const int f = g * FG + e;
+      qf[e] = FSh[(int64_t)(qok ? qrow : 0) * kFP + f] * (f < 2 ? kLog2e : w_cs);
+      qf[e] = qok ? qf[e] : 0.f;
+    }
+  }
+  const int qb = qok ? BSh[qrow] : 0;
+  const int qpos = qok ? PSh[qrow] : -1;
+  const int pb = qok && qpos >= 1 ? Bh[qpos - 1] : 0;
+  const int nq = qok ? near_set(1 << qb) : 0;
+  const int4 ci = CIh[qc];
+
+  int c0, n_ch;
+  bucket_window(BST + bh * 16, BSh[16 * qc], BSh[min(16 * qc + 15, T - 1)], NC, c0, n_ch);
+
+  // buckets every query of the chunk admits (the chunk's bucket set ci.x)
+  int nq_all = 0xff;
+#pragma unroll
+  for (int v = 0; v < 8; ++v) nq_all &= ((ci.x >> v) & 1) ? near_set(1 << v) : 0xff;
+  // the live chunks of the window, in window order, with bit 31 set on chunks
+  // every pair of which the mask admits: all 16 keys before T, their buckets
+  // admitted by every query bucket of the chunk, and no key after its first
+  // query (those skip the per-element mask)
+  int n_live = 0;
+  for (int o0 = 0; o0 < n_ch; o0 += 64) {
+    const int o = o0 + lane;
+    const int c = window_chunk(c0, o < n_ch ? o : 0, NC);
+    const int4 kc = CIh[c];
+    const bool on = o < n_ch && block_live(ci, kc);
+    const bool full = (kc.x & ~nq_all) == 0 && kc.w <= ci.z && 16 * c + 16 <= T;
+    const uint64_t m = __ballot(on);
+    if (on)
+      live_list[n_live + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0))] =
+          c | (full ? (int)0x80000000u : 0);
+    n_live += __builtin_popcountll(m);
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the list is in LDS
+  __builtin_amdgcn_wave_barrier();
+
+  // buffers over this head's sorted features, positions and buckets (a
+  // chunk's rows at a uniform offset) and its value rows (this lane's quad of
+  // row r at r * st + 4 lq floats; a quad past D reads quad 0 instead: it only
+  // feeds output columns that are never stored)
+  const __amdgpu_buffer_rsrc_t rF = buffer_rsrc(FSh, (uint32_t)T16 * kFP * 4u);
+  const __amdgpu_buffer_rsrc_t rP = buffer_rsrc(PSh, (uint32_t)T16 * 4u);
+  const __amdgpu_buffer_rsrc_t rB = buffer_rsrc(BSh, (uint32_t)T16 * 4u);
+  const uint32_t st4 = 4u * (uint32_t)Lv.st;  // < 2^24, and the slice < 4 GiB (checked on the host)
+  const __amdgpu_buffer_rsrc_t rV =
+      buffer_rsrc(V + vbase, (uint32_t)((uint64_t)(T - 1) * st4 + 4u * (uint32_t)Lv.D));
+  const int vq = (PADQ && 4 * lq >= Lv.D) ? 0 : 16 * lq;
+  const int foff = (lq * kFP + 8 * g) * 4, koff = 16 * g;
+
+  // the k-th live chunk entry (past the end: the last one again, never computed)
+  auto chunk_at = [&](int k) { return __builtin_amdgcn_readfirstlane(live_list[min(k, n_live - 1)]); };
+  struct Set {
+    float4 f0, f1;  // features 8g .. 8g+7 of key row lq
+    float4 v[4];    // value quad lq of keys 4g + i
+    int4 p, b;      // positions and buckets of keys 4g .. 4g+3
+    int full;       // the list entry: negative when no element mask is needed
+  };
+  auto ld_int4 = [&](__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    typedef unsigned uintx4 __attribute__((ext_vector_type(4)));
+    const uintx4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    return make_int4((int)v[0], (int)v[1], (int)v[2], (int)v[3]);
+  };
+  auto load_pos = [&](int e) { return ld_int4(rP, koff, 64 * (e & 0x7fffffff)); };
+  auto load_set = [&](int e, const int4& p, Set& d) {
+    const int c = e & 0x7fffffff;
+    d.f0 = buffer_load_quad(rF, foff, c * (16 * kFP * 4));
+    d.f1 = buffer_load_quad(rF, foff + 16, c * (16 * kFP * 4));
+    // keys past T (position -1) read position 0 and are masked
+    const int pv[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      d.v[i] = buffer_load_quad(rV, (int)(__umul24((uint32_t)max(pv[i], 0), st4) + (uint32_t)vq), 0);
+    d.b = ld_int4(rB, koff, 64 * c);
+    d.p = p;
+    d.full = e;
+  };
+
+  float m_i = -1e30f, l_i = 0.f;
+  floatx4 oacc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) oacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const Set& d) {
+    // S^T[key 4g + i][query lq] of the chunk, log2 units
+    floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+    s = mfma4(d.f0.x, qf[0], s);
+    s = mfma4(d.f0.y, qf[1], s);
+    s = mfma4(d.f0.z, qf[2], s);
+    s = mfma4(d.f0.w, qf[3], s);
+    s = mfma4(d.f1.x, qf[4], s);
+    s = mfma4(d.f1.y, qf[5], s);
+    s = mfma4(d.f1.z, qf[6], s);
+    s = mfma4(d.f1.w, qf[7], s);
+    if (d.full >= 0) {
+      const int kp[4] = {d.p.x, d.p.y, d.p.z, d.p.w};
+      const int kb[4] = {d.b.x, d.b.y, d.b.z, d.b.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool valid = (kp[i] >= 0) & (kp[i] <= qpos) & (((nq >> kb[i]) & 1) != 0);
+        s[i] = valid ? s[i] : -INFINITY;
+      }
+    }
+    const float mx = vmax3(vmax3(s[0], s[1], s[2]), s[3], s[3]);
+    // the running max moves only when some query's maximum passes it by more
+    // than kSparseLazy (or it is still the initial floor): the probabilities
+    // then stay below 2^kSparseLazy, and the result (O and LSE) does not depend
+    // on which maximum was subtracted
+    if (__builtin_amdgcn_ballot_w64(mx > m_i + kSparseLazy) != 0) {
+      // its new maximum over the four lane groups
+      const float m_new = fmaxf(m_i, pair_max32(pair_max16(mx)));
+      const float alpha = fast_exp2(m_i - m_new);
+      l_i *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
+      m_i = m_new;
+    }
+    float rs = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s[i] = fast_exp2(s[i] - m_i);
+      rs += s[i];
+    }
+    l_i += rs;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float va[4] = {d.v[i].x, d.v[i].y, d.v[i].z, d.v[i].w};
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mfma4(va[dt], s[i], oacc[dt]);
+    }
+  };
+
+  if (n_live > 0) {
+    // chunk j: positions in pos set j % NS (requested at step j - NS), operands
+    // in set j % NS (requested at step j - NS + 1, from those positions),
+    // computed at step j; chunk ids read from the list one step before use
+    Set sets[NS];
+    int4 ps[NS];
+    auto list_at = [&](int k) { return live_list[min(k, n_live - 1)]; };
+#pragma unroll
+    for (int j = 0; j < NS; ++j) ps[j] = load_pos(chunk_at(j));
+    WHA_FENCE();
+#pragma unroll
+    for (int j = 0; j < NS - 1; ++j) {
+      load_set(chunk_at(j), ps[j], sets[j]);
+      WHA_FENCE();
+    }
+    int id_set = chunk_at(NS - 1);  // the chunk whose operands the next step requests
+    int id_v = list_at(NS);         // the chunk whose positions it requests (a lane value)
+    // whole rounds of NS steps: a step past the last chunk only loads; the
+    // skipped computations issue no loads, so every path through a round
+    // issues the same ones
+    int k = 0;
+    do {
+#pragma unroll
+      for (int u = 0; u < NS; ++u) {
+        const int id_pos = __builtin_amdgcn_readfirstlane(id_v);
+        id_v = list_at(k + u + NS + 1);
+        WHA_FENCE();
+        ps[u] = load_pos(id_pos);
+        WHA_FENCE();
+        load_set(id_set, ps[(u + NS - 1) % NS], sets[(u + NS - 1) % NS]);
+        WHA_FENCE();
+        id_set = id_pos;
+        if (k + u < n_live) compute(sets[u]);
+      }
+      k += NS;
+    } while (k < n_live);
+    wait_vmem();  // the loads past the end land before the wave ends
+  }
+
+  // the previous position when its bucket is not near (outside every window)
+  const int pp = qpos - 1;
+  const bool extra = qok && pp >= 0 && !wave_bucket_near(pb, qb);
+  float part = 0.f;
+  if (extra) {
+#pragma unroll
+    for (int e = 0; e < FG; ++e) part += qf[e] * Fh[(int64_t)pp * kFP + g * FG + e];
+  }
+  const float sx = pair_sum32(pair_sum16(part));
+  if (extra) {
+    const float m_new = fmaxf(m_i, sx);
+    const float alpha = fast_exp2(m_i - m_new);
+    const float px = fast_exp2(sx - m_new);
+    l_i = l_i * alpha + (g == 0 ? px : 0.f);
+    m_i = m_new;
+    float vp[DP / 4];
+    load_row_frag<DP, true>(V + vbase, pp, T, Lv.D, Lv.st, g, 1.f, vp);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) oacc[dt][i] = oacc[dt][i] * alpha + px * vp[NDT * i + dt];
+    }
+  }
+
+  const float l_sum = pair_sum32(pair_sum16(l_i));
+  const float inv = qok ? 1.f / l_sum : 0.f;
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) oacc[dt][i] = oacc[dt][i] * inv;
+  }
+  store_row_frag<DP, true>(O + vbase, qok ? qpos : T, T, Lv.D, Lv.st, g, oacc, 1.f);
+  if (LSE != nullptr && g == 0 && qok) LSE[(int64_t)bh * T + qpos] = (m_i + log2f(l_sum)) * kLn2;
+}
+
 // ------------------------------------------------------------ backward
 
 // Key-stationary backward over sorted keys.  Block = 64 sorted keys of one
@@ -931,12 +1206,35 @@ hipError_t sort_and_gather(const float* feat, const int* bucket, const float* ls
 #ifndef WHA_SFWD_NW
 #define WHA_SFWD_NW 4
 #endif
+#ifndef WHA_SFWD_DMA
+#define WHA_SFWD_DMA 1
+#endif
+// chunk list of wave_sfwd_reg_kernel: 16 KB of LDS
+constexpr int kSfwdMaxChunks = 4096;
 template <int DP, bool VEC>
 hipError_t sfwd_t(const SparseBufs& sb, const float* feat, const int* bucket, const float* v, float* merged,
                   float* lse, const View& Lv, float cs, hipStream_t stream) {
   constexpr int NW = WHA_SFWD_NW;
   const int n_qt = (Lv.T + 16 * NW - 1) / (16 * NW);
   TimingScope ts("wave_fwd", stream);
+  // one wave per 16 sorted queries, when a head's value rows lie within 4 GiB
+  // of its first and a row offset is a 24-bit product (32-bit buffer offsets,
+  // v_mul_u32_u24) and its chunk list fits in LDS
+  const int NC = (Lv.T + 15) / 16;
+  if (DP == 64 && VEC && WHA_SFWD_DMA && (uint64_t)Lv.T * (uint64_t)Lv.st * 4u < (1ull << 32) &&
+      (uint64_t)Lv.st * 4u < (1u << 24) && Lv.T < (1 << 24) && NC <= kSfwdMaxChunks) {
+    const unsigned grid = (unsigned)(NC * Lv.B * Lv.H);
+    const size_t lds = (size_t)NC * sizeof(int);
+    if (Lv.D == 64)
+      hipLaunchKernelGGL(wave_sfwd_reg_kernel<false>, dim3(grid), dim3(64), lds, stream, (const float*)sb.fs,
+                         (const int*)sb.perm, (const int*)sb.bsort, (const int4*)sb.ci, (const int*)sb.bstart, feat,
+                         bucket, v, merged, lse, Lv, cs);
+    else
+      hipLaunchKernelGGL(wave_sfwd_reg_kernel<true>, dim3(grid), dim3(64), lds, stream, (const float*)sb.fs,
+                         (const int*)sb.perm, (const int*)sb.bsort, (const int4*)sb.ci, (const int*)sb.bstart, feat,
+                         bucket, v, merged, lse, Lv, cs);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL((wave_sfwd_kernel<DP, VEC, NW>), dim3((unsigned)(n_qt * Lv.B * Lv.H)), dim3(NW * 64), 0, stream,
                      (const float*)sb.fs, (const int*)sb.perm, (const int*)sb.bsort, (const int4*)sb.ci,
                      (const int*)sb.bstart, feat, bucket, v, merged, lse, Lv, cs);
