@@ -1033,6 +1033,297 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DP == 128 ?
   store_row_frag<DP, VEC>(dV + vbase, out_row, T, Lv.D, Lv.st, g, dvacc, 1.f);
 }
 
+// The same backward with one wave per workgroup (16 sorted keys) and no
+// workgroup barrier: the wave lists the live query chunks of its own key chunk
+// (the bucket window of its own buckets, block_live) in LDS, with bit 31 set on
+// chunks the mask admits whole, and walks them with two private LDS slots:
+// while it computes one chunk, the next chunk's 16 feature rows (contiguous in
+// sorted order; quad c of row r stored at c ^ (r & 7)) and 16 dO rows
+// (gathered through the permutation, swizzled 64-wide rows, LDS row 4u + g
+// holding query 4g + u so that a lane's four positions are one 16-byte load)
+// arrive by global_load_lds, and this lane's LSE, Delta and buckets of queries
+// 4g .. 4g+3 by buffer loads; the positions one step earlier, since they
+// address the rows.  Per chunk as in wave_sdkv_kernel: S and dP with queries
+// on MFMA rows, P = exp2(S - LSE log2 e), dS = P (dP - Delta), the dS block
+// stored for the dF_q kernel, dV^T += dO^T P and dF_k^T += F_q^T dS.  D padded
+// to 64, 16-byte aligned dO rows (vec).
+template <bool PADQ>
+__global__ __launch_bounds__(64) void wave_sdkv_dma_kernel(
+    const float* __restrict__ FS, const float* __restrict__ LS, const float* __restrict__ DLS,
+    const int* __restrict__ PS, const int* __restrict__ BSs, const int4* __restrict__ CI,
+    const int* __restrict__ BST, const float* __restrict__ F, const int* __restrict__ BK,
+    const float* __restrict__ V, const float* __restrict__ dO,
+    const float* __restrict__ LSE, const float* __restrict__ Delta, float* __restrict__ dF, float* __restrict__ dV,
+    float* __restrict__ DS, float* __restrict__ DSP, View Lv, float cs) {
+  constexpr int DP = 64;
+  constexpr int NDT = DP / 16, DG = DP / 4, FG = kFP / 4, NFT = kFP / 16, QPR = DP / 4;
+  constexpr int NFD = 16 * (kFP / 4) / 64;  // feature DMA instructions per chunk
+  constexpr int NOD = 16 * QPR / 64;        // dO DMA instructions per chunk
+  static_assert(NFD == 2 && NOD == 4 && NFT == 2, "16-row chunks of 32 features and 64-wide dO rows");
+  using LT = Lds<DP, true>;
+  __shared__ __align__(16) float Fs0[16 * kFP], Fs1[16 * kFP];
+  __shared__ __align__(16) float Os0[16 * DP], Os1[16 * DP];
+  extern __shared__ int live_list[];  // NC entries
+
+  const int T = Lv.T, BH = Lv.B * Lv.H;
+  const int NC = (T + 15) >> 4, T16 = 16 * NC;
+  const int n_kt_all = (T + 63) >> 6;
+  // workgroup -> (head, key chunk), a head's chunks on one XCD when BH % 8 == 0
+  const int wg = (int)blockIdx.x;
+  int bh, kc;
+  if (BH % 8 == 0) {
+    bh = (wg & 7) + 8 * ((wg >> 3) / NC);
+    kc = (wg >> 3) % NC;
+  } else {
+    bh = wg % BH;
+    kc = wg / BH;
+  }
+  const int b = bh / Lv.H, h = bh % Lv.H;
+  const int64_t vbase = (int64_t)b * Lv.sb + (int64_t)h * Lv.sh;
+  const float* FSh = FS + (int64_t)bh * T16 * kFP;
+  const int* PSh = PS + (int64_t)bh * T16;
+  const int* BSh = BSs + (int64_t)bh * T16;
+  const int4* CIh = CI + (int64_t)bh * NC;
+  const float* Fh = F + (int64_t)bh * T * kFP;
+  const int* Bh = BK + (int64_t)bh * T;
+  const int64_t rbase = (int64_t)bh * T;
+
+  const int lane = (int)threadIdx.x;
+  const int lq = lane & 15, g = lane >> 4;
+  const int krow = 16 * kc + lq;
+  const bool kok = krow < T;
+  const int kpos = kok ? PSh[krow] : -1;
+  const int kb = kok ? BSh[krow] : 0;
+  const int nk = kok ? near_set(1 << kb) : 0;  // buckets of the queries this key meets
+  const int4 ci = CIh[kc];
+
+  float kf[FG];
+  {
+    const float w_cs = cs * kLog2e;
+#pragma unroll
+    for (int e = 0; e < FG; ++e) {
+      const int f = g * FG + e;
+      kf[e] = FSh[(int64_t)(kok ? krow : 0) * kFP + f] * (f < 2 ? kLog2e : w_cs);
+      kf[e] = kok ? kf[e] : 0.f;
+    }
+  }
+  float vf[DG];
+  load_row_frag<DP, true>(V + vbase, kok && kpos >= 0 ? kpos : T, T, Lv.D, Lv.st, g, 1.f, vf);
+  const int qn = kpos + 1;
+  const bool has_qn = kok && kpos >= 0 && qn < T;
+  const int qn_b = has_qn ? Bh[qn] : 0;
+  const float qn_lse = has_qn ? LSE[rbase + qn] : 0.f;
+  const float qn_del = has_qn ? Delta[rbase + qn] : 0.f;
+
+  floatx4 dfacc[NFT], dvacc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NFT; ++dt) dfacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) dvacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  int c0, n_ch;
+  bucket_window(BST + bh * 16, BSh[16 * kc], BSh[min(16 * kc + 15, T - 1)], NC, c0, n_ch);
+
+  // query buckets every key of the chunk admits (the chunk's bucket set ci.x)
+  int nk_all = 0xff;
+#pragma unroll
+  for (int v = 0; v < 8; ++v) nk_all &= ((ci.x >> v) & 1) ? near_set(1 << v) : 0xff;
+  // live query chunks in window order; bit 31: the mask admits every pair
+  // (16 queries before T, every query bucket admitted by every key bucket, no
+  // query before the chunk's last key)
+  int n_live = 0;
+  for (int o0 = 0; o0 < n_ch; o0 += 64) {
+    const int o = o0 + lane;
+    const int c = window_chunk(c0, o < n_ch ? o : 0, NC);
+    const int4 qi = CIh[c];
+    const bool on = o < n_ch && block_live(qi, ci);
+    const bool full = (qi.x & ~nk_all) == 0 && qi.z >= ci.w && 16 * c + 16 <= T;
+    const uint64_t m = __ballot(on);
+    if (on)
+      live_list[n_live + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0))] =
+          c | (full ? (int)0x80000000u : 0);
+    n_live += __builtin_popcountll(m);
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the list is in LDS
+  __builtin_amdgcn_wave_barrier();
+
+  // DMA sources: feature DMA u fills stored quad l & 7 of row 8u + (l >> 3);
+  // dO DMA u stored quad l & 15 of LDS row 4u + g (query 4g + u); a quad past
+  // D reads quad 0 instead (it feeds only dV columns that are never stored)
+  uint32_t foff[NFD];
+#pragma unroll
+  for (int u = 0; u < NFD; ++u) {
+    const int r = 8 * u + (lane >> 3);
+    foff[u] = (uint32_t)(r * kFP + 4 * ((lane & 7) ^ (r & 7))) * 4u;
+  }
+  uint32_t oq[NOD];
+#pragma unroll
+  for (int u = 0; u < NOD; ++u) {
+    const int c = LT::pq_inv(4 * u + g, lane & 15);
+    oq[u] = (PADQ && 4 * c >= Lv.D) ? 0u : 16u * (uint32_t)c;
+  }
+  const char* Oh = reinterpret_cast<const char*>(dO + vbase);
+  const char* Fb = reinterpret_cast<const char*>(FSh);
+  const uint32_t st4 = 4u * (uint32_t)Lv.st;  // < 2^24, and the slice < 4 GiB (checked on the host)
+  const __amdgpu_buffer_rsrc_t rP = buffer_rsrc(PSh, (uint32_t)T16 * 4u);
+  const __amdgpu_buffer_rsrc_t rB = buffer_rsrc(BSh, (uint32_t)T16 * 4u);
+  const __amdgpu_buffer_rsrc_t rL = buffer_rsrc(LS + (int64_t)bh * T16, (uint32_t)T16 * 4u);
+  const __amdgpu_buffer_rsrc_t rD = buffer_rsrc(DLS + (int64_t)bh * T16, (uint32_t)T16 * 4u);
+  const int koff = 16 * g;
+  auto ld_int4 = [&](__amdgpu_buffer_rsrc_t r, int soff) {
+    typedef unsigned uintx4 __attribute__((ext_vector_type(4)));
+    const uintx4 v = __builtin_amdgcn_raw_buffer_load_b128(r, koff, soff, 0);
+    return make_int4((int)v[0], (int)v[1], (int)v[2], (int)v[3]);
+  };
+  auto chunk_at = [&](int k) { return __builtin_amdgcn_readfirstlane(live_list[min(k, n_live - 1)]); };
+  struct Q {
+    int4 p, b;    // positions and buckets of queries 4g .. 4g+3
+    float4 l, d;  // their LSE (log2 units after scaling) and Delta
+    int e;        // list entry
+  };
+  // positions of chunk entry e (they address its dO rows)
+  auto load_pos = [&](int e) { return ld_int4(rP, 64 * (e & 0x7fffffff)); };
+  auto issue = [&](int e, const int4& p, float* Fd, float* Od, Q& q) {
+    const int c = e & 0x7fffffff;
+    const char* fsrc = Fb + (size_t)c * (16 * kFP * 4);
+#pragma unroll
+    for (int u = 0; u < NFD; ++u) dma_quad(reinterpret_cast<const float*>(fsrc + foff[u]), Fd + 256 * u);
+    const int pv[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+    for (int u = 0; u < NOD; ++u)
+      dma_quad(reinterpret_cast<const float*>(Oh + (__umul24((uint32_t)max(pv[u], 0), st4) + oq[u])), Od + 256 * u);
+    // (the positions again for the mask: a copy of p, which the next step
+    // reloads, would tie the two registers and wait for that load)
+    q.p = ld_int4(rP, 64 * c);
+    q.b = ld_int4(rB, 64 * c);
+    q.l = buffer_load_quad(rL, koff, 64 * c);
+    q.d = buffer_load_quad(rD, koff, 64 * c);
+    q.e = e;
+  };
+
+  const int kt = kc >> 2;
+  float* dsk = DS + (int64_t)(bh * n_kt_all + kt) * T16 * 64 + 16 * (kc & 3) + lq;
+  auto compute = [&](const float* Fs, const float* Os, const Q& q) {
+    const int c = q.e & 0x7fffffff;
+    // lane element i: query 4g + i of the chunk, key lq
+    floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f}, dp = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < FG / 4; ++j) {
+      const float4 a = *reinterpret_cast<const float4*>(&Fs[lq * kFP + 4 * ((2 * g + j) ^ (lq & 7))]);
+      s = mfma4(a.x, kf[4 * j + 0], s);
+      s = mfma4(a.y, kf[4 * j + 1], s);
+      s = mfma4(a.z, kf[4 * j + 2], s);
+      s = mfma4(a.w, kf[4 * j + 3], s);
+    }
+#pragma unroll
+    for (int j = 0; j < DG / 4; ++j) {
+      // dO row of query lq (LDS row tr16(lq)), quads 4g .. 4g+3
+      const float4 a = lds_read_quad<DP, true>(Os, tr16(lq), 4 * g + j);
+      dp = mfma4(a.x, vf[4 * j + 0], dp);
+      dp = mfma4(a.y, vf[4 * j + 1], dp);
+      dp = mfma4(a.z, vf[4 * j + 2], dp);
+      dp = mfma4(a.w, vf[4 * j + 3], dp);
+    }
+    const float lv[4] = {q.l.x, q.l.y, q.l.z, q.l.w};
+    const float dv4[4] = {q.d.x, q.d.y, q.d.z, q.d.w};
+    const int pv[4] = {q.p.x, q.p.y, q.p.z, q.p.w};
+    const int bv[4] = {q.b.x, q.b.y, q.b.z, q.b.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float p = fast_exp2(s[i] - lv[i] * kLog2e);
+      if (q.e >= 0) {
+        const bool valid = (pv[i] >= kpos) & (pv[i] >= 0) & (((nk >> bv[i]) & 1) != 0);
+        p = valid ? p : 0.f;
+      }
+      s[i] = p;
+      dp[i] = p * (dp[i] - dv4[i]);
+    }
+    float* dsq = dsk + (int64_t)(16 * c + 4 * g) * 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dsq[i * 64] = dp[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float oa[NDT];
+      lds_read_seg<DP, NDT, true>(Os, 4 * i + g, lq, oa);
+      // features 2lq, 2lq + 1 of query 4g + i
+      const int r = 4 * g + i;
+      const float2 fa = *reinterpret_cast<const float2*>(&Fs[r * kFP + 4 * ((lq >> 1) ^ (r & 7)) + 2 * (lq & 1)]);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) dvacc[dt] = mfma4(oa[dt], s[i], dvacc[dt]);
+      dfacc[0] = mfma4(fa.x, dp[i], dfacc[0]);
+      dfacc[1] = mfma4(fa.y, dp[i], dfacc[1]);
+    }
+  };
+
+  if (n_live > 0) {
+    Q q0, q1;
+    const int e0 = chunk_at(0);
+    const int4 p0 = load_pos(e0);
+    wait_vmem();
+    issue(e0, p0, Fs0, Os0, q0);
+    // entries for slot 1 (eb, positions pb) and slot 0 (ea, pa), each written in
+    // one half of the loop and read in the other (no register copies)
+    int eb = chunk_at(1), ea;
+    int4 pb = load_pos(eb), pa;
+    // step on slot 0 (entry k), then slot 1 (entry k + 1); every step issues the
+    // same loads (past the end, the last entry again, never computed)
+    int k = 0;
+    do {
+      wait_vmem();  // slot 0 holds entry k; entry k + 1's positions are in
+      issue(eb, pb, Fs1, Os1, q1);
+      ea = chunk_at(k + 2);
+      pa = load_pos(ea);
+      compute(Fs0, Os0, q0);
+      if (k + 1 >= n_live) break;
+      wait_vmem();  // slot 1 holds entry k + 1; entry k + 2's positions are in
+      issue(ea, pa, Fs0, Os0, q0);
+      eb = chunk_at(k + 3);
+      pb = load_pos(eb);
+      compute(Fs1, Os1, q1);
+      k += 2;
+    } while (k < n_live);
+    wait_vmem();  // the loads past the end land before the wave ends
+  }
+
+  // the query at position kpos + 1 when its bucket is not near this key's
+  const bool extra = has_qn && !wave_bucket_near(kb, qn_b);
+  float sp = 0.f, dpp = 0.f;
+  float dof[DG];
+  float fq[FG];
+  if (extra) {
+#pragma unroll
+    for (int e = 0; e < FG; ++e) {
+      fq[e] = Fh[(int64_t)qn * kFP + g * FG + e];
+      sp += kf[e] * fq[e];
+    }
+    load_row_frag<DP, true>(dO + vbase, qn, T, Lv.D, Lv.st, g, 1.f, dof);
+#pragma unroll
+    for (int e = 0; e < DG; ++e) dpp += vf[e] * dof[e];
+  }
+  sp = pair_sum32(pair_sum16(sp));
+  dpp = pair_sum32(pair_sum16(dpp));
+  float dsx = 0.f;
+  if (extra) {
+    const float p = fast_exp2(sp - qn_lse * kLog2e);
+    dsx = p * (dpp - qn_del);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dvacc[dt][i] += p * dof[NDT * i + dt];
+    }
+#pragma unroll
+    for (int dt = 0; dt < NFT; ++dt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dfacc[dt][i] += dsx * fq[NFT * i + dt];
+    }
+  }
+  if (has_qn && g == 0) DSP[rbase + qn] = dsx;
+
+  const int out_row = kok && kpos >= 0 ? kpos : T;
+  store_row_frag<kFP, true>(dF + rbase * kFP, out_row, T, kFP, kFP, g, dfacc, 1.f);
+  store_row_frag<DP, true>(dV + vbase, out_row, T, Lv.D, Lv.st, g, dvacc, 1.f);
+}
+
 // dF_q = dS F_k over sorted queries.  Block = 64 sorted queries of one (b,h)
 // (4 waves x 16), keys = the tile's bucket window, 64 key feature rows per LDS
 // stage; a wave reads the dS block of (its chunk, key chunk) exactly when
@@ -1247,6 +1538,24 @@ hipError_t sdkv_t(const SparseBufs& sb, const float* feat, const int* bucket, co
                   const View& Lv, float cs, hipStream_t stream) {
   const int n_kt = (Lv.T + 63) / 64;
   TimingScope ts("wave_bwd_dkv", stream);
+  // one wave per 16 sorted keys, under the same conditions as the forward's
+  const int NC = (Lv.T + 15) / 16;
+  if (DP == 64 && VEC && WHA_SFWD_DMA && (uint64_t)Lv.T * (uint64_t)Lv.st * 4u < (1ull << 32) &&
+      (uint64_t)Lv.st * 4u < (1u << 24) && Lv.T < (1 << 24) && NC <= kSfwdMaxChunks) {
+    const unsigned grid = (unsigned)(NC * Lv.B * Lv.H);
+    const size_t lds = (size_t)NC * sizeof(int);
+    if (Lv.D == 64)
+      hipLaunchKernelGGL(wave_sdkv_dma_kernel<false>, dim3(grid), dim3(64), lds, stream, (const float*)sb.fs,
+                         (const float*)sb.ls, (const float*)sb.dls, (const int*)sb.perm, (const int*)sb.bsort,
+                         (const int4*)sb.ci, (const int*)sb.bstart, feat, bucket, v, d_merged, lse, delta, dfk, dv, ds,
+                         sb.dsp, Lv, cs);
+    else
+      hipLaunchKernelGGL(wave_sdkv_dma_kernel<true>, dim3(grid), dim3(64), lds, stream, (const float*)sb.fs,
+                         (const float*)sb.ls, (const float*)sb.dls, (const int*)sb.perm, (const int*)sb.bsort,
+                         (const int4*)sb.ci, (const int*)sb.bstart, feat, bucket, v, d_merged, lse, delta, dfk, dv, ds,
+                         sb.dsp, Lv, cs);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL((wave_sdkv_kernel<DP, VEC>), dim3((unsigned)(n_kt * Lv.B * Lv.H)), dim3(256), 0, stream,
                      (const float*)sb.fs, (const float*)sb.ls, (const float*)sb.dls, (const int*)sb.perm,
                      (const int*)sb.bsort, (const int4*)sb.ci, (const int*)sb.bstart, feat, bucket, v, d_merged,
