@@ -513,9 +513,10 @@ __global__ __launch_bounds__(NW * 64) void wave_sfwd_kernel(const float* __restr
 // staging and no workgroup barrier.  The wave lists the live key chunks of its
 // own query chunk (the bucket window of its own buckets, block_live per
 // 16-key chunk) in LDS, then walks them with every operand loaded straight
-// into the MFMA operand registers, two chunks ahead of the one it computes
-// (three register sets; the key positions, which address the value rows, one
-// step before the rows).  A wave's time is then the sum of its own live
+// into the MFMA operand registers, NS - 1 chunks ahead of the one it computes
+// (NS register sets; the key positions, which address the value rows, one
+// step before the rows; NS = 2 at four waves per SIMD measured ahead of
+// NS = 3 at three and NS = 4 at two).  A wave's time is then the sum of its own live
 // chunks rather than, per 64-key stage, the most any wave of a block had, and
 // a CU holds as many chunks in flight as its waves have registers.  Lane
 // (lq, g) loads features 8g .. 8g+7 of key row lq (the S = F_k F_q^T A
@@ -530,11 +531,11 @@ __global__ __launch_bounds__(NW * 64) void wave_sfwd_kernel(const float* __restr
 // passes it by more than kSparseLazy.  D padded to 64, 16-byte aligned value
 // rows (vec).
 #ifndef WHA_SFWD_NS
-#define WHA_SFWD_NS 3
+#define WHA_SFWD_NS 2
 #endif
 constexpr float kSparseLazy = 8.f;  // log2 units
 template <bool PADQ, int NS = WHA_SFWD_NS>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NS <= 3 ? 3 : 2))) void wave_sfwd_reg_kernel(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(NS <= 2 ? 4 : NS == 3 ? 3 : 2))) void wave_sfwd_reg_kernel(
     const float* __restrict__ FS, const int* __restrict__ PS, const int* __restrict__ BSs,
     const int4* __restrict__ CI, const int* __restrict__ BST, const float* __restrict__ F,
     const int* __restrict__ BK, const float* __restrict__ V, float* __restrict__ O, float* __restrict__ LSE, View Lv,
