@@ -94,8 +94,8 @@ CASES += [(p, True, (1, 2500, 256, 4, 16)) for p in ("natural", "far", "wrap")]
 CASES += [("natural", False, (1, 2500, 256, 4, 16))]
 # content scores spanning tens of log2 units (the sparse forward's lazy running max)
 CASES += [("loud", s, sh) for sh in ((2, 300, 128, 2, 16), (1, 1024, 256, 4, 16)) for s in (True, False)]
-# 263 chunks of 16 positions: the one-wave kernels build their live-chunk lists
-# over five groups of 64 window offsets (longer windows than at T = 2500)
+# 263 chunks of 16 positions: bucket windows of about 100 chunks, so the one-wave
+# kernels build their live-chunk lists over several groups of 64 window offsets
 CASES += [("natural", True, (1, 4200, 128, 2, 16))]
 
 
