@@ -29,6 +29,7 @@
 //                    (A operand of contractions over rows; the accumulators
 //                    then hold d = NDT*(4g+i)+dt, the layout store_row_frag writes)
 // Head dims pad to DP = 48, 64 or 128 with zeros (32-bit loads: any stride).
+#include <algorithm>
 #include <type_traits>
 
 #include "wha_launch.hpp"
@@ -41,29 +42,53 @@ namespace {
 template <int DP>
 constexpr int kSWof = DP == 128 ? 4 : 8;
 
-// A 16-row chunk of one tensor in a wave's registers: element lane + 64p of the
-// chunk is row (lane + 64p) / DP, head-dim entry (lane + 64p) % DP; zero past
-// T and D.
+// Element lane + 64p of a 16-row chunk, in row-major [16][DP] order, is row
+// (lane + 64p) / DP, head-dim entry (lane + 64p) % DP.  The (row, entry) pair
+// of a lane repeats every PERIOD elements, ROWS rows further on, so a lane
+// needs PERIOD offsets, computed once: its loads add a uniform row step and
+// its LDS stores an immediate.
+template <int DP>
+struct ChunkLanes {
+  static constexpr int PERIOD = DP == 48 ? 3 : DP == 64 ? 1 : 2;
+  static constexpr int ROWS = 64 * PERIOD / DP;
+  int goff[PERIOD];  // bytes from the chunk's first row; past D: kOutside
+  int loff[PERIOD];  // floats into a [16][DP + 4] LDS tile
+  // above every record count (rows of a head span < 2^31 bytes)
+  static constexpr int kOutside = (int)0x80000000u;
+  __device__ __forceinline__ ChunkLanes(int lane, int D, int st) {
+#pragma unroll
+    for (int j = 0; j < PERIOD; ++j) {
+      const int idx = lane + 64 * j, row = idx / DP, d = idx % DP;
+      goff[j] = d < D ? 4 * (row * st + d) : kOutside;
+      loff[j] = row * (DP + 4) + d;
+    }
+  }
+};
+
+// A 16-row chunk of one tensor in a wave's registers (element p as above);
+// zero past T and D.  Loads are raw buffer loads against a record that ends
+// at the last valid entry of row T-1: an offset of a row at or past T is at
+// least (T - row0) * st >= its end (st >= D), and entries past D carry
+// kOutside, so both read as zero.  Requires T * st * 4 < 2^31 (checked by
+// small_problem; also for 16 rows, so that no offset wraps) and row0 < T.
 template <int DP>
 struct ChunkRaw {
   static constexpr int PER = 16 * DP / 64;
+  using Lanes = ChunkLanes<DP>;
   float r[PER];
-  __device__ __forceinline__ void load(const float* __restrict__ base, int row0, int T, int D, int64_t st,
-                                       int lane) {
+  __device__ __forceinline__ void load(const float* __restrict__ head, int row0, int T, int D, int st,
+                                       const Lanes& cl) {
+    const int bytes = 4 * ((T - 1 - row0) * st + D);
+    const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(head + (int64_t)row0 * st, (uint32_t)bytes);
+    const int step = 4 * Lanes::ROWS * st;
 #pragma unroll
-    for (int p = 0; p < PER; ++p) {
-      const int idx = lane + 64 * p;
-      const int row = row0 + idx / DP, d = idx % DP;
-      r[p] = (row < T && d < D) ? base[(int64_t)row * st + d] : 0.f;
-    }
+    for (int p = 0; p < PER; ++p)
+      r[p] = buffer_load_float(rs, cl.goff[p % Lanes::PERIOD] + (p / Lanes::PERIOD) * step, 0);
   }
   // into a [16][DP + 4] LDS tile
-  __device__ __forceinline__ void store(float* tile, int lane) const {
+  __device__ __forceinline__ void store(float* tile, const Lanes& cl) const {
 #pragma unroll
-    for (int p = 0; p < PER; ++p) {
-      const int idx = lane + 64 * p;
-      tile[(idx / DP) * (DP + 4) + idx % DP] = r[p];
-    }
+    for (int p = 0; p < PER; ++p) tile[cl.loff[p % Lanes::PERIOD] + (p / Lanes::PERIOD) * Lanes::ROWS * (DP + 4)] = r[p];
   }
 };
 
@@ -159,6 +184,8 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
   // branches, never to EXEC-masked blocks (which MFMAs would not respect)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lq = lane & 15, g = lane >> 4;
+  const int st = (int)L.st;  // < 2^29 (small_problem)
+  const ChunkLanes<DP> cl(lane, L.D, st);
   const int qrow = 16 * qg + lq;            // this lane's query (MFMA column)
   const int key_last = min(qrow, L.T - 1);  // keys after it are masked
   float* ks = stage[wave][0];
@@ -167,13 +194,13 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
   // the block's 16 queries, staged once by wave 0
   if (wave == 0) {
     ChunkRaw<DP> qr;
-    qr.load(Q + base, 16 * qg, L.T, L.D, L.st, lane);
-    qr.store(qs, lane);
+    qr.load(Q + base, 16 * qg, L.T, L.D, st, cl);
+    qr.store(qs, cl);
   }
   ChunkRaw<DP> kr, vr;
   if (wave <= qg) {
-    kr.load(K + base, 16 * wave, L.T, L.D, L.st, lane);
-    vr.load(V + base, 16 * wave, L.T, L.D, L.st, lane);
+    kr.load(K + base, 16 * wave, L.T, L.D, st, cl);
+    vr.load(V + base, 16 * wave, L.T, L.D, st, cl);
   }
   __syncthreads();
   float qf[DG];
@@ -191,8 +218,8 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
   for (int dt = 0; dt < NDT; ++dt) oacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   for (int c = wave; c <= qg; c += kSW) {
-    kr.store(ks, lane);
-    vr.store(vs, lane);
+    kr.store(ks, cl);
+    vr.store(vs, cl);
     wave_lds_sync();
     if (c == wave) {
       float kfa[DG];
@@ -202,9 +229,13 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
       for (int j = 0; j < DG; ++j) a = fmaf(qf[j], kfa[j], a);
       m = pair_sum32(pair_sum16(a));  // identical in the query's four lane groups
     }
-    if (c + kSW <= qg) {  // the next chunk's loads in flight during this one
-      kr.load(K + base, 16 * (c + kSW), L.T, L.D, L.st, lane);
-      vr.load(V + base, 16 * (c + kSW), L.T, L.D, L.st, lane);
+    {  // the next chunk's loads in flight during this one (clamped: every
+       // trip issues the same loads, so no register copies merge paths)
+      const int cn = min(c + kSW, qg);
+      WHA_FENCE();
+      kr.load(K + base, 16 * cn, L.T, L.D, st, cl);
+      vr.load(V + base, 16 * cn, L.T, L.D, st, cl);
+      WHA_FENCE();
     }
     const int key0 = 16 * c;  // <= 16*qg <= T-1: the chunk's first key is valid for every query here
     // S^T[key][query] - m (log2 units): lane element i = key key0+4g+i, query
@@ -340,14 +371,16 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
   // branches, never to EXEC-masked blocks (which MFMAs would not respect)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lq = lane & 15, g = lane >> 4;
+  const int st = (int)L.st;  // < 2^29 (small_problem)
+  const ChunkLanes<DP> cl(lane, L.D, st);
   const int row = 16 * kg + lq;  // this lane's key (first pass) and query (second pass)
   const int n_kv = n_g - kg;     // key-stationary tasks
 
   for (int t = wave; t < 5; t += kSW) {
     const float* src = t == 0 ? K : t == 1 ? V : t == 2 ? Q : t == 3 ? dO : O;
     ChunkRaw<DP> r;
-    r.load(src + base, 16 * kg, L.T, L.D, L.st, lane);
-    r.store(own[t], lane);
+    r.load(src + base, 16 * kg, L.T, L.D, st, cl);
+    r.store(own[t], cl);
   }
   __syncthreads();
 
@@ -358,7 +391,10 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
     dvacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
     dqacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
-  const float* lse = LSE + (int64_t)bh * L.T;
+  // the head's LSE row as a buffer: rows past T read as zero with no branch
+  // (a branch around a load would make the compiler wait for every load in
+  // flight, the prefetched chunk's included)
+  const __amdgpu_buffer_rsrc_t lse_rs = buffer_rsrc(LSE + (int64_t)bh * L.T, (uint32_t)(4 * L.T));
 
   // ---- key-stationary tasks: query chunks c = kg + wave, kg + wave + kSW, ...
   if (wave < n_kv) {
@@ -377,26 +413,30 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
     ChunkRaw<DP> qr, dr, orr;
     float lsv[4];
     auto load = [&](int c) {
-      qr.load(Q + base, 16 * c, L.T, L.D, L.st, lane);
-      dr.load(dO + base, 16 * c, L.T, L.D, L.st, lane);
-      orr.load(O + base, 16 * c, L.T, L.D, L.st, lane);
+      qr.load(Q + base, 16 * c, L.T, L.D, st, cl);
+      dr.load(dO + base, 16 * c, L.T, L.D, st, cl);
+      orr.load(O + base, 16 * c, L.T, L.D, st, cl);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int q = 16 * c + 4 * g + i;
-        lsv[i] = q < L.T ? -lse[q] * inv_scale : 0.f;
+        lsv[i] = buffer_load_float(lse_rs, 4 * q, 0);  // negated and scaled at use: no wait here
       }
     };
     load(kg + wave);
     for (int c = kg + wave; c < n_g; c += kSW) {
       const int q0 = 16 * c;
-      qr.store(qs, lane);
-      dr.store(os, lane);
-      orr.store(ys, lane);
+      qr.store(qs, cl);
+      dr.store(os, cl);
+      orr.store(ys, cl);
       float lse2[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) lse2[i] = lsv[i];
+      for (int i = 0; i < 4; ++i) lse2[i] = -lsv[i] * inv_scale;
       wave_lds_sync();
-      if (c + kSW < n_g) load(c + kSW);  // the next chunk's loads in flight during this one
+      // the next chunk's loads in flight during this one (clamped: every trip
+      // issues the same loads), kept ahead of the contractions by the fences
+      WHA_FENCE();
+      load(min(c + kSW, n_g - 1));
+      WHA_FENCE();
 
       float qf[DG], df[DG], qc[4][NDT], dc[4][NDT];
       row_frag<DP>(qs, lq, g, 1.f, qf);
@@ -463,18 +503,21 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
       for (int j = 0; j < DG; ++j) dpart += df[j] * of[j];
     }
     const float delta = pair_sum32(pair_sum16(dpart));
-    const float lse2 = row < L.T ? lse[row] * kLog2e : 0.f;
+    const float lse2 = buffer_load_float(lse_rs, 4 * row, 0) * kLog2e;
     ChunkRaw<DP> kr, vr;
-    kr.load(K + base, 16 * j0, L.T, L.D, L.st, lane);
-    vr.load(V + base, 16 * j0, L.T, L.D, L.st, lane);
+    kr.load(K + base, 16 * j0, L.T, L.D, st, cl);
+    vr.load(V + base, 16 * j0, L.T, L.D, st, cl);
     for (int c = j0; c <= kg; c += kSW) {
       const int key0 = 16 * c;
-      kr.store(ks, lane);
-      vr.store(vs, lane);
+      kr.store(ks, cl);
+      vr.store(vs, cl);
       wave_lds_sync();
-      if (c + kSW <= kg) {  // the next chunk's loads in flight during this one
-        kr.load(K + base, 16 * (c + kSW), L.T, L.D, L.st, lane);
-        vr.load(V + base, 16 * (c + kSW), L.T, L.D, L.st, lane);
+      {  // the next chunk's loads in flight during this one (clamped)
+        const int cn = min(c + kSW, kg);
+        WHA_FENCE();
+        kr.load(K + base, 16 * cn, L.T, L.D, st, cl);
+        vr.load(V + base, 16 * cn, L.T, L.D, st, cl);
+        WHA_FENCE();
       }
       float kf[DG], vf[DG], kc[4][NDT];
       row_frag<DP>(ks, lq, g, 1.f, kf);
@@ -516,7 +559,10 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
 }
 
 bool small_problem(const View& L) {
-  return (int64_t)L.B * L.H * ((L.T + 63) / 64) < kSmallBlocks && L.T <= kSmallMaxT && padded_dim(L.D) != 0;
+  // the split-sweep kernels address a head's rows, and a chunk's 16, with
+  // 32-bit byte offsets below 2^31
+  return (int64_t)L.B * L.H * ((L.T + 63) / 64) < kSmallBlocks && L.T <= kSmallMaxT && padded_dim(L.D) != 0 &&
+         (int64_t)std::max(L.T, 16) * L.st * 4 < ((int64_t)1 << 31);
 }
 
 namespace {
