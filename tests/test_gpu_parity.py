@@ -165,6 +165,33 @@ def test_deterministic(pkg, torch_dev, wide):
         np.testing.assert_array_equal(x, y)
 
 
+@pytest.mark.parametrize("offset,D", [(1, 42), (2, 42), (2, 64), (0, 33), (4, 48)])
+def test_small_chunk_unit_widths(pkg, torch_dev, offset, D):
+    """The small-problem kernels read their chunks in units of 4, 2 or 1 floats,
+    the widest that the strides, the head dim and every tensor's alignment allow:
+    views at an odd float offset (1-float units), at an 8-byte offset (2-float
+    units at an even head dim), an odd head dim (1-float units) and 16-byte
+    aligned views (4-float units at head dim 48) all meet the bar."""
+    torch, dev = torch_dev
+    B, H, T = 2, 3, 77
+    print(f"case small chunk units offset={offset} D={D}", flush=True)
+    q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=500 + D + offset)
+    n = B * H * T * D
+
+    def at_offset(a):
+        buf = torch.empty(n + offset, device=dev)
+        buf[offset:].copy_(torch.from_numpy(a).reshape(-1))
+        return buf[offset:].view(B, H, T, D)
+
+    tq, tk, tv, tdo = (at_offset(a) for a in (q, k, v, do))
+    o, lse = pkg.attn_fwd(tq, tk, tv)
+    dq, dk, dv = pkg.attn_bwd(tq, tk, tv, o, tdo, lse)
+    torch.cuda.synchronize()
+    ref = oracle.fwd_bwd_bhtd(q, k, v, do, "f32")
+    for name, got, want in zip(("O", "dQ", "dK", "dV"), (o, dq, dk, dv), ref[:4]):
+        assert_parity(f"units offset={offset} D={D} {name}", got.cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("wide", [False, True])
 def test_causality(pkg, torch_dev, wide):
     """Changing K and V at position j leaves O, LSE and dQ of rows < j unchanged."""

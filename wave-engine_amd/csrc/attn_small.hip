@@ -30,6 +30,8 @@
 //                    then hold d = NDT*(4g+i)+dt, the layout store_row_frag writes)
 // Head dims pad to DP = 48, 64 or 128 with zeros (32-bit loads: any stride).
 #include <algorithm>
+#include <cstdint>
+#include <initializer_list>
 #include <type_traits>
 
 #include "wha_launch.hpp"
@@ -42,15 +44,21 @@ namespace {
 template <int DP>
 constexpr int kSWof = DP == 128 ? 4 : 8;
 
-// Element lane + 64p of a 16-row chunk, in row-major [16][DP] order, is row
-// (lane + 64p) / DP, head-dim entry (lane + 64p) % DP.  The (row, entry) pair
-// of a lane repeats every PERIOD elements, ROWS rows further on, so a lane
+// A 16-row chunk is read as units of VEC consecutive head-dim entries (VEC =
+// 4, 2 or 1, the widest the view's strides and alignment allow): unit
+// lane + 64p, in row-major [16][DP / VEC] order, is row (lane + 64p) / E,
+// entries VEC * ((lane + 64p) % E) .. +VEC-1, E = DP / VEC.  The (row, entry)
+// pair of a lane repeats every PERIOD units, ROWS rows further on, so a lane
 // needs PERIOD offsets, computed once: its loads add a uniform row step and
 // its LDS stores an immediate.
-template <int DP>
+template <int DP, int VEC>
 struct ChunkLanes {
-  static constexpr int PERIOD = DP == 48 ? 3 : DP == 64 ? 1 : 2;
-  static constexpr int ROWS = 64 * PERIOD / DP;
+  static constexpr int E = DP / VEC;
+  static constexpr int G = E % 64 == 0 ? 64 : E % 32 == 0 ? 32 : E % 16 == 0 ? 16 : E % 8 == 0 ? 8 : 4;  // gcd(E, 64)
+  static constexpr int PERIOD = E / G;
+  static constexpr int ROWS = 64 * PERIOD / E;
+  static constexpr int PER = 16 * E / 64;  // units per lane
+  static_assert(DP % VEC == 0 && PER % PERIOD == 0, "chunk unit layout");
   int goff[PERIOD];  // bytes from the chunk's first row; past D: kOutside
   int loff[PERIOD];  // floats into a [16][DP + 4] LDS tile
   // above every record count (rows of a head span < 2^31 bytes)
@@ -58,37 +66,61 @@ struct ChunkLanes {
   __device__ __forceinline__ ChunkLanes(int lane, int D, int st) {
 #pragma unroll
     for (int j = 0; j < PERIOD; ++j) {
-      const int idx = lane + 64 * j, row = idx / DP, d = idx % DP;
+      const int idx = lane + 64 * j, row = idx / E, d = VEC * (idx % E);
       goff[j] = d < D ? 4 * (row * st + d) : kOutside;
       loff[j] = row * (DP + 4) + d;
     }
   }
 };
 
-// A 16-row chunk of one tensor in a wave's registers (element p as above);
-// zero past T and D.  Loads are raw buffer loads against a record that ends
-// at the last valid entry of row T-1: an offset of a row at or past T is at
-// least (T - row0) * st >= its end (st >= D), and entries past D carry
-// kOutside, so both read as zero.  Requires T * st * 4 < 2^31 (checked by
-// small_problem; also for 16 rows, so that no offset wraps) and row0 < T.
-template <int DP>
+// A 16-row chunk of one tensor in a wave's registers (unit p as above); zero
+// past T and D.  Loads are raw buffer loads against a record that ends at
+// the last valid entry of row T-1: an offset of a row at or past T is at least
+// (T - row0) * st >= its end (st >= D), and units past D carry kOutside, so
+// both read as zero (VEC divides D, so no unit straddles the end of a row).
+// Requires T * st * 4 < 2^31 (checked by small_problem; also for 16 rows, so
+// that no offset wraps) and row0 < T.
+template <int DP, int VEC>
 struct ChunkRaw {
-  static constexpr int PER = 16 * DP / 64;
-  using Lanes = ChunkLanes<DP>;
-  float r[PER];
+  using Lanes = ChunkLanes<DP, VEC>;
+  static constexpr int PER = Lanes::PER;
+  float r[PER * VEC];
   __device__ __forceinline__ void load(const float* __restrict__ head, int row0, int T, int D, int st,
                                        const Lanes& cl) {
+    typedef unsigned uintx2 __attribute__((ext_vector_type(2)));
+    typedef unsigned uintx4 __attribute__((ext_vector_type(4)));
     const int bytes = 4 * ((T - 1 - row0) * st + D);
     const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(head + (int64_t)row0 * st, (uint32_t)bytes);
     const int step = 4 * Lanes::ROWS * st;
 #pragma unroll
-    for (int p = 0; p < PER; ++p)
-      r[p] = buffer_load_float(rs, cl.goff[p % Lanes::PERIOD] + (p / Lanes::PERIOD) * step, 0);
+    for (int p = 0; p < PER; ++p) {
+      const int off = cl.goff[p % Lanes::PERIOD] + (p / Lanes::PERIOD) * step;
+      if constexpr (VEC == 4) {
+        const uintx4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[4 * p + e] = __uint_as_float(v[e]);
+      } else if constexpr (VEC == 2) {
+        const uintx2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+        r[2 * p] = __uint_as_float(v[0]);
+        r[2 * p + 1] = __uint_as_float(v[1]);
+      } else {
+        r[p] = buffer_load_float(rs, off, 0);
+      }
+    }
   }
   // into a [16][DP + 4] LDS tile
   __device__ __forceinline__ void store(float* tile, const Lanes& cl) const {
 #pragma unroll
-    for (int p = 0; p < PER; ++p) tile[cl.loff[p % Lanes::PERIOD] + (p / Lanes::PERIOD) * Lanes::ROWS * (DP + 4)] = r[p];
+    for (int p = 0; p < PER; ++p) {
+      float* t = tile + cl.loff[p % Lanes::PERIOD] + (p / Lanes::PERIOD) * Lanes::ROWS * (DP + 4);
+      if constexpr (VEC == 4) {
+        *reinterpret_cast<float4*>(t) = make_float4(r[4 * p], r[4 * p + 1], r[4 * p + 2], r[4 * p + 3]);
+      } else if constexpr (VEC == 2) {
+        *reinterpret_cast<float2*>(t) = make_float2(r[2 * p], r[2 * p + 1]);
+      } else {
+        *t = r[p];
+      }
+    }
   }
 };
 
@@ -159,7 +191,7 @@ __device__ __forceinline__ void write_wave_part(float* tile, const floatx4 (&acc
 
 }  // namespace
 
-template <int DP>
+template <int DP, int VEC>
 __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const float* __restrict__ Q,
                                                                        const float* __restrict__ K,
                                                                        const float* __restrict__ V,
@@ -185,22 +217,23 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lq = lane & 15, g = lane >> 4;
   const int st = (int)L.st;  // < 2^29 (small_problem)
-  const ChunkLanes<DP> cl(lane, L.D, st);
+  const ChunkLanes<DP, VEC> cl(lane, L.D, st);
   const int qrow = 16 * qg + lq;            // this lane's query (MFMA column)
   const int key_last = min(qrow, L.T - 1);  // keys after it are masked
   float* ks = stage[wave][0];
   float* vs = stage[wave][1];
 
-  // the block's 16 queries, staged once by wave 0
-  if (wave == 0) {
-    ChunkRaw<DP> qr;
-    qr.load(Q + base, 16 * qg, L.T, L.D, st, cl);
-    qr.store(qs, cl);
-  }
-  ChunkRaw<DP> kr, vr;
+  // each wave's first K, V chunk, then the block's 16 queries, staged once by
+  // wave 0 (its K and V loads in flight behind them)
+  ChunkRaw<DP, VEC> kr, vr;
   if (wave <= qg) {
     kr.load(K + base, 16 * wave, L.T, L.D, st, cl);
     vr.load(V + base, 16 * wave, L.T, L.D, st, cl);
+  }
+  if (wave == 0) {
+    ChunkRaw<DP, VEC> qr;
+    qr.load(Q + base, 16 * qg, L.T, L.D, st, cl);
+    qr.store(qs, cl);
   }
   __syncthreads();
   float qf[DG];
@@ -348,7 +381,7 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
 // key-stationary ones first; each wave keeps its partial dK, dV and dQ, and
 // the partials merge through LDS in a fixed order (deterministic).  No dS
 // leaves the chip.
-template <int DP>
+template <int DP, int VEC>
 __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ O, const float* __restrict__ dO, const float* __restrict__ LSE, float* __restrict__ dQ,
@@ -372,13 +405,39 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lq = lane & 15, g = lane >> 4;
   const int st = (int)L.st;  // < 2^29 (small_problem)
-  const ChunkLanes<DP> cl(lane, L.D, st);
+  const ChunkLanes<DP, VEC> cl(lane, L.D, st);
   const int row = 16 * kg + lq;  // this lane's key (first pass) and query (second pass)
   const int n_kv = n_g - kg;     // key-stationary tasks
+  // this wave's first query-stationary key chunk (> kg: none)
+  const int j0 = ((wave - n_kv) % kSW + kSW) % kSW;
+
+  // the head's LSE row as a buffer: rows past T read as zero with no branch
+  // (a branch around a load would make the compiler wait for every load in
+  // flight, the prefetched chunk's included)
+  const __amdgpu_buffer_rsrc_t lse_rs = buffer_rsrc(LSE + (int64_t)bh * L.T, (uint32_t)(4 * L.T));
+  // Chunks in flight: Q, dO, O rows and raw LSE of the next key-stationary
+  // task, K and V rows of the next query-stationary one.  The first of each
+  // are requested before the block's own rows, so the three arrive together.
+  ChunkRaw<DP, VEC> qr, dr, orr, kr, vr;
+  float lsv[4];
+  auto load_ks = [&](int c) {
+    qr.load(Q + base, 16 * c, L.T, L.D, st, cl);
+    dr.load(dO + base, 16 * c, L.T, L.D, st, cl);
+    orr.load(O + base, 16 * c, L.T, L.D, st, cl);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lsv[i] = buffer_load_float(lse_rs, 4 * (16 * c + 4 * g + i), 0);
+  };
+  auto load_qs = [&](int c) {
+    kr.load(K + base, 16 * c, L.T, L.D, st, cl);
+    vr.load(V + base, 16 * c, L.T, L.D, st, cl);
+  };
+  if (wave < n_kv) load_ks(kg + wave);
+  if (j0 <= kg) load_qs(j0);
+  const float lse_row = buffer_load_float(lse_rs, 4 * row, 0);  // the second pass's query
 
   for (int t = wave; t < 5; t += kSW) {
     const float* src = t == 0 ? K : t == 1 ? V : t == 2 ? Q : t == 3 ? dO : O;
-    ChunkRaw<DP> r;
+    ChunkRaw<DP, VEC> r;
     r.load(src + base, 16 * kg, L.T, L.D, st, cl);
     r.store(own[t], cl);
   }
@@ -391,11 +450,6 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
     dvacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
     dqacc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
-  // the head's LSE row as a buffer: rows past T read as zero with no branch
-  // (a branch around a load would make the compiler wait for every load in
-  // flight, the prefetched chunk's included)
-  const __amdgpu_buffer_rsrc_t lse_rs = buffer_rsrc(LSE + (int64_t)bh * L.T, (uint32_t)(4 * L.T));
-
   // ---- key-stationary tasks: query chunks c = kg + wave, kg + wave + kSW, ...
   if (wave < n_kv) {
     float* qs = stage[0][wave];
@@ -410,19 +464,6 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
     row_frag<DP>(own[0], lq, g, 1.f, kf);
     row_frag<DP>(own[1], lq, g, 1.f, vf);
     const float inv_scale = 1.f / scale;
-    ChunkRaw<DP> qr, dr, orr;
-    float lsv[4];
-    auto load = [&](int c) {
-      qr.load(Q + base, 16 * c, L.T, L.D, st, cl);
-      dr.load(dO + base, 16 * c, L.T, L.D, st, cl);
-      orr.load(O + base, 16 * c, L.T, L.D, st, cl);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int q = 16 * c + 4 * g + i;
-        lsv[i] = buffer_load_float(lse_rs, 4 * q, 0);  // negated and scaled at use: no wait here
-      }
-    };
-    load(kg + wave);
     for (int c = kg + wave; c < n_g; c += kSW) {
       const int q0 = 16 * c;
       qr.store(qs, cl);
@@ -435,7 +476,7 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
       // the next chunk's loads in flight during this one (clamped: every trip
       // issues the same loads), kept ahead of the contractions by the fences
       WHA_FENCE();
-      load(min(c + kSW, n_g - 1));
+      load_ks(min(c + kSW, n_g - 1));
       WHA_FENCE();
 
       float qf[DG], df[DG], qc[4][NDT], dc[4][NDT];
@@ -488,7 +529,6 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
   }
 
   // ---- query-stationary tasks: key chunk j is task n_kv + j, j = 0 .. kg
-  const int j0 = ((wave - n_kv) % kSW + kSW) % kSW;  // this wave's first
   if (j0 <= kg) {
     float* ks = stage[0][wave];
     float* vs = stage[1][wave];
@@ -503,22 +543,16 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
       for (int j = 0; j < DG; ++j) dpart += df[j] * of[j];
     }
     const float delta = pair_sum32(pair_sum16(dpart));
-    const float lse2 = buffer_load_float(lse_rs, 4 * row, 0) * kLog2e;
-    ChunkRaw<DP> kr, vr;
-    kr.load(K + base, 16 * j0, L.T, L.D, st, cl);
-    vr.load(V + base, 16 * j0, L.T, L.D, st, cl);
+    const float lse2 = lse_row * kLog2e;
     for (int c = j0; c <= kg; c += kSW) {
       const int key0 = 16 * c;
       kr.store(ks, cl);
       vr.store(vs, cl);
       wave_lds_sync();
-      {  // the next chunk's loads in flight during this one (clamped)
-        const int cn = min(c + kSW, kg);
-        WHA_FENCE();
-        kr.load(K + base, 16 * cn, L.T, L.D, st, cl);
-        vr.load(V + base, 16 * cn, L.T, L.D, st, cl);
-        WHA_FENCE();
-      }
+      // the next chunk's loads in flight during this one (clamped)
+      WHA_FENCE();
+      load_qs(min(c + kSW, kg));
+      WHA_FENCE();
       float kf[DG], vf[DG], kc[4][NDT];
       row_frag<DP>(ks, lq, g, 1.f, kf);
       row_frag<DP>(vs, lq, g, 1.f, vf);
@@ -566,35 +600,68 @@ bool small_problem(const View& L) {
 }
 
 namespace {
-template <int DP>
+// The widest chunk unit (4, 2 or 1 floats) that the view's strides, the head
+// dim and every tensor's alignment allow.
+int small_vec(const View& L, std::initializer_list<const float*> ptrs) {
+  for (int vec : {4, 2}) {
+    bool ok = L.D % vec == 0 && L.st % vec == 0 && L.sh % vec == 0 && L.sb % vec == 0;
+    for (const float* p : ptrs) ok = ok && reinterpret_cast<uintptr_t>(p) % (4 * vec) == 0;
+    if (ok) return vec;
+  }
+  return 1;
+}
+
+template <int DP, int VEC>
 hipError_t fwd_small_t(const float* q, const float* k, const float* v, float* o, float* lse, const View& L,
                        float scale, hipStream_t stream) {
   const float sl2 = (float)((double)scale * 1.4426950408889634);
   const dim3 grid((unsigned)((int64_t)L.B * L.H * ((L.T + 15) / 16)));
   TimingScope ts("attn_fwd", stream);
-  hipLaunchKernelGGL(attn_fwd_small_kernel<DP>, grid, dim3(kSWof<DP> * 64), 0, stream, q, k, v, o, lse, L, sl2);
+  hipLaunchKernelGGL((attn_fwd_small_kernel<DP, VEC>), grid, dim3(kSWof<DP> * 64), 0, stream, q, k, v, o, lse, L,
+                     sl2);
   return hipGetLastError();
 }
 
-template <int DP>
+template <int DP, int VEC>
 hipError_t bwd_small_t(const float* q, const float* k, const float* v, const float* o, const float* d_o,
                        const float* lse, float* dq, float* dk, float* dv, const View& L, float scale,
                        hipStream_t stream) {
   const float sl2 = (float)((double)scale * 1.4426950408889634);
   const dim3 grid((unsigned)((int64_t)L.B * L.H * ((L.T + 15) / 16)));
   TimingScope ts("attn_bwd_dkv", stream);  // dK, dV and dQ
-  hipLaunchKernelGGL(attn_bwd_small_kernel<DP>, grid, dim3(kSWof<DP> * 64), 0, stream, q, k, v, o, d_o, lse, dq, dk,
-                     dv, L, scale, sl2);
+  hipLaunchKernelGGL((attn_bwd_small_kernel<DP, VEC>), grid, dim3(kSWof<DP> * 64), 0, stream, q, k, v, o, d_o, lse,
+                     dq, dk, dv, L, scale, sl2);
   return hipGetLastError();
+}
+
+template <int DP>
+hipError_t fwd_small_d(const float* q, const float* k, const float* v, float* o, float* lse, const View& L,
+                       float scale, hipStream_t stream) {
+  switch (small_vec(L, {q, k, v})) {
+    case 4: return fwd_small_t<DP, 4>(q, k, v, o, lse, L, scale, stream);
+    case 2: return fwd_small_t<DP, 2>(q, k, v, o, lse, L, scale, stream);
+    default: return fwd_small_t<DP, 1>(q, k, v, o, lse, L, scale, stream);
+  }
+}
+
+template <int DP>
+hipError_t bwd_small_d(const float* q, const float* k, const float* v, const float* o, const float* d_o,
+                       const float* lse, float* dq, float* dk, float* dv, const View& L, float scale,
+                       hipStream_t stream) {
+  switch (small_vec(L, {q, k, v, o, d_o})) {
+    case 4: return bwd_small_t<DP, 4>(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
+    case 2: return bwd_small_t<DP, 2>(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
+    default: return bwd_small_t<DP, 1>(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
+  }
 }
 }  // namespace
 
 hipError_t launch_attn_fwd_small(const float* q, const float* k, const float* v, float* o, float* lse,
                                  const View& L, float scale, hipStream_t stream) {
   switch (padded_dim(L.D)) {
-    case 48: return fwd_small_t<48>(q, k, v, o, lse, L, scale, stream);
-    case 64: return fwd_small_t<64>(q, k, v, o, lse, L, scale, stream);
-    case 128: return fwd_small_t<128>(q, k, v, o, lse, L, scale, stream);
+    case 48: return fwd_small_d<48>(q, k, v, o, lse, L, scale, stream);
+    case 64: return fwd_small_d<64>(q, k, v, o, lse, L, scale, stream);
+    case 128: return fwd_small_d<128>(q, k, v, o, lse, L, scale, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -603,9 +670,9 @@ hipError_t launch_attn_bwd_small(const float* q, const float* k, const float* v,
                                  const float* lse, float* dq, float* dk, float* dv, const View& L, float scale,
                                  hipStream_t stream) {
   switch (padded_dim(L.D)) {
-    case 48: return bwd_small_t<48>(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
-    case 64: return bwd_small_t<64>(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
-    case 128: return bwd_small_t<128>(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
+    case 48: return bwd_small_d<48>(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
+    case 64: return bwd_small_d<64>(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
+    case 128: return bwd_small_d<128>(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
     default: return hipErrorInvalidValue;
   }
 }
