@@ -373,11 +373,12 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
 //     the accumulators started from -LSE/scale and -Delta), P =
 //     exp2(S scale log2(e)), dS = P dP with Delta = dO.O of the chunk's rows
 //     formed in place, then dV^T += dO^T P and dK^T += Q^T dS
-//     (contractions over the chunk's rows);
-//   - key chunks 0 .. kg of a query-stationary pass (lane column lq = query)
+//     (contractions over the chunk's rows); the diagonal chunk kg also gives
+//     its queries' dQ^T += K^T dS^T from the same dS;
+//   - key chunks 0 .. kg-1 of a query-stationary pass (lane column lq = query)
 //     that forms S^T and dP^T the same way (P from the saved LSE, Delta of the
 //     block's own queries) and dQ^T += K^T dS^T,
-// n_g + 1 tasks for every block.  Task t goes to wave t % kSW, the
+// n_g tasks for every block.  Task t goes to wave t % kSW, the
 // key-stationary ones first; each wave keeps its partial dK, dV and dQ, and
 // the partials merge through LDS in a fixed order (deterministic).  No dS
 // leaves the chip.
@@ -392,6 +393,7 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
   // own: the block's K, V rows (its keys) and Q, dO, O rows (its queries).
   __shared__ __align__(16) float stage[3][kSW][TILE];
   __shared__ __align__(16) float own[5][TILE];
+  __shared__ __align__(16) float ds_t[16 * 20];  // the diagonal chunk's dS, transposed (pitch 20)
 
   const int BH = L.B * L.H;
   const int n_g = (L.T + 15) / 16;
@@ -408,7 +410,7 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
   const ChunkLanes<DP, VEC> cl(lane, L.D, st);
   const int row = 16 * kg + lq;  // this lane's key (first pass) and query (second pass)
   const int n_kv = n_g - kg;     // key-stationary tasks
-  // this wave's first query-stationary key chunk (> kg: none)
+  // this wave's first query-stationary key chunk (>= kg: none)
   const int j0 = ((wave - n_kv) % kSW + kSW) % kSW;
 
   // the head's LSE row as a buffer: rows past T read as zero with no branch
@@ -432,7 +434,7 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
     vr.load(V + base, 16 * c, L.T, L.D, st, cl);
   };
   if (wave < n_kv) load_ks(kg + wave);
-  if (j0 <= kg) load_qs(j0);
+  if (j0 < kg) load_qs(j0);
   const float lse_row = buffer_load_float(lse_rs, 4 * row, 0);  // the second pass's query
 
   for (int t = wave; t < 5; t += kSW) {
@@ -524,12 +526,31 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
           dkacc[dt] = mfma4(qc[i][dt], dp[i], dkacc[dt]);
         }
       }
+      if (c == kg) {
+        // The diagonal chunk (wave 0): its queries are the block's own, so
+        // their dQ^T[d][query] += K^T[d][key] dS^T[key][query] comes from the
+        // same dS, transposed through LDS: lane (lq, g) holds dS[query 4g+i]
+        // [key lq]; the MFMA's k-index g <-> key 4g+i takes dS^T[key 4g+i]
+        // [query lq].  No query-stationary task recomputes this chunk.
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ds_t[(4 * g + i) * 20 + lq] = dp[i];
+        wave_lds_sync();
+        const float4 t4 = *reinterpret_cast<const float4*>(&ds_t[lq * 20 + 4 * g]);
+        const float dst[4] = {t4.x, t4.y, t4.z, t4.w};
+        float kc[4][NDT];
+        col_frag<DP>(own[0], lq, g, kc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) dqacc[dt] = mfma4(kc[i][dt], dst[i], dqacc[dt]);
+        }
+      }
       wave_lds_sync();  // this chunk's tiles are read before the next one overwrites them
     }
   }
 
-  // ---- query-stationary tasks: key chunk j is task n_kv + j, j = 0 .. kg
-  if (j0 <= kg) {
+  // ---- query-stationary tasks: key chunk j is task n_kv + j, j = 0 .. kg-1
+  if (j0 < kg) {
     float* ks = stage[0][wave];
     float* vs = stage[1][wave];
     float qf[DG], df[DG];
@@ -544,14 +565,14 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
     }
     const float delta = pair_sum32(pair_sum16(dpart));
     const float lse2 = lse_row * kLog2e;
-    for (int c = j0; c <= kg; c += kSW) {
+    for (int c = j0; c < kg; c += kSW) {
       const int key0 = 16 * c;
       kr.store(ks, cl);
       vr.store(vs, cl);
       wave_lds_sync();
       // the next chunk's loads in flight during this one (clamped)
       WHA_FENCE();
-      load_qs(min(c + kSW, kg));
+      load_qs(min(c + kSW, kg - 1));
       WHA_FENCE();
       float kf[DG], vf[DG], kc[4][NDT];
       row_frag<DP>(ks, lq, g, 1.f, kf);
