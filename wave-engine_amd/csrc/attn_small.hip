@@ -159,22 +159,48 @@ __device__ __forceinline__ void col_frag(const float* tile, int lq, int g, float
   }
 }
 
+// Four consecutive entries (d .. d+3 of one row, d a multiple of 4) of a
+// 16-row output to global memory: as two 8-byte stores when VEC >= 2 (D and
+// the strides even, the tensor 8-byte aligned; VEC == 2 and D == d + 2 store
+// the first pair only), else entry by entry below D.  No 16-byte store: its
+// data registers need a wait state before they are overwritten, which this
+// compiler does not always leave.
+template <int VEC>
+__device__ __forceinline__ void store_quad(float* __restrict__ p, int d, int D, float x0, float x1, float x2,
+                                           float x3) {
+  if constexpr (VEC >= 2) {
+    if (d < D) *reinterpret_cast<float2*>(p) = make_float2(x0, x1);
+    if (d + 2 < D) *reinterpret_cast<float2*>(p + 2) = make_float2(x2, x3);
+  } else {
+    if (d < D) p[0] = x0;
+    if (d + 1 < D) p[1] = x1;
+    if (d + 2 < D) p[2] = x2;
+    if (d + 3 < D) p[3] = x3;
+  }
+}
+
 // The waves' partial accumulators written to LDS by write_wave_part (wave w's
-// tile at sm + w*TILE) are summed by the whole block, one output element per
-// thread in turn, adding the waves in order (deterministic), and row r of the
-// 16 goes to row row0 + r of dst, times mul.  Requires a __syncthreads()
+// tile at sm + w*TILE) are summed by the whole block, four consecutive output
+// entries per thread, adding the waves in order (deterministic), and row r of
+// the 16 goes to row row0 + r of dst, times mul.  Requires a __syncthreads()
 // between the writes and this call.
-template <int DP>
+template <int DP, int VEC>
 __device__ __forceinline__ void store_wave_sums(const float* sm, float* __restrict__ dst, int row0, int T, int D,
                                                 int64_t st, float mul) {
   constexpr int kSW = kSWof<DP>, TILE = 16 * (DP + 4);
-  for (int e = threadIdx.x; e < 16 * DP; e += kSW * 64) {
-    const int r = e / DP, d = e % DP;
+  for (int e4 = threadIdx.x; e4 < 4 * DP; e4 += kSW * 64) {
+    const int r = (4 * e4) / DP, d = (4 * e4) % DP;
     const int off = r * (DP + 4) + d;
-    float x = sm[off];
+    float4 x = *reinterpret_cast<const float4*>(sm + off);
 #pragma unroll
-    for (int w = 1; w < kSW; ++w) x += sm[w * TILE + off];
-    if (row0 + r < T && d < D) dst[(int64_t)(row0 + r) * st + d] = x * mul;
+    for (int w = 1; w < kSW; ++w) {
+      const float4 y = *reinterpret_cast<const float4*>(sm + w * TILE + off);
+      x.x += y.x;
+      x.y += y.y;
+      x.z += y.z;
+      x.w += y.w;
+    }
+    if (row0 + r < T) store_quad<VEC>(dst + (int64_t)(row0 + r) * st + d, d, D, x.x * mul, x.y * mul, x.z * mul, x.w * mul);
   }
 }
 
@@ -203,7 +229,7 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
   // the wave's partial output for the merge
   __shared__ __align__(16) float stage[kSW][2][TILE];
   __shared__ __align__(16) float qs[TILE];
-  __shared__ float sm_m[kSW][16], sm_l[kSW][16], sm_wt[kSW][16], sm_inv[16];
+  __shared__ float sm_m[kSW][16], sm_l[kSW][16];
 
   const int BH = L.B * L.H;
   const int n_g = (L.T + 15) / 16;
@@ -338,31 +364,37 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
     for (int i = 0; i < 4; ++i) ks[lq * (DP + 4) + NDT * (4 * g + i) + dt] = oacc[dt][i];
   }
   __syncthreads();
-  // per query row: the waves' weights 2^(m_w - M) and 1 / sum, then the whole
-  // block forms the weighted sums, one output element per thread in turn
-  if (tid < 16) {
+  // Four consecutive entries of one query row per thread: the row's wave
+  // weights 2^(m_w - M) and 1 / sum (formed by every thread of the row, no
+  // second barrier), then the weighted sum of the waves' partials in wave
+  // order; the thread with the row's first entries writes its LSE.
+  for (int e4 = tid; e4 < 4 * DP; e4 += kSW * 64) {
+    const int r = (4 * e4) / DP, d = (4 * e4) % DP;
+    const int off = r * (DP + 4) + d;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kSW; ++w) M = fmaxf(M, sm_m[w][tid]);
-    float Ls = 0.f;
+    for (int w = 0; w < kSW; ++w) M = fmaxf(M, sm_m[w][r]);
+    float wt[kSW], Ls = 0.f;
 #pragma unroll
     for (int w = 0; w < kSW; ++w) {
-      const float wt = fast_exp2(sm_m[w][tid] - M);
-      sm_wt[w][tid] = wt;
-      Ls += wt * sm_l[w][tid];
+      wt[w] = fast_exp2(sm_m[w][r] - M);
+      Ls += wt[w] * sm_l[w][r];
     }
-    sm_inv[tid] = 1.f / Ls;
-    const int q = 16 * qg + tid;
-    if (LSE != nullptr && q < L.T) LSE[(int64_t)bh * L.T + q] = (M + log2f(Ls)) * kLn2;
-  }
-  __syncthreads();
-  for (int e = tid; e < 16 * DP; e += kSW * 64) {
-    const int r = e / DP, d = e % DP;
-    const int off = r * (DP + 4) + d;
-    float acc = 0.f;
+    const float inv = 1.f / Ls;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int w = 0; w < kSW; ++w) acc += sm_wt[w][r] * stage[w][0][off];
-    if (16 * qg + r < L.T && d < L.D) O[base + (int64_t)(16 * qg + r) * L.st + d] = acc * sm_inv[r];
+    for (int w = 0; w < kSW; ++w) {
+      const float4 y = *reinterpret_cast<const float4*>(&stage[w][0][off]);
+      acc.x += wt[w] * y.x;
+      acc.y += wt[w] * y.y;
+      acc.z += wt[w] * y.z;
+      acc.w += wt[w] * y.w;
+    }
+    const int q = 16 * qg + r;
+    if (q < L.T) {
+      if (d == 0 && LSE != nullptr) LSE[(int64_t)bh * L.T + q] = (M + log2f(Ls)) * kLn2;
+      store_quad<VEC>(O + base + (int64_t)q * L.st + d, d, L.D, acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    }
   }
 }
 
@@ -608,9 +640,9 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
   write_wave_part<DP>(stage[1][wave], dkacc, lq, g);
   write_wave_part<DP>(stage[2][wave], dqacc, lq, g);
   __syncthreads();
-  store_wave_sums<DP>(&stage[0][0][0], dV + base, 16 * kg, L.T, L.D, L.st, 1.f);
-  store_wave_sums<DP>(&stage[1][0][0], dK + base, 16 * kg, L.T, L.D, L.st, scale);
-  store_wave_sums<DP>(&stage[2][0][0], dQ + base, 16 * kg, L.T, L.D, L.st, scale);
+  store_wave_sums<DP, VEC>(&stage[0][0][0], dV + base, 16 * kg, L.T, L.D, L.st, 1.f);
+  store_wave_sums<DP, VEC>(&stage[1][0][0], dK + base, 16 * kg, L.T, L.D, L.st, scale);
+  store_wave_sums<DP, VEC>(&stage[2][0][0], dQ + base, 16 * kg, L.T, L.D, L.st, scale);
 }
 
 bool small_problem(const View& L) {
@@ -623,10 +655,10 @@ bool small_problem(const View& L) {
 namespace {
 // The widest chunk unit (4, 2 or 1 floats) that the view's strides, the head
 // dim and every tensor's alignment allow.
-int small_vec(const View& L, std::initializer_list<const float*> ptrs) {
+int small_vec(const View& L, std::initializer_list<const void*> ptrs) {
   for (int vec : {4, 2}) {
     bool ok = L.D % vec == 0 && L.st % vec == 0 && L.sh % vec == 0 && L.sb % vec == 0;
-    for (const float* p : ptrs) ok = ok && reinterpret_cast<uintptr_t>(p) % (4 * vec) == 0;
+    for (const void* p : ptrs) ok = ok && reinterpret_cast<uintptr_t>(p) % (4 * vec) == 0;
     if (ok) return vec;
   }
   return 1;
@@ -658,7 +690,7 @@ hipError_t bwd_small_t(const float* q, const float* k, const float* v, const flo
 template <int DP>
 hipError_t fwd_small_d(const float* q, const float* k, const float* v, float* o, float* lse, const View& L,
                        float scale, hipStream_t stream) {
-  switch (small_vec(L, {q, k, v})) {
+  switch (small_vec(L, {q, k, v, o})) {
     case 4: return fwd_small_t<DP, 4>(q, k, v, o, lse, L, scale, stream);
     case 2: return fwd_small_t<DP, 2>(q, k, v, o, lse, L, scale, stream);
     default: return fwd_small_t<DP, 1>(q, k, v, o, lse, L, scale, stream);
@@ -669,7 +701,7 @@ template <int DP>
 hipError_t bwd_small_d(const float* q, const float* k, const float* v, const float* o, const float* d_o,
                        const float* lse, float* dq, float* dk, float* dv, const View& L, float scale,
                        hipStream_t stream) {
-  switch (small_vec(L, {q, k, v, o, d_o})) {
+  switch (small_vec(L, {q, k, v, o, d_o, dq, dk, dv})) {
     case 4: return bwd_small_t<DP, 4>(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
     case 2: return bwd_small_t<DP, 2>(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
     default: return bwd_small_t<DP, 1>(q, k, v, o, d_o, lse, dq, dk, dv, L, scale, stream);
