@@ -351,6 +351,7 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_fwd_small_kernel(const fl
     wave_lds_sync();  // this chunk's tiles are read before the next one overwrites them
   }
 
+  wait_vmem();  // the last trip's clamped prefetch lands before the wave can end
   // merge the waves' (max, sum, O) of each query: weights 2^(m_w - M);
   // a wave with no chunk keeps m = -inf and weighs zero
   const float lt = pair_sum32(pair_sum16(l));
@@ -635,6 +636,7 @@ __global__ __launch_bounds__(kSWof<DP> * 64) void attn_bwd_small_kernel(
     }
   }
 
+  wait_vmem();      // the last trips' clamped prefetches land before the wave can end
   __syncthreads();  // every wave is done with its staged chunks
   write_wave_part<DP>(stage[0][wave], dvacc, lq, g);
   write_wave_part<DP>(stage[1][wave], dkacc, lq, g);
