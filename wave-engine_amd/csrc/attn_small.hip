@@ -20,15 +20,17 @@
 //                          statistics pass, no dS workspace)
 // Each wave stages its chunk's operands in its own LDS region: a 16-row chunk
 // is read from global memory row by row (consecutive lanes on consecutive
-// head-dim entries, so every load instruction touches one or two rows), and
-// the next chunk's loads are in flight while the current chunk is consumed.
+// units of 4, 2 or 1 head-dim entries, so every load instruction touches a
+// few rows), and the next chunk's loads are in flight while the current chunk
+// is consumed.
 // From LDS each lane takes the two MFMA layouts the contractions need:
 //   row fragment     lane (lq, g) holds row lq, d = g*DG .. g*DG+DG-1
 //                    (A/B operands of contractions over the head dimension)
 //   column fragment  lane (lq, g) holds rows 4g+i (i < 4), d = NDT*lq+dt
 //                    (A operand of contractions over rows; the accumulators
 //                    then hold d = NDT*(4g+i)+dt, the layout store_row_frag writes)
-// Head dims pad to DP = 48, 64 or 128 with zeros (32-bit loads: any stride).
+// Head dims pad to DP = 48, 64 or 128 with zeros; any stride (the unit width
+// follows the strides and the tensors' alignment).
 #include <algorithm>
 #include <cstdint>
 #include <initializer_list>
