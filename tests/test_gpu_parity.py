@@ -192,6 +192,33 @@ def test_small_chunk_unit_widths(pkg, torch_dev, offset, D):
         assert_parity(f"units offset={offset} D={D} {name}", got.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("stride_t", [64, 1 << 25])
+def test_small_problem_row_stride_limit(pkg, torch_dev, stride_t):
+    """The small-problem kernels address a chunk's 16 rows with 32-bit byte
+    offsets, so a row stride whose 16 rows span 2 GiB (2^25 floats) sends even a
+    tiny problem to the 64-row tile kernels; with T = 1 the views stay a few
+    floats long.  Both routes meet the bar."""
+    torch, dev = torch_dev
+    B, H, T, D = 2, 3, 1, 64
+    print(f"case small row stride {stride_t}", flush=True)
+    q, k, v, do = pkg.synth_inputs(B, H, T, D, seed=77)
+    strides = (H * D, D, stride_t, 1)
+
+    def view(a=None):
+        t = torch.empty_strided((B, H, T, D), strides, dtype=torch.float32, device=dev)
+        if a is not None:
+            t.copy_(torch.from_numpy(a))
+        return t
+
+    tq, tk, tv, tdo = (view(a) for a in (q, k, v, do))
+    o, lse = pkg.attn_fwd(tq, tk, tv, out=view())
+    dq, dk, dv = pkg.attn_bwd(tq, tk, tv, o, tdo, lse, dq=view(), dk=view(), dv=view())
+    torch.cuda.synchronize()
+    ref = oracle.fwd_bwd_bhtd(q, k, v, do, "f32")
+    for name, got, want in zip(("O", "dQ", "dK", "dV"), (o, dq, dk, dv), ref[:4]):
+        assert_parity(f"row stride {stride_t} {name}", got.cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("wide", [False, True])
 def test_causality(pkg, torch_dev, wide):
     """Changing K and V at position j leaves O, LSE and dQ of rows < j unchanged."""
